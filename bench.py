@@ -1,0 +1,351 @@
+"""Benchmark of the MI355X decode-GEMM hot path (BASELINE.json metric).
+
+Workload (the configuration the metric is quoted on):
+one Qwen3-4B decoder layer's four decode GEMMs at M = 8 rows, bf16 —
+QKV [6144, 2560], o_proj [2560, 4096], gate_up [19456, 2560] with the fused
+SwiGLU epilogue, down [2560, 9728].  Weights ~N(0, 0.02) and activations
+~N(0, 1), seeded, synthetic.  A *step* is those four GEMMs for one layer;
+consecutive steps walk 36 distinct layers' weights (7.27 GB), so every step
+streams its 201.85 MB from HBM and the 256 MB MALL cannot serve it.
+
+``value`` = algorithmic bytes per step / device time per step (GB/s), with
+inputs resident in HBM.  Algorithmic bytes per GEMM = 2NK + 2MK + out
+(out = 2MN, 2*M*9728 for gate_up, 12M for lm_head+argmax); split-K
+workspace traffic is not counted.
+
+Timing: the K timed steps are captured into one HIP graph (the way the
+decode step runs) and replayed once between two synchronisations; HIP
+events on the launch stream give the time.  Per-kernel durations (roofline,
+per-GEMM table) come from graphs of back-to-back launches of one kernel over
+rotating weights, also timed with events on the launch stream; they include
+the inter-kernel gap, so they slightly understate kernel-only bandwidth
+(rocprofv3 --kernel-trace --stats gives kernel-only durations; see profiles/).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E, vendor figure
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
+METRIC = "achieved HBM GB/s (% of peak) per decode GEMM at M=1/8; decode tok/s at bs=16"
+
+SHAPES = {   # name: (N, K, kind)
+    "qkv": (6144, 2560, "gemm"),
+    "o_proj": (2560, 4096, "gemm"),
+    "gate_up": (9728, 2560, "gateup"),     # N = I, weight [2I, K]
+    "down": (2560, 9728, "gemm"),
+    "lm_head": (151936, 2560, "lm_argmax"),
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def alg_bytes(name: str, M: int) -> int:
+    N, K, kind = SHAPES[name]
+    if kind == "gateup":
+        return 2 * (2 * N) * K + 2 * M * K + 2 * M * N
+    if kind == "lm_argmax":
+        return 2 * N * K + 2 * M * K + 12 * M
+    return 2 * N * K + 2 * M * K + 2 * M * N
+
+
+def alg_flops(name: str, M: int) -> int:
+    N, K, kind = SHAPES[name]
+    return 2 * M * (2 * N if kind == "gateup" else N) * K
+
+
+class Workload:
+    """36 layers of synthetic Qwen3-4B decode weights plus fixed activations."""
+
+    def __init__(self, layers: int, M: int, device: str = "cuda:0", seed: int = 0):
+        import torch
+
+        from starter_amd import kernels as Kn
+
+        self.torch, self.Kn = torch, Kn
+        self.M, self.dev, self.L = M, device, layers
+        gen = torch.Generator(device=device).manual_seed(seed)
+        bf16 = torch.bfloat16
+
+        def w(n, k):
+            return (torch.randn(n, k, generator=gen, device=device) * 0.02).to(bf16)
+
+        self.wqkv = [w(6144, 2560) for _ in range(layers)]
+        self.wo = [w(2560, 4096) for _ in range(layers)]
+        self.wgu = [w(19456, 2560) for _ in range(layers)]
+        self.wd = [w(2560, 9728) for _ in range(layers)]
+        self.wlm = [w(151936, 2560) for _ in range(2)]
+        torch.cuda.synchronize()
+        self.x = torch.randn(M, 2560, generator=gen, device=device).to(bf16)
+        self.attn = torch.randn(M, 4096, generator=gen, device=device).to(bf16)
+        self.act = torch.randn(M, 9728, generator=gen, device=device).to(bf16)
+        self.mm = {
+            "qkv": Kn.SkinnyMatmul(M, 6144, 2560, device),
+            "o_proj": Kn.SkinnyMatmul(M, 2560, 4096, device),
+            "gate_up": Kn.SkinnyGateUp(M, 9728, 2560, device),
+            "down": Kn.SkinnyMatmul(M, 2560, 9728, device),
+            "lm_head": Kn.LmArgmax(M, 151936, 2560, device),
+        }
+        self.out = {
+            "qkv": torch.empty(M, 6144, dtype=bf16, device=device),
+            "o_proj": torch.empty(M, 2560, dtype=bf16, device=device),
+            "gate_up": torch.empty(M, 9728, dtype=bf16, device=device),
+            "down": torch.empty(M, 2560, dtype=bf16, device=device),
+        }
+        self.ids = torch.empty(M, dtype=torch.int64, device=device)
+        self.maxv = torch.empty(M, dtype=torch.float32, device=device)
+
+    def launch(self, name: str, layer: int) -> None:
+        Kn, mm = self.Kn, self.mm[name]
+        if name == "qkv":
+            Kn.gemm(self.x, self.wqkv[layer], out=self.out["qkv"], config=mm.config, ws=mm.ws)
+        elif name == "o_proj":
+            Kn.gemm(self.attn, self.wo[layer], out=self.out["o_proj"], config=mm.config, ws=mm.ws)
+        elif name == "gate_up":
+            w = self.wgu[layer]
+            Kn.gateup_swiglu(self.x, w[:9728], w[9728:], out=self.out["gate_up"], config=mm.config, ws=mm.ws)
+        elif name == "down":
+            Kn.gemm(self.act, self.wd[layer], out=self.out["down"], config=mm.config, ws=mm.ws)
+        elif name == "lm_head":
+            Kn.lm_argmax(self.x, self.wlm[layer % 2], config=mm.config, ws=mm.ws, ids=self.ids, maxv=self.maxv)
+
+    def step(self, i: int) -> None:
+        layer = i % self.L
+        for name in ("qkv", "o_proj", "gate_up", "down"):
+            self.launch(name, layer)
+
+    def capture(self, fn, n: int):
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for i in range(min(n, 3)):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(self, g, reps: int = 1) -> list[float]:
+        """Milliseconds per replay, HIP events on the current (launch) stream."""
+        torch = self.torch
+        out = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            b.synchronize()
+            out.append(a.elapsed_time(b))
+        return out
+
+    def kernel_us(self, name: str, launches: int, reps: int = 5) -> float:
+        """Median per-launch time of back-to-back launches over rotating weights."""
+        nl = 2 if name == "lm_head" else self.L
+        g = self.capture(lambda i: self.launch(name, i % nl), launches)
+        g.replay()
+        t = self.time_graph(g, reps)
+        del g
+        return statistics.median(t) * 1000.0 / launches
+
+
+def cpu_baseline(M: int, samples: int) -> dict:
+    """The reference's own CPU path for one step: torch F.linear (bf16 in,
+    fp32 accumulate, bf16 out; engine/kernels/gemm.py:527 `a @ w.t()`) for QKV,
+    o_proj and down, F.silu(g) * u over the gate/up projection (gemm.py:569),
+    on the host cores of this box.  Median of `samples` steps after 3 warmups."""
+    import torch
+    import torch.nn.functional as F
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    bf = torch.bfloat16
+    w = {n: (torch.randn(2 * N if k == "gateup" else N, K, generator=g) * 0.02).to(bf)
+         for n, (N, K, k) in SHAPES.items() if n != "lm_head"}
+    x = torch.randn(M, 2560, generator=g).to(bf)
+    attn = torch.randn(M, 4096, generator=g).to(bf)
+    act = torch.randn(M, 9728, generator=g).to(bf)
+
+    def step():
+        F.linear(x, w["qkv"])
+        F.linear(attn, w["o_proj"])
+        gu = F.linear(x, w["gate_up"])
+        F.silu(gu[:, :9728]) * gu[:, 9728:]
+        F.linear(act, w["down"])
+
+    for _ in range(3):
+        step()
+    ts = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    step_bytes = sum(alg_bytes(n, M) for n in ("qkv", "o_proj", "gate_up", "down"))
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(step_bytes / t / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "reference",
+            "sample": f"{samples} steps (median) of the M={M} layer workload via torch F.linear/F.silu on CPU "
+                      f"(the reference's a @ w.t() baseline path), {t * 1e3:.2f} ms/step, {cpu}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=72)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--M", type=int, default=8)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--sweep", action="store_true", help="also time all five shapes at M in 1..64 (BASELINE config 4)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-samples", type=int, default=20)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build measures the single-GPU hot path "
+              f"(--gpus {args.gpus} requested; multi-GPU sharding is a design note, not a measured path)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from starter_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from starter_amd.build import build
+
+        log("library missing; building")
+        build()
+    if not torch.cuda.is_available():
+        log("no ROCm GPU visible")
+        return 1
+    torch.cuda.set_device(0)
+    log(f"device {torch.cuda.get_device_name(0)}; building workload (36 layers of weights)")
+    wl = Workload(args.layers, args.M)
+
+    layer_names = ("qkv", "o_proj", "gate_up", "down")
+    step_bytes = sum(alg_bytes(n, args.M) for n in layer_names)
+    step_flops = sum(alg_flops(n, args.M) for n in layer_names)
+
+    if args.warmup > 0:
+        gw = wl.capture(wl.step, args.warmup)
+        gw.replay()
+        torch.cuda.synchronize()
+        del gw
+    g = wl.capture(wl.step, args.steps)
+    g.replay()   # untimed replay of the captured graph (first-touch of its pool)
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    ms = min(wl.time_graph(g, 3))   # best of three replays of the K-step graph
+    ms_per_step = ms / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del g
+
+    # Per-kernel timing: the dominant kernel of the step (gate_up) and the
+    # per-GEMM table at M = 1 and M = 8.
+    per_gemm = {}
+    for M in sorted({1, args.M}):
+        wlM = wl if M == args.M else Workload(args.layers, M, seed=1)
+        for name in SHAPES:
+            n = 8 if name == "lm_head" else 72
+            us = wlM.kernel_us(name, n)
+            gbs = alg_bytes(name, M) / (us * 1e-6) / 1e9
+            per_gemm.setdefault(name, {})[f"M{M}"] = {
+                "us": round(us, 3), "GB/s": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
+                "TFLOP/s": round(alg_flops(name, M) / (us * 1e-6) / 1e12, 3)}
+            log(f"{name:8s} M={M:2d}: {us:8.2f} us  {gbs:7.1f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
+        if wlM is not wl:
+            del wlM
+            torch.cuda.empty_cache()
+
+    sweep = None
+    if args.sweep:
+        sweep = {}
+        for M in (1, 2, 4, 8, 16, 32, 40, 64):
+            wlM = Workload(min(args.layers, 12), M, seed=2)
+            for name in SHAPES:
+                us = wlM.kernel_us(name, 8 if name == "lm_head" else 36)
+                gbs = alg_bytes(name, M) / (us * 1e-6) / 1e9
+                sweep.setdefault(name, {})[f"M{M}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
+                                                       "TFLOP/s": round(alg_flops(name, M) / (us * 1e-6) / 1e12, 3)}
+                log(f"sweep {name:8s} M={M:2d}: {us:8.2f} us {gbs:7.1f} GB/s")
+            del wlM
+            torch.cuda.empty_cache()
+
+    dom = per_gemm["gate_up"][f"M{args.M}"]
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_gate_up_m8.json"
+    if tfile.exists() and args.M == 8:
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(dom["GB/s"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "kernel": f"gate_up+swiglu M={args.M} ({alg_bytes('gate_up', args.M)} algorithmic bytes/launch, "
+                          f"{dom['us']} us/launch)"}
+
+    cpu = None
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(args.M, args.cpu_samples)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
+        "config": {"workload": "qwen3-4b decoder-layer decode GEMMs: qkv 6144x2560, o_proj 2560x4096, "
+                               "gate_up 19456x2560+swiglu, down 2560x9728",
+                   "M": args.M, "layers_rotated": args.layers, "step_bytes": step_bytes,
+                   "step_tflops": round(step_flops / (ms_per_step * 1e-3) / 1e12, 3),
+                   "frac_peak_hbm": round(value / PEAK_HBM_GBS, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "per_gemm": per_gemm,
+    }
+    if sweep is not None:
+        line["sweep"] = sweep
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,163 @@
+/*
+ * starter_amd.h - C ABI of the MI355X (gfx950) decode-GEMM hot path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * enqueues its kernels on the given HIP stream and returns an sk_status code.
+ * Nothing here allocates device memory, synchronises the host or depends on
+ * host-side pointer values of the data, so every call can be captured into a
+ * HIP graph and replayed.  Kernels never abort: a bad argument is reported as a
+ * status code before anything is enqueued.
+ *
+ * Data layout (the reference's tensor layouts, engine/model.py:112-116 and
+ * engine/kernels/gemm.py:365-369):
+ *   A  [M, K]  bf16 row-major, row stride lda (elements)   - activations
+ *   W  [N, K]  bf16 row-major, row stride ldw (elements)   - torch Linear weight
+ *   C  [M, N]  bf16 row-major, row stride ldc (elements)   - C = A @ W^T
+ * Arithmetic: bf16 inputs, fp32 accumulation, one rounding to bf16 (RNE) at
+ * the end, as torch F.linear / the reference's tl.dot + `.to(bf16)` path.
+ *
+ * Alignment: A, W (and Wg/Wu) must be 16-byte aligned and lda/ldw multiples
+ * of 8 elements; K must be a multiple of 32.  M may be 0 (nothing is enqueued).
+ *
+ * Workspace: ops that need device scratch take (ws, ws_bytes); query the size
+ * with sk_workspace_bytes() for the same op/shape/config and allocate it once
+ * (outside graph capture).  Calls that share one workspace must not overlap.
+ */
+#ifndef STARTER_AMD_H
+#define STARTER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t sk_bf16; /* raw bfloat16 bits */
+
+typedef enum sk_status {
+  SK_OK = 0,
+  SK_ERR_NULL = 1,        /* a required pointer is NULL */
+  SK_ERR_SHAPE = 2,       /* M/N/K/stride out of the supported range */
+  SK_ERR_ALIGN = 3,       /* pointer or stride misaligned for 16-byte loads */
+  SK_ERR_WORKSPACE = 4,   /* workspace missing or smaller than required */
+  SK_ERR_CONFIG = 5,      /* explicit config invalid for this shape */
+  SK_ERR_LAUNCH = 6,      /* the HIP runtime rejected a launch */
+  SK_ERR_DEVICE = 7,      /* no usable gfx950 device / runtime query failed */
+  SK_ERR_ALIAS = 8        /* an output overlaps an input it must not alias */
+} sk_status;
+
+typedef enum sk_op {
+  SK_OP_GEMM = 0,         /* C = A @ W^T                                  */
+  SK_OP_GATEUP = 1,       /* Out = swiglu(A @ Wg^T, A @ Wu^T)             */
+  SK_OP_LM_ARGMAX = 2,    /* ids/maxv = argmax_n bf16(A @ W^T)[m, n]      */
+  SK_OP_ARGMAX = 3        /* ids/maxv = argmax over given bf16 logits     */
+} sk_op;
+
+typedef enum sk_path {
+  SK_PATH_AUTO = 0,
+  SK_PATH_MFMA = 1,       /* v_mfma_f32_16x16x32_bf16 tiles, 16 weight rows per wave tile */
+  SK_PATH_GEMV = 2        /* VALU v_dot2_f32_bf16, lanes span K, DPP/shuffle lane reduction */
+} sk_path;
+
+/*
+ * Launch configuration.  The reference picks a Triton config per shape at
+ * warmup (engine/kernels/gemm.py:381-401, 516-558); here the defaults come
+ * from an offline-tuned table (sk_default_config) and an explicit config can
+ * be passed to any op (NULL = default) to test or time one candidate.
+ *
+ *   path   : SK_PATH_MFMA or SK_PATH_GEMV
+ *   waves  : wavefronts per workgroup; they split the workgroup's K slice and
+ *            their fp32 partials are summed in LDS in fixed wave order
+ *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns)
+ *   rows   : weight rows per workgroup tile (MFMA: 16 or 32; GEMV: 1..8)
+ *   split  : global K splits; >1 writes fp32 partials to the workspace that a
+ *            second kernel sums in fixed split order (no atomics)
+ *   grid   : workgroups to launch (0 = derive from the device's CU count)
+ */
+typedef struct sk_config {
+  int32_t path;
+  int32_t waves;
+  int32_t ku;
+  int32_t rows;
+  int32_t split;
+  int32_t grid;
+} sk_config;
+
+/* Library version, (major << 16) | minor. */
+int sk_version(void);
+
+/* Static message for a status code. */
+const char* sk_strerror(int status);
+
+/* Default launch configuration for op at (M, N, K) on a device with num_cu
+ * compute units (pass 0 for the MI355X's 256).  Pure host logic.
+ * Replaces the warmup-time pickers pick_matmul / pick_gateup / pick_normed
+ * (engine/kernels/gemm.py:516-660). */
+int sk_default_config(int op, int M, int N, int K, int num_cu, sk_config* out);
+
+/* Check a config against op/shape limits (tile sizes, LDS, registers).
+ * Pure host logic; returns SK_OK or SK_ERR_CONFIG/SK_ERR_SHAPE. */
+int sk_check_config(int op, int M, int N, int K, const sk_config* cfg);
+
+/* Workspace bytes op needs at (M, N, K) with cfg (NULL = default config). */
+size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg);
+
+/* C[M,N] = bf16(A[M,K] @ W[N,K]^T), fp32 accumulation.
+ * Replaces SkinnyMatmul.__call__ / _skinny_kernel + _sum_kernel
+ * (engine/kernels/gemm.py:349-378, 59-112) and Gemv without gate/up
+ * (gemm.py:259-292); the reference's cuBLAS baseline is `a @ w.t()`
+ * (gemm.py:527).  Call sites: mm["qkv"], mm["o"], mm["d"], mm["lm"]
+ * (engine/model.py:202-210). */
+int sk_gemm_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw,
+                 sk_bf16* C, int64_t ldc, int M, int N, int K,
+                 const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Out[M,I] = bf16(bf16(silu(bf16 g)) * bf16 u), g = A @ Wg^T, u = A @ Wu^T,
+ * both fp32-accumulated.  Wg/Wu are the gate and up halves of the fused
+ * gate|up weight (engine/model.py:116: wgu[:I], wgu[I:]).
+ * Replaces SkinnyGateUp.__call__ / _gateup_kernel + _sum_gateup_kernel +
+ * _swiglu_epilogue (engine/kernels/gemm.py:315-346, 124-181, 115-121) and the
+ * cuBLAS + swiglu pipeline (gemm.py:569, engine/kernels/swiglu.py:14-33).
+ * Call site: mm["gu"] (engine/model.py:207). */
+int sk_gateup_swiglu_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* Wg, const sk_bf16* Wu,
+                          int64_t ldw, sk_bf16* Out, int64_t ldo, int M, int I, int K,
+                          const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* ids[m] = min{ n : L[m,n] = max_n L[m,n] }, maxv[m] = float(max_n L[m,n]),
+ * where L = bf16(A @ W^T) is never written to memory.  Lowest index wins on
+ * exact ties, NaN compares above every number (torch.argmax semantics).
+ * Replaces `mm["lm"](...)` followed by `logits.argmax(dim=-1)`
+ * (engine/model.py:210, 375; engine/engine.py:207, 228) and rank 0 of
+ * fast_topk (engine/kernels/topk.py:17-46).  Needs a workspace. */
+int sk_lm_argmax_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw,
+                      int64_t* ids, float* maxv, int M, int V, int K,
+                      const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Argmax over materialised bf16 logits L[M,V] (row stride ld), same tie and
+ * NaN rules as sk_lm_argmax_bf16.  Replaces `logits.argmax(dim=-1)`
+ * (engine/engine.py:207) and fast_topk rank 0 (engine/kernels/topk.py:17-37).
+ * Needs a workspace (sk_workspace_bytes(SK_OP_ARGMAX, M, V, 0, NULL)). */
+int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, float* maxv,
+                   void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* xout = bf16(x + y); out = bf16(w * bf16(xout * rsqrt(mean(xout^2) + eps))).
+ * All [M, K] with row stride ld; xout must not overlap x or y; out must not
+ * overlap x, y or xout.  Replaces add_rms_norm (engine/kernels/add_rmsnorm.py:
+ * 15-43), the unfused prologue of the qkv/gu/lm call sites
+ * (engine/model.py:153, 166-170). */
+int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, float eps,
+                        sk_bf16* xout, sk_bf16* out, int M, int K, int64_t ld,
+                        hipStream_t stream);
+
+/* Out[M,I] = bf16(bf16(silu(g)) * u) for gu[M, 2I] = [g | u] (row stride ld_gu).
+ * Replaces swiglu (engine/kernels/swiglu.py:14-33). */
+int sk_swiglu_bf16(const sk_bf16* gu, int64_t ld_gu, sk_bf16* out, int64_t ld_out,
+                   int M, int I, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STARTER_AMD_H */

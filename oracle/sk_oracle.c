@@ -1,0 +1,195 @@
+/*
+ * sk_oracle.c - CPU restatement of the reference's decode-GEMM hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker.
+ * The product (libstarter_amd.so) never links or calls it.
+ *
+ * Every function restates the arithmetic of a reference function, cited per
+ * function.  bf16 values are raw uint16 bits; fp32 -> bf16 is round to nearest
+ * even with NaN kept quiet, the rounding of torch's `.to(torch.bfloat16)` and
+ * Triton's `.to(tl.bfloat16)`.
+ *
+ * Accumulation order: the reference's contract is "fp32 accumulation, one
+ * rounding to bf16" (engine/kernels/gemm.py:87-101; its cuBLAS baseline
+ * `a @ w.t()`, gemm.py:527) and its tests fix no summation order (tolerance
+ * 0.02*max|ref| + 1e-3, tests/test_kernels.py:111-124).  This file fixes one:
+ * eight interleaved fp32 partial sums p[j] = sum_{k = j mod 8} a*w in k order,
+ * combined as ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)).  Deterministic, and
+ * vectorisable without reassociation.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+static inline float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u; /* NaN -> canonical quiet NaN, as torch */
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline float round_bf(float f) { return bf2f(f2bf(f)); }
+
+/* fp32 dot product of two bf16 rows in the fixed 8-lane order above. */
+static float dot_bf16(const uint16_t* a, const uint16_t* w, int K) {
+  float p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int k = 0;
+  for (; k + 8 <= K; k += 8)
+    for (int j = 0; j < 8; ++j) p[j] += bf2f(a[k + j]) * bf2f(w[k + j]);
+  for (int j = 0; k < K; ++k, ++j) p[j] += bf2f(a[k]) * bf2f(w[k]);
+  return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+}
+
+/* bf16 round of fp32 value (exported for the tests' rounding checks). */
+uint16_t oracle_f32_to_bf16(float f) { return f2bf(f); }
+
+/* C[m,n] fp32 sums (before rounding): the reference's `acc` of
+ * _skinny_kernel (gemm.py:87-97) / Gemv (gemm.py:233-244). */
+void oracle_gemm_f32(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, float* C, int M, int N, int K,
+                     int threads) {
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (int n = 0; n < N; ++n)
+    for (int m = 0; m < M; ++m) C[(int64_t)m * N + n] = dot_bf16(A + (int64_t)m * lda, W + (int64_t)n * ldw, K);
+}
+
+/* C = bf16(A @ W^T): SkinnyMatmul (gemm.py:98-99, 104-112) and `a @ w.t()`. */
+void oracle_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, uint16_t* C, int64_t ldc, int M,
+                      int N, int K, int threads) {
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (int n = 0; n < N; ++n)
+    for (int m = 0; m < M; ++m)
+      C[(int64_t)m * ldc + n] = f2bf(dot_bf16(A + (int64_t)m * lda, W + (int64_t)n * ldw, K));
+}
+
+/* _swiglu_epilogue (gemm.py:115-121) / _swiglu_kernel (swiglu.py:21-24):
+ * bf16(g), bf16(u), s = bf16(g / (1 + exp(-g))) in fp32, out = bf16(s * u). */
+static inline uint16_t swiglu_bf(float g, float u) {
+  const float gb = round_bf(g), ub = round_bf(u);
+  const float s = round_bf(gb / (1.0f + expf(-gb)));
+  return f2bf(s * ub);
+}
+
+uint16_t oracle_swiglu_scalar(uint16_t g, uint16_t u) { return swiglu_bf(bf2f(g), bf2f(u)); }
+
+/* swiglu over gu[M, 2I] = [g | u] (swiglu.py:27-33). */
+void oracle_swiglu_bf16(const uint16_t* gu, int64_t ld_gu, uint16_t* out, int64_t ld_out, int M, int I) {
+  for (int m = 0; m < M; ++m)
+    for (int i = 0; i < I; ++i)
+      out[(int64_t)m * ld_out + i] = swiglu_bf(bf2f(gu[(int64_t)m * ld_gu + i]), bf2f(gu[(int64_t)m * ld_gu + I + i]));
+}
+
+/* SkinnyGateUp (gemm.py:149-168, 171-181): g and u fp32-accumulated over the
+ * gate rows Wg = wgu[0:I] and up rows Wu = wgu[I:2I] (model.py:116), then the
+ * SwiGLU epilogue. */
+void oracle_gateup_swiglu_bf16(const uint16_t* A, int64_t lda, const uint16_t* Wg, const uint16_t* Wu, int64_t ldw,
+                               uint16_t* out, int64_t ldo, int M, int I, int K, int threads) {
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+  for (int n = 0; n < I; ++n)
+    for (int m = 0; m < M; ++m) {
+      const float g = dot_bf16(A + (int64_t)m * lda, Wg + (int64_t)n * ldw, K);
+      const float u = dot_bf16(A + (int64_t)m * lda, Wu + (int64_t)n * ldw, K);
+      out[(int64_t)m * ldo + n] = swiglu_bf(g, u);
+    }
+}
+
+/* add_rms_norm (add_rmsnorm.py:15-29; cast placement rmsnorm.py:34-45):
+ * s = bf16(x + y) -> xout; var = sum(s^2) / K; r = 1 / sqrt(var + eps);
+ * out = bf16(w * bf16(s * r)).  The reference reduces sum(s^2) with an fp32
+ * tree (tl.sum); its result sits within a few fp32 ulps of the exact sum, so
+ * the oracle forms the sum exactly in fp64 and rounds it once to fp32 rather
+ * than adopting one particular tree order. */
+void oracle_add_rmsnorm_bf16(const uint16_t* x, const uint16_t* y, const uint16_t* w, float eps, uint16_t* xout,
+                             uint16_t* out, int M, int K, int64_t ld) {
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* xr = x + (int64_t)m * ld;
+    const uint16_t* yr = y + (int64_t)m * ld;
+    double sq = 0.0;
+    for (int k = 0; k < K; ++k) {
+      const uint16_t s = f2bf(bf2f(xr[k]) + bf2f(yr[k]));
+      xout[(int64_t)m * ld + k] = s;
+      const double sf = (double)bf2f(s);
+      sq += sf * sf;
+    }
+    const float r = 1.0f / sqrtf((float)sq / (float)K + eps);
+    for (int k = 0; k < K; ++k) {
+      const float sf = bf2f(xout[(int64_t)m * ld + k]);
+      out[(int64_t)m * ld + k] = f2bf(bf2f(w[k]) * round_bf(sf * r));
+    }
+  }
+}
+
+/* torch.argmax over bf16 logits (engine.py:207; topk.py:27-34): the first
+ * column holding the row maximum; any NaN counts as the maximum (first NaN
+ * wins); -0 == +0.  maxv = that value as fp32. */
+void oracle_argmax_bf16(const uint16_t* L, int64_t ld, int M, int V, int64_t* ids, float* maxv) {
+  for (int m = 0; m < M; ++m) {
+    const uint16_t* r = L + (int64_t)m * ld;
+    int best = 0;
+    float bv = bf2f(r[0]);
+    for (int n = 1; n < V && !isnan(bv); ++n) {
+      const float v = bf2f(r[n]);
+      if (isnan(v) || v > bv) {
+        bv = v;
+        best = n;
+      }
+    }
+    ids[m] = best;
+    maxv[m] = bv;
+  }
+}
+
+/* lm_head + greedy token: argmax over bf16(A @ W^T) rows (model.py:210 then
+ * engine.py:207), without keeping the logits. */
+void oracle_lm_argmax_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t ldw, int M, int V, int K,
+                           int64_t* ids, float* maxv, int threads) {
+  for (int m = 0; m < M; ++m) {
+    int64_t best = -1;
+    float bv = 0.0f;
+    int nan_seen = 0;
+#pragma omp parallel num_threads(threads > 0 ? threads : 1)
+    {
+      int64_t lb = -1;
+      float lv = 0.0f;
+      int ln = 0;
+#pragma omp for schedule(static)
+      for (int n = 0; n < V; ++n) {
+        const float v = bf2f(f2bf(dot_bf16(A + (int64_t)m * lda, W + (int64_t)n * ldw, K)));
+        if (ln) continue;
+        if (isnan(v)) {
+          ln = 1;
+          lb = n;
+          lv = v;
+        } else if (lb < 0 || v > lv) {
+          lb = n;
+          lv = v;
+        }
+      }
+#pragma omp critical
+      {
+        if (lb >= 0) {
+          if (ln) {
+            if (!nan_seen || lb < best) {
+              best = lb;
+              bv = lv;
+              nan_seen = 1;
+            }
+          } else if (!nan_seen && (best < 0 || lv > bv || (lv == bv && lb < best))) {
+            best = lb;
+            bv = lv;
+          }
+        }
+      }
+    }
+    ids[m] = best;
+    maxv[m] = bv;
+  }
+}

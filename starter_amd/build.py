@@ -1,0 +1,90 @@
+"""Build libstarter_amd.so (gfx950) in-tree with hipcc.
+
+The library is the C ABI declared in ``include/starter_amd.h``.  Every
+translation unit is compiled to an object under ``starter_amd/_build`` in
+parallel (one per epilogue for the kernel instances), then linked into
+``starter_amd/lib/libstarter_amd.so``.  No CMake, no torch extension: the
+library links only against the HIP runtime, which it shares with
+PyTorch-ROCm when both are loaded in one process.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "lib" / "libstarter_amd.so"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 anywhere in the device code.
+COMMON = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+]
+
+N_EPI = 5  # EPI_STORE, EPI_SWIGLU, EPI_ARGMAX, EPI_PART, EPI_PART_GU
+
+
+def _units() -> list[tuple[Path, list[str], Path]]:
+    units = [(CSRC / "sk_abi.hip", [], BUILD / "sk_abi.o")]
+    for epi in range(N_EPI):
+        units.append((CSRC / "sk_inst_mfma.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfma_{epi}.o"))
+        units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
+    return units
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    # hipcc's host pass warns about the device-only target feature; anything
+    # else is surfaced.
+    noise = ("packed-fp32-ops", "warning: feature flag", "1 warning generated", "warnings generated")
+    for line in (r.stderr or "").splitlines():
+        if line.strip() and not any(n in line for n in noise):
+            print(line, file=sys.stderr)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every HIP translation unit and link the shared library."""
+    if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
+        raise RuntimeError("hipcc not found; the library needs ROCm's hipcc to build")
+    BUILD.mkdir(parents=True, exist_ok=True)
+    LIB.parent.mkdir(parents=True, exist_ok=True)
+    jobs = jobs or min(16, os.cpu_count() or 4)
+    units = _units()
+
+    def compile_one(u):
+        src, defs, obj = u
+        cmd = [HIPCC, *COMMON, *defs, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        _run(cmd)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(compile_one, units))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    import time
+
+    t0 = time.time()
+    out = build(verbose="-v" in sys.argv)
+    print(f"built {out} in {time.time() - t0:.1f}s")

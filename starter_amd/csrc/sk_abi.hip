@@ -1,0 +1,481 @@
+// sk_abi.hip - extern "C" entry points of libstarter_amd.so (declared in
+// include/starter_amd.h): argument validation, the launch planner and the
+// kernel launches.  Validation happens before any HIP call, so a rejected
+// call touches neither the device nor the stream.
+#include "starter_amd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string.h>
+#include <unordered_map>
+
+#define SK_AUX_KERNELS 1
+#include "sk_registry.hpp"
+
+namespace {
+
+constexpr int kDefaultCU = 256;          // MI355X compute units
+constexpr int kMaxGrid = 8192;           // bound on workgroups of a persistent launch
+constexpr size_t kMaxLds = 160 * 1024;   // gfx950 LDS per CU (dynamic LDS budget per workgroup)
+constexpr size_t kPrefLds = 64 * 1024;   // keep >= 2 workgroups per CU when the table has a choice
+constexpr int kArgmaxChunk = 4096;       // columns per workgroup of sk_argmax_bf16
+constexpr int kMaxM = 64;                // rows per kernel launch; more are chunked
+
+int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Device facts, queried once per device.
+// ---------------------------------------------------------------------------
+struct DevInfo {
+  int status = -1;   // -1 unknown, else sk_status
+  int num_cu = 0;
+};
+
+std::mutex g_mu;
+DevInfo g_dev[64];
+
+int device_info(int* num_cu) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SK_ERR_DEVICE;
+  std::lock_guard<std::mutex> lk(g_mu);
+  DevInfo& d = g_dev[dev];
+  if (d.status < 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+      d.status = SK_ERR_DEVICE;
+    } else if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+      d.status = SK_ERR_DEVICE;   // code objects are built for gfx950 only
+    } else {
+      d.num_cu = prop.multiProcessorCount;
+      d.status = SK_OK;
+    }
+  }
+  *num_cu = d.num_cu;
+  return d.status;
+}
+
+// Occupancy (workgroups per CU) and static limits of a kernel instance.
+struct FnInfo {
+  int max_threads = 0;
+  size_t spill = 0;
+};
+std::unordered_map<const void*, FnInfo> g_fn;
+std::unordered_map<unsigned long long, int> g_occ;
+
+int fn_info(const void* fn, FnInfo* out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_fn.find(fn);
+  if (it == g_fn.end()) {
+    hipFuncAttributes a;
+    if (hipFuncGetAttributes(&a, fn) != hipSuccess) return SK_ERR_DEVICE;
+    FnInfo f;
+    f.max_threads = a.maxThreadsPerBlock;
+    f.spill = a.localSizeBytes;
+    it = g_fn.emplace(fn, f).first;
+  }
+  *out = it->second;
+  return SK_OK;
+}
+
+int occupancy(const void* fn, int threads, size_t lds) {
+  const unsigned long long key =
+      (reinterpret_cast<uintptr_t>(fn) * 1315423911ull) ^ ((unsigned long long)threads << 40) ^ (unsigned long long)lds;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_occ.find(key);
+    if (it != g_occ.end()) return it->second;
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn), threads, lds) != hipSuccess)
+    n = 1;
+  if (n < 1) n = 1;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_occ[key] = n;
+  return n;
+}
+
+// ---------------------------------------------------------------------------
+// Planner: config -> kernel instance, decomposition, LDS and workspace.
+// ---------------------------------------------------------------------------
+struct Plan {
+  sk_config cfg;
+  int epi = 0;
+  int tm = 0, tn = 0, tku = 0;  // template parameters: MT|MR, NT|R, KU bound
+  int nrb = 0;                  // tiles along N
+  int slice_units = 0;
+  size_t lds = 0;
+  sk::KernelFn fn = nullptr;
+};
+
+int bucket(const int* list, int n, int v) {
+  for (int i = 0; i < n; ++i)
+    if (list[i] >= v) return list[i];
+  return -1;
+}
+
+int epi_for(int op, int split) {
+  if (op == SK_OP_GEMM) return split > 1 ? sk::EPI_PART : sk::EPI_STORE;
+  if (op == SK_OP_GATEUP) return split > 1 ? sk::EPI_PART_GU : sk::EPI_SWIGLU;
+  return sk::EPI_ARGMAX;
+}
+
+// Pure host logic: fills everything except fn/grid-from-occupancy.
+int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
+  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+  if (M < 1 || M > kMaxM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
+  if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0) return SK_ERR_CONFIG;
+  if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
+  const bool gateup = (op == SK_OP_GATEUP);
+  pl->cfg = c;
+  pl->epi = epi_for(op, c.split);
+  int units, partial_rows;
+  if (c.path == SK_PATH_MFMA) {
+    if (gateup ? c.rows != 16 : (c.rows != 16 && c.rows != 32)) return SK_ERR_CONFIG;
+    units = K / 32;
+    pl->tm = cdiv(M, 16);
+    pl->tn = gateup ? 2 : c.rows / 16;
+    pl->tku = bucket(sk::kMfmaKU, (int)(sizeof(sk::kMfmaKU) / sizeof(int)), c.ku);
+    partial_rows = 16 * pl->tn;
+    if (c.waves > sk::max_waves_for_regs(sk::mfma_regs(pl->tm, pl->tn, pl->tku < 0 ? 20 : pl->tku)))
+      return SK_ERR_CONFIG;
+  } else if (c.path == SK_PATH_GEMV) {
+    if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
+    if (M > 8) return SK_ERR_CONFIG;
+    units = cdiv(K, 512);
+    pl->tm = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+    pl->tn = c.rows;
+    pl->tku = bucket(sk::kGemvKU, (int)(sizeof(sk::kGemvKU) / sizeof(int)), c.ku);
+    partial_rows = gateup ? 2 * c.rows : c.rows;
+    if (c.waves > sk::max_waves_for_regs(sk::gemv_regs(pl->tm, partial_rows, pl->tku < 0 ? 10 : pl->tku)))
+      return SK_ERR_CONFIG;
+  } else {
+    return SK_ERR_CONFIG;
+  }
+  if (pl->tku < 0) return SK_ERR_CONFIG;
+  pl->slice_units = cdiv(units, c.split);
+  if ((long)c.waves * c.ku < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
+  if (c.split > 1 && (c.split - 1) * pl->slice_units >= units) return SK_ERR_CONFIG;  // empty split
+  const int out_rows = (c.path == SK_PATH_MFMA) ? (gateup ? 16 : c.rows) : c.rows;
+  pl->nrb = cdiv(N, out_rows);
+  pl->lds = (size_t)2 * c.waves * M * partial_rows * sizeof(float) + (op == SK_OP_LM_ARGMAX ? 8 * (size_t)M : 0);
+  if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
+  if (c.grid > 0 && (c.grid % c.split) != 0) return SK_ERR_CONFIG;
+  return SK_OK;
+}
+
+// Upper bound of the workgroups a plan launches (what the workspace covers).
+int grid_bound(const Plan& pl) {
+  if (pl.cfg.grid > 0) return pl.cfg.grid;
+  return pl.cfg.split * (pl.nrb < kMaxGrid ? pl.nrb : kMaxGrid);
+}
+
+size_t plan_workspace(int op, int M, int N, const Plan& pl) {
+  if (op == SK_OP_LM_ARGMAX) return (size_t)grid_bound(pl) * M * sizeof(unsigned long long);
+  if (pl.cfg.split > 1) return (size_t)(op == SK_OP_GATEUP ? 2 : 1) * pl.cfg.split * M * (size_t)N * sizeof(float);
+  return 0;
+}
+
+int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
+  (void)num_cu;   // the table is tuned for the MI355X's 256 CUs
+  if (M < 1 || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
+  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+  const int Mk = M > kMaxM ? kMaxM : M;
+  const int units = K / 32;
+  const int MT = cdiv(Mk, 16);
+  const bool gateup = (op == SK_OP_GATEUP);
+  const int NT = gateup ? 2 : 1;
+  // Prefer the largest K-unit bound (fewest waves sharing a tile, most bytes
+  // in flight per wave) whose registers still allow the wave count, then the
+  // fewest global K splits whose LDS fits the preferred budget.
+  const int kus[] = {20, 16, 10, 8, 5};
+  for (size_t pass = 0; pass < 2; ++pass) {
+    const size_t lds_cap = pass == 0 ? kPrefLds : kMaxLds;
+    for (int ku_cap : kus) {
+      const int wmax = sk::max_waves_for_regs(sk::mfma_regs(MT, NT, ku_cap));
+      if (sk::mfma_regs(MT, NT, ku_cap) > 256) continue;    // keep >= 2 waves per SIMD
+      for (int split = 1; split <= 32; ++split) {
+        if (op == SK_OP_LM_ARGMAX && split > 1) break;
+        const int slice = cdiv(units, split);
+        if (split > 1 && (split - 1) * slice >= units) break;
+        const int waves = cdiv(slice, ku_cap);
+        if (waves > wmax) continue;
+        sk_config c;
+        memset(&c, 0, sizeof(c));
+        c.path = SK_PATH_MFMA;
+        c.rows = 16;
+        c.split = split;
+        c.waves = waves;
+        c.ku = cdiv(slice, waves);
+        c.grid = 0;
+        Plan pl;
+        if (plan_shape(op, Mk, N, K, c, &pl) != SK_OK) continue;
+        if (pl.lds > lds_cap) continue;
+        *out = c;
+        return SK_OK;
+      }
+    }
+  }
+  return SK_ERR_SHAPE;
+}
+
+int resolve_config(int op, int M, int N, int K, const sk_config* cfg, sk_config* out) {
+  if (cfg) {
+    *out = *cfg;
+    if (out->path == SK_PATH_AUTO) {
+      sk_config d;
+      int st = default_config(op, M, N, K, 0, &d);
+      if (st) return st;
+      *out = d;
+    }
+    return SK_OK;
+  }
+  return default_config(op, M, N, K, 0, out);
+}
+
+// Bind the kernel instance and compute the launch grid.
+int bind_plan(Plan* pl, int num_cu, int* grid) {
+  sk::KernelFn fn = (pl->cfg.path == SK_PATH_MFMA) ? sk::mfma_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku)
+                                                    : sk::gemv_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
+  if (!fn) return SK_ERR_CONFIG;
+  FnInfo fi;
+  int st = fn_info(reinterpret_cast<const void*>(fn), &fi);
+  if (st) return st;
+  const int threads = 64 * pl->cfg.waves;
+  if (threads > fi.max_threads) return SK_ERR_CONFIG;
+  if (pl->lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)pl->lds) != hipSuccess)
+    return SK_ERR_CONFIG;
+  pl->fn = fn;
+  const int S = pl->cfg.split;
+  if (pl->cfg.grid > 0) {
+    *grid = pl->cfg.grid;
+    return SK_OK;
+  }
+  const int per_cu = occupancy(reinterpret_cast<const void*>(fn), threads, pl->lds);
+  long cap = (long)per_cu * num_cu / S;   // resident workgroups per K split
+  if (cap < 1) cap = 1;
+  int per_split = pl->nrb < cap ? pl->nrb : (int)cap;
+  if (per_split > kMaxGrid) per_split = kMaxGrid;
+  // Even out tiles per workgroup so the last round is not a partial one.
+  const int tiles_per = cdiv(pl->nrb, per_split);
+  per_split = cdiv(pl->nrb, tiles_per);
+  *grid = per_split * S;
+  return SK_OK;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return pa < pb + bbytes && pb < pa + abytes;
+}
+
+int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SK_OK : SK_ERR_LAUNCH;
+}
+
+// Shared driver of the three GEMM-family ops (rows beyond 64 are processed in
+// 64-row chunks, each streaming the weights once more).
+int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, const sk_bf16* W1, int64_t ldw,
+                    sk_bf16* C, int64_t ldc, int64_t* ids, float* maxv, int M, int N, int K, const sk_config* cfg,
+                    void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (M < 0 || N < 1 || K < 32) return SK_ERR_SHAPE;
+  if (!A || !W0 || (op == SK_OP_GATEUP && !W1)) return SK_ERR_NULL;
+  if (op == SK_OP_LM_ARGMAX ? (!ids || !maxv) : !C) return SK_ERR_NULL;
+  if ((K & 31) != 0 || lda < K || ldw < K || (op != SK_OP_LM_ARGMAX && ldc < N)) return SK_ERR_SHAPE;
+  if (!aligned16(A) || !aligned16(W0) || (W1 && !aligned16(W1)) || (lda & 7) || (ldw & 7)) return SK_ERR_ALIGN;
+  if (M == 0) return SK_OK;
+  // Validate every chunk's plan before enqueuing anything.
+  Plan plans[2];
+  int chunk_rows[2] = {M < kMaxM ? M : kMaxM, M % kMaxM};
+  const int nplans = (M > kMaxM && (M % kMaxM) != 0) ? 2 : 1;
+  for (int i = 0; i < nplans; ++i) {
+    sk_config c;
+    int st = resolve_config(op, chunk_rows[i], N, K, cfg, &c);
+    if (st) return st;
+    st = plan_shape(op, chunk_rows[i], N, K, c, &plans[i]);
+    if (st) return st;
+    const size_t need = plan_workspace(op, chunk_rows[i], N, plans[i]);
+    if (need > 0 && (!ws || ws_bytes < need)) return SK_ERR_WORKSPACE;
+  }
+  if (op == SK_OP_LM_ARGMAX && M > kMaxM) return SK_ERR_SHAPE;   // ids of one call come from one pass
+  int num_cu = 0;
+  int st = device_info(&num_cu);
+  if (st) return st;
+  int grids[2];
+  for (int i = 0; i < nplans; ++i) {
+    st = bind_plan(&plans[i], num_cu, &grids[i]);
+    if (st) return st;
+    if (op == SK_OP_LM_ARGMAX && grids[i] > grid_bound(plans[i])) return SK_ERR_CONFIG;
+  }
+  for (int m0 = 0; m0 < M; m0 += kMaxM) {
+    const int rows = (M - m0) < kMaxM ? (M - m0) : kMaxM;
+    const Plan& pl = plans[rows == chunk_rows[0] ? 0 : 1];
+    const int grid = grids[rows == chunk_rows[0] ? 0 : 1];
+    sk::Args a;
+    memset(&a, 0, sizeof(a));
+    a.A = A + (int64_t)m0 * lda;
+    a.W0 = W0;
+    a.W1 = W1;
+    a.C = C ? C + (int64_t)m0 * ldc : nullptr;
+    a.part = static_cast<float*>(ws);
+    a.best = static_cast<unsigned long long*>(ws);
+    a.lda = lda;
+    a.ldw = ldw;
+    a.ldc = ldc;
+    a.M = rows;
+    a.N = N;
+    a.K = K;
+    a.S = pl.cfg.split;
+    a.slice_units = pl.slice_units;
+    a.ku = pl.cfg.ku;
+    a.nrb = pl.nrb;
+    pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
+    if ((st = launch_status())) return st;
+    if (op == SK_OP_LM_ARGMAX) {
+      sk::argmax_final_kernel<<<dim3(rows), dim3(256), 0, stream>>>(a.best, grid, rows, ids + m0, maxv + m0);
+    } else if (pl.cfg.split > 1) {
+      const long total = (long)rows * N;
+      int g = (int)((total + 255) / 256);
+      if (g > 4 * num_cu * 8) g = 4 * num_cu * 8;
+      if (op == SK_OP_GATEUP)
+        sk::splitk_reduce_kernel<true><<<dim3(g), dim3(256), 0, stream>>>(a.part, a.C, ldc, rows, N, pl.cfg.split);
+      else
+        sk::splitk_reduce_kernel<false><<<dim3(g), dim3(256), 0, stream>>>(a.part, a.C, ldc, rows, N, pl.cfg.split);
+    }
+    if ((st = launch_status())) return st;
+  }
+  return SK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sk_version(void) { return (0 << 16) | 1; }
+
+const char* sk_strerror(int status) {
+  switch (status) {
+    case SK_OK: return "ok";
+    case SK_ERR_NULL: return "a required pointer is NULL";
+    case SK_ERR_SHAPE: return "shape or stride out of the supported range";
+    case SK_ERR_ALIGN: return "pointer or stride not aligned for 16-byte loads";
+    case SK_ERR_WORKSPACE: return "workspace missing or too small";
+    case SK_ERR_CONFIG: return "launch configuration invalid for this shape";
+    case SK_ERR_LAUNCH: return "kernel launch failed";
+    case SK_ERR_DEVICE: return "no usable gfx950 device";
+    case SK_ERR_ALIAS: return "output overlaps an input";
+  }
+  return "unknown status";
+}
+
+int sk_default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
+  if (!out) return SK_ERR_NULL;
+  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+  return default_config(op, M, N, K, num_cu, out);
+}
+
+int sk_check_config(int op, int M, int N, int K, const sk_config* cfg) {
+  if (!cfg) return SK_ERR_NULL;
+  sk_config c;
+  int st = resolve_config(op, M > kMaxM ? kMaxM : M, N, K, cfg, &c);
+  if (st) return st;
+  Plan pl;
+  return plan_shape(op, M > kMaxM ? kMaxM : M, N, K, c, &pl);
+}
+
+size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg) {
+  if (op == SK_OP_ARGMAX) {
+    if (M < 1 || N < 1) return 0;
+    return (size_t)cdiv(N, kArgmaxChunk) * M * sizeof(unsigned long long);
+  }
+  if (M < 1) return 0;
+  const int Mk = M > kMaxM ? kMaxM : M;
+  sk_config c;
+  if (resolve_config(op, Mk, N, K, cfg, &c)) return 0;
+  Plan pl;
+  if (plan_shape(op, Mk, N, K, c, &pl)) return 0;
+  return plan_workspace(op, Mk, N, pl);
+}
+
+int sk_gemm_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N,
+                 int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  return run_gemm_family(SK_OP_GEMM, A, lda, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, ws, ws_bytes,
+                         stream);
+}
+
+int sk_gateup_swiglu_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw,
+                          sk_bf16* Out, int64_t ldo, int M, int I, int K, const sk_config* cfg, void* ws,
+                          size_t ws_bytes, hipStream_t stream) {
+  return run_gemm_family(SK_OP_GATEUP, A, lda, Wg, Wu, ldw, Out, ldo, nullptr, nullptr, M, I, K, cfg, ws, ws_bytes,
+                         stream);
+}
+
+int sk_lm_argmax_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M,
+                      int V, int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  return run_gemm_family(SK_OP_LM_ARGMAX, A, lda, W, nullptr, ldw, nullptr, 0, ids, maxv, M, V, K, cfg, ws, ws_bytes,
+                         stream);
+}
+
+int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, float* maxv, void* ws, size_t ws_bytes,
+                   hipStream_t stream) {
+  if (M < 0 || V < 1 || ld < V) return SK_ERR_SHAPE;
+  if (!L || !ids || !maxv) return SK_ERR_NULL;
+  if (!aligned16(L) || (ld & 7)) return SK_ERR_ALIGN;
+  if (M == 0) return SK_OK;
+  if (M > 65535) return SK_ERR_SHAPE;
+  const int chunks = cdiv(V, kArgmaxChunk);
+  const size_t need = (size_t)chunks * M * sizeof(unsigned long long);
+  if (!ws || ws_bytes < need) return SK_ERR_WORKSPACE;
+  int num_cu = 0;
+  int st = device_info(&num_cu);
+  if (st) return st;
+  unsigned long long* best = static_cast<unsigned long long*>(ws);
+  sk::argmax_partial_kernel<<<dim3(chunks, M), dim3(256), 0, stream>>>(L, ld, M, V, kArgmaxChunk, best);
+  if ((st = launch_status())) return st;
+  sk::argmax_final_kernel<<<dim3(M), dim3(256), 0, stream>>>(best, chunks, M, ids, maxv);
+  return launch_status();
+}
+
+int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, float eps, sk_bf16* xout, sk_bf16* out,
+                        int M, int K, int64_t ld, hipStream_t stream) {
+  if (M < 0 || K < 8 || (K & 7) || K > sk::RMS_THREADS * 8 * sk::RMS_MAX_CHUNKS || ld < K) return SK_ERR_SHAPE;
+  if (!x || !y || !w || !xout || !out) return SK_ERR_NULL;
+  if (!aligned16(x) || !aligned16(y) || !aligned16(w) || !aligned16(xout) || !aligned16(out) || (ld & 7))
+    return SK_ERR_ALIGN;
+  if (M == 0) return SK_OK;
+  if (M > 65535) return SK_ERR_SHAPE;
+  // xout may be x or y itself (each element is read before the same thread
+  // writes it), but must not partially overlap them; out overlaps nothing.
+  const size_t bytes = ((size_t)(M - 1) * ld + K) * sizeof(sk_bf16);
+  if ((xout != x && overlaps(xout, bytes, x, bytes)) || (xout != y && overlaps(xout, bytes, y, bytes)) ||
+      overlaps(out, bytes, x, bytes) || overlaps(out, bytes, y, bytes) || overlaps(out, bytes, xout, bytes))
+    return SK_ERR_ALIAS;
+  int num_cu = 0;
+  int st = device_info(&num_cu);
+  if (st) return st;
+  sk::add_rmsnorm_kernel<<<dim3(M), dim3(sk::RMS_THREADS), 0, stream>>>(x, y, w, eps, xout, out, K, ld);
+  return launch_status();
+}
+
+int sk_swiglu_bf16(const sk_bf16* gu, int64_t ld_gu, sk_bf16* out, int64_t ld_out, int M, int I, hipStream_t stream) {
+  if (M < 0 || I < 1 || ld_gu < 2 * (int64_t)I || ld_out < I) return SK_ERR_SHAPE;
+  if (!gu || !out) return SK_ERR_NULL;
+  if (M == 0) return SK_OK;
+  const size_t in_bytes = ((size_t)(M - 1) * ld_gu + 2 * (size_t)I) * sizeof(sk_bf16);
+  const size_t out_bytes = ((size_t)(M - 1) * ld_out + I) * sizeof(sk_bf16);
+  if (overlaps(out, out_bytes, gu, in_bytes)) return SK_ERR_ALIAS;
+  int num_cu = 0;
+  int st = device_info(&num_cu);
+  if (st) return st;
+  const long total = (long)M * I;
+  long g = (total + 255) / 256;
+  if (g > 8L * num_cu * 8) g = 8L * num_cu * 8;
+  sk::swiglu_kernel<<<dim3((unsigned)g), dim3(256), 0, stream>>>(gu, ld_gu, out, ld_out, M, I);
+  return launch_status();
+}
+
+}  // extern "C"

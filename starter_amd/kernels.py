@@ -1,0 +1,341 @@
+"""Python face of the decode-GEMM hot path, mirroring the reference's kernel API.
+
+Each class/function keeps the reference's name, argument meaning and error
+behaviour (a Python exception on failure) and runs the HIP kernels of
+libstarter_amd.so through the C ABI:
+
+===========================  ==================================================
+reference                    here
+===========================  ==================================================
+SkinnyMatmul  gemm.py:349    SkinnyMatmul (sk_gemm_bf16)
+SkinnyGateUp  gemm.py:315    SkinnyGateUp (sk_gateup_swiglu_bf16)
+Gemv          gemm.py:259    Gemv (sk_gemm_bf16 / sk_gateup_swiglu_bf16, GEMV path)
+pick_matmul   gemm.py:516    pick_matmul (offline table instead of warmup timing)
+pick_gateup   gemm.py:561    pick_gateup
+pick_normed   gemm.py:602    pick_normed
+add_rms_norm  add_rmsnorm.py add_rms_norm (sk_add_rmsnorm_bf16)
+swiglu        swiglu.py      swiglu (sk_swiglu_bf16)
+fast_topk[0]  topk.py:40     argmax (sk_argmax_bf16)
+logits.argmax engine.py:207  LmArgmax (sk_lm_argmax_bf16, fused into lm_head)
+===========================  ==================================================
+
+All tensors are bf16 and live on one ROCm device; outputs are allocated per
+call with ``torch.empty`` (inside a graph capture they come from the graph's
+pool, as in the reference), workspaces once per instance.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import (SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_PATH_GEMV, SK_PATH_MFMA, SkConfig,
+                   check, cfg_ptr, lib)
+
+BF16 = torch.bfloat16
+
+__all__ = [
+    "SkinnyMatmul", "SkinnyGateUp", "Gemv", "LmArgmax", "gemm", "gateup_swiglu", "lm_argmax", "argmax",
+    "add_rms_norm", "swiglu", "pick_matmul", "pick_gateup", "pick_normed", "pick_lm_argmax", "SkConfig",
+    "SK_PATH_MFMA", "SK_PATH_GEMV",
+]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _mat(t: torch.Tensor, name: str) -> None:
+    _need(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _need(t.dtype == BF16, f"{name} must be bfloat16, got {t.dtype}")
+    _need(t.dim() == 2 and t.stride(1) == 1, f"{name} must be 2-D with unit inner stride")
+
+
+def _device_guard(t: torch.Tensor) -> None:
+    if torch.cuda.current_device() != t.device.index:
+        torch.cuda.set_device(t.device)
+
+
+def _workspace(op: int, M: int, N: int, K: int, cfg: SkConfig | None, device) -> torch.Tensor | None:
+    n = _lib.workspace_bytes(op, M, N, K, cfg)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+
+
+def _ws_args(ws: torch.Tensor | None):
+    return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+
+
+def _config(config: SkConfig | None, kw: dict) -> SkConfig | None:
+    if config is not None and kw:
+        raise ValueError("pass either config= or individual config fields, not both")
+    if kw:
+        return SkConfig.make(**kw)
+    return config
+
+
+# ---------------------------------------------------------------------------
+# Functional entry points
+# ---------------------------------------------------------------------------
+
+def gemm(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, config: SkConfig | None = None,
+         ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = a @ w.T`` (bf16, fp32 accumulation)."""
+    _mat(a, "a")
+    _mat(w, "w")
+    M, K = a.shape
+    N = w.shape[0]
+    _need(w.shape[1] == K, f"K mismatch: a {tuple(a.shape)} vs w {tuple(w.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=BF16, device=a.device)
+    _mat(out, "out")
+    _need(tuple(out.shape) == (M, N), "out shape")
+    if ws is None and _lib.workspace_bytes(SK_OP_GEMM, M, N, K, config):
+        ws = _workspace(SK_OP_GEMM, M, N, K, config, a.device)
+    _device_guard(a)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_gemm_bf16(a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
+                             M, N, K, cfg_ptr(config), wp, wn, _stream(a)), "sk_gemm_bf16")
+    return out
+
+
+def gateup_swiglu(a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, out: torch.Tensor | None = None,
+                  config: SkConfig | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = swiglu(a @ wg.T, a @ wu.T)`` with the reference's bf16 casts."""
+    _mat(a, "a")
+    _mat(wg, "wg")
+    _mat(wu, "wu")
+    M, K = a.shape
+    I = wg.shape[0]
+    _need(wg.shape == wu.shape and wg.shape[1] == K and wg.stride(0) == wu.stride(0), "gate/up weight shapes")
+    if out is None:
+        out = torch.empty((M, I), dtype=BF16, device=a.device)
+    _mat(out, "out")
+    _need(tuple(out.shape) == (M, I), "out shape")
+    if ws is None and _lib.workspace_bytes(SK_OP_GATEUP, M, I, K, config):
+        ws = _workspace(SK_OP_GATEUP, M, I, K, config, a.device)
+    _device_guard(a)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_gateup_swiglu_bf16(a.data_ptr(), a.stride(0), wg.data_ptr(), wu.data_ptr(), wg.stride(0),
+                                      out.data_ptr(), out.stride(0), M, I, K, cfg_ptr(config), wp, wn, _stream(a)),
+          "sk_gateup_swiglu_bf16")
+    return out
+
+
+def lm_argmax(a: torch.Tensor, w: torch.Tensor, config: SkConfig | None = None, ws: torch.Tensor | None = None,
+              ids: torch.Tensor | None = None, maxv: torch.Tensor | None = None):
+    """Greedy token per row of ``bf16(a @ w.T)`` without materialising the logits.
+    Returns ``(ids int64 [M], maxv float32 [M])``."""
+    _mat(a, "a")
+    _mat(w, "w")
+    M, K = a.shape
+    V = w.shape[0]
+    _need(w.shape[1] == K, "K mismatch")
+    ids = torch.empty((M,), dtype=torch.int64, device=a.device) if ids is None else ids
+    maxv = torch.empty((M,), dtype=torch.float32, device=a.device) if maxv is None else maxv
+    if ws is None:
+        ws = _workspace(SK_OP_LM_ARGMAX, M, V, K, config, a.device)
+    _device_guard(a)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_lm_argmax_bf16(a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), ids.data_ptr(),
+                                  maxv.data_ptr(), M, V, K, cfg_ptr(config), wp, wn, _stream(a)),
+          "sk_lm_argmax_bf16")
+    return ids, maxv
+
+
+def argmax(logits: torch.Tensor, ws: torch.Tensor | None = None):
+    """``(logits.argmax(-1), logits.max(-1).float())`` over bf16 logits, lowest index on ties."""
+    _mat(logits, "logits")
+    M, V = logits.shape
+    ids = torch.empty((M,), dtype=torch.int64, device=logits.device)
+    maxv = torch.empty((M,), dtype=torch.float32, device=logits.device)
+    if ws is None:
+        ws = _workspace(SK_OP_ARGMAX, M, V, 0, None, logits.device)
+    _device_guard(logits)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_argmax_bf16(logits.data_ptr(), logits.stride(0), M, V, ids.data_ptr(), maxv.data_ptr(), wp, wn,
+                               _stream(logits)), "sk_argmax_bf16")
+    return ids, maxv
+
+
+def add_rms_norm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, eps: float,
+                 xout: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``xout = x + y`` (bf16; in place into ``x`` when ``xout`` is None), returns
+    ``rms_norm(xout, weight)`` (engine/kernels/add_rmsnorm.py:65-76)."""
+    _mat(x, "x")
+    _mat(y, "y")
+    M, K = x.shape
+    _need(y.shape == x.shape and y.stride(0) == x.stride(0), "x/y shapes")
+    _need(weight.dtype == BF16 and weight.is_contiguous() and weight.numel() == K, "weight")
+    xout = x if xout is None else xout
+    _need(xout.shape == x.shape and xout.stride(0) == x.stride(0), "xout shape")
+    if out is None:
+        out = torch.empty_like(x)
+    _need(out.shape == x.shape and out.stride(0) == x.stride(0), "out shape")
+    _device_guard(x)
+    check(lib().sk_add_rmsnorm_bf16(x.data_ptr(), y.data_ptr(), weight.data_ptr(), float(eps), xout.data_ptr(),
+                                    out.data_ptr(), M, K, x.stride(0), _stream(x)), "sk_add_rmsnorm_bf16")
+    return out
+
+
+def swiglu(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gu[:, :I]) * gu[:, I:]`` with both bf16 roundings (engine/kernels/swiglu.py:27-33)."""
+    _mat(gu, "gu")
+    M, two_i = gu.shape
+    _need(two_i % 2 == 0, "gu must hold [gate | up]")
+    I = two_i // 2
+    if out is None:
+        out = torch.empty((M, I), dtype=BF16, device=gu.device)
+    _device_guard(gu)
+    check(lib().sk_swiglu_bf16(gu.data_ptr(), gu.stride(0), out.data_ptr(), out.stride(0), M, I, _stream(gu)),
+          "sk_swiglu_bf16")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Reference-shaped classes: fixed (M, N, K) and config per instance.
+# ---------------------------------------------------------------------------
+
+class _Planned:
+    op = SK_OP_GEMM
+
+    def __init__(self, M: int, N: int, K: int, device, config: SkConfig | None = None, **cfg_kw):
+        self.M, self.N, self.K = M, N, K
+        self.device = torch.device(device)
+        self.config = _config(config, cfg_kw)
+        if self.config is not None:
+            st = _lib.check_config(self.op, M, N, K, self.config)
+            if st != _lib.SK_OK:
+                raise _lib.SkError(st, f"config {self.config} for op {self.op} at M={M} N={N} K={K}")
+        self.ws = _workspace(self.op, M, N, K, self.config, self.device) if M > 0 else None
+        self._h = None   # normed activation buffer of the norm prologue
+
+    def _normed(self, a: torch.Tensor, norm) -> torch.Tensor:
+        y, wn, xout, eps = norm
+        if self._h is None or self._h.shape != a.shape:
+            self._h = torch.empty_like(a)
+        return add_rms_norm(a, y, wn, eps, xout, out=self._h)
+
+
+class SkinnyMatmul(_Planned):
+    """``C[M, N] = A[M, K] @ W[N, K]^T`` (engine/kernels/gemm.py:349-378).
+
+    ``norm=(y, w_norm, xout, eps)`` runs ``xout = a + y; a = rms_norm(xout, w_norm)``
+    in front, like the reference's fused prologue (gemm.py:363-366)."""
+
+    op = SK_OP_GEMM
+
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, norm=None) -> torch.Tensor:
+        if norm is not None:
+            a = self._normed(a, norm)
+        return gemm(a, w, config=self.config, ws=self.ws)
+
+
+class SkinnyGateUp(_Planned):
+    """``swiglu(a @ wg.T, a @ wu.T)`` in one pass over both weight halves
+    (engine/kernels/gemm.py:315-346)."""
+
+    op = SK_OP_GATEUP
+
+    def __call__(self, a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, norm=None) -> torch.Tensor:
+        if norm is not None:
+            a = self._normed(a, norm)
+        return gateup_swiglu(a, wg, wu, config=self.config, ws=self.ws)
+
+
+class Gemv(_Planned):
+    """VALU GEMV for M <= 8 rows, optionally the SwiGLU pair (engine/kernels/gemm.py:259-292).
+
+    Config fields are those of the GEMV path: ``rows`` weight rows per tile
+    (2, 4, 8), ``ku`` 512-column units per wave, ``waves`` per workgroup."""
+
+    def __init__(self, M: int, N: int, K: int, device, gateup: bool = False, config: SkConfig | None = None,
+                 **cfg_kw):
+        if M > 8:
+            raise ValueError("Gemv handles at most 8 rows")
+        self.op = SK_OP_GATEUP if gateup else SK_OP_GEMM
+        self.gateup = gateup
+        if config is None and not cfg_kw:
+            cfg_kw = dict(path=SK_PATH_GEMV, waves=1, ku=(K + 511) // 512, rows=4)
+        elif cfg_kw:
+            cfg_kw.setdefault("path", SK_PATH_GEMV)
+        super().__init__(M, N, K, device, config, **cfg_kw)
+
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, w2: torch.Tensor | None = None, norm=None) -> torch.Tensor:
+        if norm is not None:
+            a = self._normed(a, norm)
+        if self.gateup:
+            return gateup_swiglu(a, w, w2, config=self.config, ws=self.ws)
+        return gemm(a, w, config=self.config, ws=self.ws)
+
+
+class LmArgmax(_Planned):
+    """lm_head projection fused with the greedy argmax: ``(ids, maxv)``."""
+
+    op = SK_OP_LM_ARGMAX
+
+    def __call__(self, a: torch.Tensor, w: torch.Tensor, norm=None):
+        if norm is not None:
+            a = self._normed(a, norm)
+        return lm_argmax(a, w, config=self.config, ws=self.ws)
+
+
+# ---------------------------------------------------------------------------
+# Pickers: the reference times candidates at warmup (gemm.py:477-660); here
+# the configuration comes from the library's offline-tuned table, so a picker
+# only binds shapes.  The signatures are the reference's; ``log`` receives one
+# line naming the chosen config, ``ws`` (the rotation list) is accepted and
+# unused.
+# ---------------------------------------------------------------------------
+
+def _log_choice(log, what: str, op: int, M: int, N: int, K: int) -> None:
+    if log:
+        log(f"{what} M={M} N={N} K={K}: {_lib.default_config(op, M, N, K).as_dict()}")
+
+
+def pick_matmul(a: torch.Tensor, w: torch.Tensor, log=None, ws: list | None = None):
+    """``f(a, w) -> a @ w.T`` for this exact shape (engine/kernels/gemm.py:516-558)."""
+    M, K = a.shape
+    N = w.shape[0]
+    mm = SkinnyMatmul(M, N, K, a.device)
+    _log_choice(log, "matmul", SK_OP_GEMM, M, N, K)
+    return lambda a, w: mm(a, w)
+
+
+def pick_gateup(a: torch.Tensor, wgu: torch.Tensor, log=None, ws: list | None = None):
+    """``f(a, wgu) -> swiglu(a @ wgu.T)`` (engine/kernels/gemm.py:561-599)."""
+    M, K = a.shape
+    I = wgu.shape[0] // 2
+    mm = SkinnyGateUp(M, I, K, a.device)
+    _log_choice(log, "gateup", SK_OP_GATEUP, M, I, K)
+    return lambda a, wgu: mm(a, wgu[:I], wgu[I:])
+
+
+def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, w: torch.Tensor, eps: float,
+                log=None, ws: list | None = None):
+    """``f(x, y, w_norm, xout, w) -> proj(rms_norm(x + y))`` that also writes
+    ``xout = x + y`` (engine/kernels/gemm.py:602-660).  ``kind``: "matmul" or "gateup"."""
+    M, K = x.shape
+    if kind == "matmul":
+        mm = SkinnyMatmul(M, w.shape[0], K, x.device)
+        _log_choice(log, "normed matmul", SK_OP_GEMM, M, w.shape[0], K)
+        return lambda x, y, w_norm, xout, w: mm(x, w, norm=(y, w_norm, xout, eps))
+    if kind == "gateup":
+        I = w.shape[0] // 2
+        mm = SkinnyGateUp(M, I, K, x.device)
+        _log_choice(log, "normed gateup", SK_OP_GATEUP, M, I, K)
+        return lambda x, y, w_norm, xout, w: mm(x, w[:I], w[I:], norm=(y, w_norm, xout, eps))
+    raise ValueError(f"unknown kind {kind!r}")
+
+
+def pick_lm_argmax(x: torch.Tensor, w: torch.Tensor, eps: float, log=None):
+    """``f(x, y, w_norm, xout, w) -> (ids, maxv)``: the normed lm_head with the
+    greedy argmax fused in (replaces ``mm["lm"](...).argmax(-1)``)."""
+    M, K = x.shape
+    mm = LmArgmax(M, w.shape[0], K, x.device)
+    _log_choice(log, "normed lm_argmax", SK_OP_LM_ARGMAX, M, w.shape[0], K)
+    return lambda x, y, w_norm, xout, w: mm(x, w, norm=(y, w_norm, xout, eps))

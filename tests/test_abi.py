@@ -1,0 +1,139 @@
+"""The C ABI on the CPU: the library loads, exports what the header declares,
+and its host logic (planner, workspace sizes, argument validation) behaves.
+
+No kernel runs here.  Calls with invalid arguments return their status code
+before touching the HIP runtime; the one call that gets past validation
+without a GPU must report SK_ERR_DEVICE (fail loudly, no fallback).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from starter_amd import _lib
+from starter_amd._lib import (SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_DEVICE, SK_ERR_NULL, SK_ERR_SHAPE, SK_ERR_WORKSPACE,
+                              SK_OK, SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_PATH_GEMV,
+                              SK_PATH_MFMA, SkConfig)
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "starter_amd.h"
+QWEN = {"qkv": (SK_OP_GEMM, 6144, 2560), "o": (SK_OP_GEMM, 2560, 4096), "gu": (SK_OP_GATEUP, 9728, 2560),
+        "d": (SK_OP_GEMM, 2560, 9728), "lm": (SK_OP_GEMM, 151936, 2560), "lm_argmax": (SK_OP_LM_ARGMAX, 151936, 2560)}
+FAKE = 0x10000   # an aligned address that is never dereferenced on the host
+
+
+def _declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(sk_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = _declared()
+    assert set(names) == set(_lib.EXPORTS)
+    for n in names:
+        assert isinstance(getattr(lib, n), ctypes._CFuncPtr), n
+
+
+def test_version_and_status_strings():
+    lib = _lib.lib()
+    assert lib.sk_version() >= 1
+    msgs = {lib.sk_strerror(c).decode() for c in range(9)}
+    assert len(msgs) == 9 and "ok" in msgs
+    assert lib.sk_strerror(99).decode() == "unknown status"
+
+
+@pytest.mark.parametrize("name", list(QWEN))
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 40, 64, 96, 128])
+def test_default_config_is_valid_for_every_decode_shape(name, M):
+    op, N, K = QWEN[name]
+    if op == SK_OP_LM_ARGMAX and M > 64:
+        pytest.skip("lm_argmax takes at most 64 rows per call")
+    cfg = _lib.default_config(op, M, N, K)
+    assert _lib.check_config(op, M, N, K, cfg) == SK_OK, cfg
+    # The wave count covers the K slice and the workspace exists only where needed.
+    units = K // 32
+    assert cfg.waves * cfg.ku * cfg.split >= units
+    ws = _lib.workspace_bytes(op, M, N, K, cfg)
+    if op == SK_OP_LM_ARGMAX:
+        assert ws >= 8 * min(M, 64)
+    elif cfg.split == 1:
+        assert ws == 0
+    else:
+        assert ws == (2 if op == SK_OP_GATEUP else 1) * cfg.split * min(M, 64) * N * 4
+
+
+def test_default_config_prefers_no_global_split_at_decode_m():
+    for name in ("qkv", "gu", "lm_argmax"):
+        op, N, K = QWEN[name]
+        for M in (1, 8):
+            assert _lib.default_config(op, M, N, K).split == 1, (name, M)
+
+
+@pytest.mark.parametrize("cfg,op,M,N,K,expect", [
+    (SkConfig.make(SK_PATH_MFMA, 0, 20, 16), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),     # no waves
+    (SkConfig.make(SK_PATH_MFMA, 4, 20, 24), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),     # rows
+    (SkConfig.make(SK_PATH_MFMA, 4, 10, 16), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),     # K not covered
+    (SkConfig.make(SK_PATH_MFMA, 4, 21, 16), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),     # no KU instance
+    (SkConfig.make(SK_PATH_MFMA, 16, 20, 16), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),    # registers
+    (SkConfig.make(SK_PATH_MFMA, 2, 20, 16, 2), SK_OP_LM_ARGMAX, 8, 151936, 2560, SK_ERR_CONFIG),  # split argmax
+    (SkConfig.make(SK_PATH_MFMA, 4, 20, 32), SK_OP_GATEUP, 8, 9728, 2560, SK_ERR_CONFIG),   # gate/up rows
+    (SkConfig.make(SK_PATH_GEMV, 1, 5, 4), SK_OP_GEMM, 16, 6144, 2560, SK_ERR_CONFIG),      # GEMV M > 8
+    (SkConfig.make(9, 4, 20, 16), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),                # path
+    (SkConfig.make(SK_PATH_MFMA, 4, 20, 16), SK_OP_GEMM, 8, 6144, 2568, SK_ERR_SHAPE),      # K % 32
+    (SkConfig.make(SK_PATH_MFMA, 4, 20, 16, 1, 3), SK_OP_GEMM, 8, 6144, 2560, SK_OK),       # explicit grid
+    (SkConfig.make(SK_PATH_MFMA, 4, 10, 16, 2, 3), SK_OP_GEMM, 8, 6144, 2560, SK_ERR_CONFIG),  # grid % split
+    (SkConfig.make(SK_PATH_GEMV, 2, 3, 2), SK_OP_GATEUP, 4, 9728, 2560, SK_OK),
+    (SkConfig.make(SK_PATH_MFMA, 16, 5, 16), SK_OP_GATEUP, 64, 9728, 2560, SK_ERR_CONFIG),  # LDS > 160 KiB
+])
+def test_check_config(cfg, op, M, N, K, expect):
+    assert _lib.check_config(op, M, N, K, cfg) == expect
+
+
+def _gemm(lib, A=FAKE, lda=2560, W=FAKE, ldw=2560, C=FAKE, ldc=6144, M=8, N=6144, K=2560, cfg=None, ws=None,
+          wsb=0):
+    return lib.sk_gemm_bf16(A, lda, W, ldw, C, ldc, M, N, K, _lib.cfg_ptr(cfg), ws, wsb, None)
+
+
+def test_argument_validation_precedes_any_device_work():
+    lib = _lib.lib()
+    assert _gemm(lib, A=None) == SK_ERR_NULL
+    assert _gemm(lib, C=None) == SK_ERR_NULL
+    assert _gemm(lib, A=FAKE + 2) == SK_ERR_ALIGN
+    assert _gemm(lib, lda=2564) == SK_ERR_ALIGN
+    assert _gemm(lib, K=2568, lda=2568, ldw=2568) == SK_ERR_SHAPE
+    assert _gemm(lib, ldc=100) == SK_ERR_SHAPE
+    assert _gemm(lib, M=-1) == SK_ERR_SHAPE
+    assert _gemm(lib, M=0) == SK_OK               # empty batch: nothing enqueued
+    split = SkConfig.make(SK_PATH_MFMA, 4, 10, 16, 2)
+    assert _gemm(lib, cfg=split) == SK_ERR_WORKSPACE
+    assert _gemm(lib, cfg=split, ws=FAKE, wsb=16) == SK_ERR_WORKSPACE
+    assert _gemm(lib, cfg=SkConfig.make(SK_PATH_MFMA, 4, 10, 16)) == SK_ERR_CONFIG
+    assert lib.sk_lm_argmax_bf16(FAKE, 2560, FAKE, 2560, FAKE, FAKE, 8, 151936, 2560, None, None, 0, None) \
+        == SK_ERR_WORKSPACE
+    assert lib.sk_argmax_bf16(FAKE, 151936, 4, 151936, FAKE, FAKE, None, 0, None) == SK_ERR_WORKSPACE
+    assert lib.sk_argmax_bf16(FAKE, 151937, 4, 151936, FAKE, FAKE, FAKE, 1 << 20, None) == SK_ERR_ALIGN
+    X, Y, XO, OUT = FAKE, FAKE + (1 << 20), FAKE + (2 << 20), FAKE + (3 << 20)
+    rms = lambda x, y, xo, out: lib.sk_add_rmsnorm_bf16(x, y, FAKE, 1e-6, xo, out, 4, 2560, 2560, None)
+    assert rms(X, Y, X + 64, OUT) == 8            # SK_ERR_ALIAS: xout partially overlaps x
+    assert rms(X, Y, XO, XO + 16) == 8            # out overlaps xout
+    assert rms(X, Y, XO, Y) == 8                  # out overlaps y
+    assert lib.sk_swiglu_bf16(FAKE, 100, FAKE, 50, 2, 60, None) == SK_ERR_SHAPE
+
+
+def test_workspace_bytes():
+    assert _lib.workspace_bytes(SK_OP_ARGMAX, 4, 151936, 0) == 4 * ((151936 + 4095) // 4096) * 8
+    assert _lib.workspace_bytes(SK_OP_GEMM, 0, 6144, 2560) == 0
+    cfg = SkConfig.make(SK_PATH_MFMA, 4, 10, 16, 2)
+    assert _lib.workspace_bytes(SK_OP_GEMM, 8, 6144, 2560, cfg) == 2 * 8 * 6144 * 4
+    assert _lib.workspace_bytes(SK_OP_GATEUP, 8, 9728, 2560, cfg) == 2 * 2 * 8 * 9728 * 4
+
+
+def test_valid_call_without_gpu_fails_loudly():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; the GPU tests exercise this path")
+    assert _gemm(_lib.lib()) == SK_ERR_DEVICE

@@ -1,0 +1,293 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Every oracle function is checked against (a) torch's CPU library routine for
+the same reference function, (b) a closed form or exact special case that the
+mathematics fixes, and (c) the committed golden fixtures.  The
+``test_pins_reject_planted_mistakes`` cases feed deliberately broken oracles
+(dropped term, transposed operand, wrong cast order, wrong tie rule) through
+the same checks and require each to be caught.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from tests._util import BF16, assert_parity, bits, from_bits, randn_bf16, rel_violations
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _golden(name: str):
+    return np.load(GOLDEN / f"{name}.npz", allow_pickle=False)
+
+
+# --------------------------------------------------------------------------
+# checks shared by the real oracle and the planted-mistake variants
+# --------------------------------------------------------------------------
+
+def _check_gemm_vs_torch(gemm_fn, M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = randn_bf16((M, K), 1.0, g)
+    w = randn_bf16((N, K), 0.02, g)
+    out = from_bits(gemm_fn(bits(x), bits(w)))
+    ref = F.linear(x, w)
+    bad, _ = rel_violations(out, ref)
+    return bad == 0 and (out != ref).float().mean().item() < 0.01
+
+
+def _check_gemm_exact_integers(gemm_fn):
+    """Small integers: every product and partial sum is exact in fp32, so the
+    only correct answer is the exact one.  M != N pins operand orientation."""
+    rng = np.random.default_rng(7)
+    M, N, K = 5, 11, 96
+    a = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    w = rng.integers(-3, 4, size=(N, K)).astype(np.float32)
+    exact = a @ w.T
+    out = oracle.bf16_to_f32(gemm_fn(oracle.f32_to_bf16(a), oracle.f32_to_bf16(w)))
+    return np.array_equal(out, oracle.bf16_to_f32(oracle.f32_to_bf16(exact)))
+
+
+def _check_swiglu(swiglu_fn):
+    g = torch.Generator().manual_seed(3)
+    gu = randn_bf16((4, 2 * 700), 3.0, g)
+    ref = F.silu(gu[:, :700]) * gu[:, 700:]
+    return torch.equal(from_bits(swiglu_fn(bits(gu))), ref)
+
+
+def _check_argmax(argmax_fn):
+    d = _golden("argmax_m7_v1000")
+    ids, maxv = argmax_fn(d["logits"])
+    return np.array_equal(ids, d["ids"]) and np.array_equal(maxv, d["maxv"], equal_nan=True)
+
+
+# --------------------------------------------------------------------------
+# GEMM
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(1, 6144, 2560), (8, 6144, 2560), (8, 2560, 4096), (4, 2560, 9728),
+                                   (16, 777, 2560), (40, 512, 2560), (64, 256, 2560), (3, 40, 96)])
+def test_oracle_gemm_matches_torch_linear(M, N, K):
+    assert _check_gemm_vs_torch(oracle.gemm, M, N, K, seed=M * 1000 + N)
+
+
+def test_oracle_gemm_exact_integer_products():
+    assert _check_gemm_exact_integers(oracle.gemm)
+
+
+def test_oracle_gemm_one_hot_weights_gather_columns():
+    """W row n = e_{p(n)}: C[:, n] must be A[:, p(n)] bit for bit."""
+    g = torch.Generator().manual_seed(11)
+    M, K, N = 6, 2560, 300
+    x = randn_bf16((M, K), 1.0, g)
+    perm = torch.randperm(K, generator=g)[:N]
+    w = torch.zeros(N, K, dtype=BF16)
+    w[torch.arange(N), perm] = 1.0
+    out = from_bits(oracle.gemm(bits(x), bits(w)))
+    assert torch.equal(out, x[:, perm])
+
+
+def test_oracle_gemm_f32_close_to_fp64():
+    """The fp32 sums stay within the fp32 accumulation bound K*u*sum|a*w| of fp64."""
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 8, 1024, 9728
+    x = randn_bf16((M, K), 1.0, g)
+    w = randn_bf16((N, K), 0.02, g)
+    f32 = torch.from_numpy(oracle.gemm_f32(bits(x), bits(w))).double()
+    exact = x.double() @ w.double().T
+    bound = K * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T)
+    assert bool(((f32 - exact).abs() <= bound).all())
+    # The bf16 result is the rounding of the fp32 sum.
+    out = oracle.gemm(bits(x), bits(w))
+    assert np.array_equal(out, oracle.f32_to_bf16(f32.float().numpy()))
+
+
+@pytest.mark.parametrize("name", ["gemm_m3_n40_k96", "gemm_m1_n48_k2560", "gemm_m19_n33_k256"])
+def test_oracle_gemm_golden(name):
+    d = _golden(name)
+    out = from_bits(oracle.gemm(d["x"], d["w"]))
+    assert_parity(out, from_bits(d["y"]), name)
+
+
+# --------------------------------------------------------------------------
+# SwiGLU and gate/up
+# --------------------------------------------------------------------------
+
+def test_oracle_swiglu_bitexact_vs_torch():
+    assert _check_swiglu(oracle.swiglu)
+
+
+def test_oracle_swiglu_every_bf16_gate_value():
+    """All 65536 bf16 gate values against F.silu(g) * u (torch CPU)."""
+    gvals = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(BF16)
+    finite = torch.isfinite(gvals.float())
+    gvals = gvals[finite]
+    u = torch.full_like(gvals, 1.5)
+    gu = torch.stack([gvals, u]).T.contiguous().view(-1, 2)   # M rows of [g | u] with I = 1
+    out = from_bits(oracle.swiglu(bits(gu)))[:, 0]
+    ref = F.silu(gvals) * u
+    assert torch.equal(out, ref)
+
+
+def test_oracle_swiglu_golden():
+    d = _golden("swiglu_m3_i512")
+    assert np.array_equal(oracle.swiglu(d["gu"]), d["y"])
+
+
+@pytest.mark.parametrize("M,I,K", [(1, 9728, 2560), (8, 2048, 2560), (16, 512, 2560), (3, 24, 256)])
+def test_oracle_gateup_matches_torch(M, I, K):
+    g = torch.Generator().manual_seed(M + I)
+    x = randn_bf16((M, K), 1.0, g)
+    wgu = randn_bf16((2 * I, K), 0.02, g)
+    out = from_bits(oracle.gateup_swiglu(bits(x), bits(wgu[:I]), bits(wgu[I:])))
+    ref = F.silu(F.linear(x, wgu[:I])) * F.linear(x, wgu[I:])
+    # F.linear's own summation order differs from the oracle's; the epilogue
+    # then amplifies a 1-ulp difference of g or u by at most one more rounding.
+    assert_parity(out, ref, f"gateup M={M}")
+    # Same arithmetic composed from the oracle's own pieces is bit-exact.
+    g32 = oracle.gemm(bits(x), bits(wgu[:I]))
+    u32 = oracle.gemm(bits(x), bits(wgu[I:]))
+    assert np.array_equal(out.view(torch.int16).numpy().view(np.uint16),
+                          oracle.swiglu(np.concatenate([g32, u32], axis=1)))
+
+
+def test_oracle_gateup_golden():
+    d = _golden("gateup_m2_i24_k256")
+    I = d["wgu"].shape[0] // 2
+    out = from_bits(oracle.gateup_swiglu(d["x"], d["wgu"][:I], d["wgu"][I:]))
+    assert_parity(out, from_bits(d["y"]), "gateup golden")
+
+
+# --------------------------------------------------------------------------
+# Residual add + RMSNorm
+# --------------------------------------------------------------------------
+
+def _ref_rmsnorm(x, w, eps):
+    h = x.float()
+    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+    return w * h.to(x.dtype)
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (9, 2560), (5, 4096), (3, 128)])
+def test_oracle_add_rmsnorm_matches_closed_form(M, K):
+    g = torch.Generator().manual_seed(M * K)
+    x = randn_bf16((M, K), 1.0, g)
+    y = randn_bf16((M, K), 1.0, g)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    xout, out = oracle.add_rmsnorm(bits(x), bits(y), bits(w), 1e-6)
+    assert torch.equal(from_bits(xout), x + y)          # bit-exact residual stream
+    ref = _ref_rmsnorm(x + y, w, 1e-6)
+    o = from_bits(out)
+    # rstd can differ from torch's by the fp32 summation order of sum(s^2):
+    # then bf16(s * r) moves by one ulp and the weight product by at most two.
+    diff = (o.float() - ref.float()).abs()
+    two_ulp = ref.float().abs() * 2.0 ** -6 + 1e-30
+    assert bool((diff <= two_ulp).all())
+    assert (o != ref).float().mean().item() < 1e-3
+
+
+def test_oracle_add_rmsnorm_golden():
+    d = _golden("add_rmsnorm_m4_k2560")
+    xout, out = oracle.add_rmsnorm(d["x"], d["y"], d["w"], float(d["eps"]))
+    assert np.array_equal(xout, d["xout"])
+    assert (out != d["out"]).mean() < 1e-3
+
+
+# --------------------------------------------------------------------------
+# Argmax and lm_head + argmax
+# --------------------------------------------------------------------------
+
+def test_oracle_argmax_golden_ties_nan_signed_zero():
+    assert _check_argmax(oracle.argmax)
+
+
+@pytest.mark.parametrize("M,V", [(3, 151936), (64, 1024), (5, 1)])
+def test_oracle_argmax_matches_torch(M, V):
+    g = torch.Generator().manual_seed(V)
+    L = (torch.randn(M, V, generator=g) * 4).to(BF16)
+    if V > 300:
+        L[0, 7] = L[0].max() + 1
+        L[1, 100] = L[1, 200] = L[1].max() + 2
+    ids, maxv = oracle.argmax(bits(L))
+    assert np.array_equal(ids, torch.argmax(L, -1).numpy())
+    assert np.array_equal(maxv, L.max(-1).values.float().numpy())
+
+
+def test_oracle_lm_argmax_golden_and_consistency():
+    d = _golden("lm_argmax_m4_v777_k128")
+    ids, maxv = oracle.lm_argmax(d["x"], d["w"])
+    # Against torch's logits: wherever the bf16 top-2 differ, the pick must agree.
+    L = from_bits(d["logits"]).float()
+    top2 = torch.topk(L, 2, dim=-1).values
+    for m in range(L.shape[0]):
+        if top2[m, 0] - top2[m, 1] > 1e-2:
+            assert ids[m] == d["ids"][m]
+    # Against the oracle's own gemm + argmax: identical arithmetic, identical answer.
+    gi, gv = oracle.argmax(oracle.gemm(d["x"], d["w"]))
+    assert np.array_equal(ids, gi) and np.array_equal(maxv, gv)
+
+
+def test_f32_to_bf16_rounding_matches_torch():
+    vals = np.array([1.0, 1.00390625, 1.01171875, 1.0039062, 1.0039063, -2.5, 3.4028235e38, 3.39e38,
+                     1e-40, -1e-45, 0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, 1.9921875, 0.1],
+                    dtype=np.float32)
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([vals, rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 20000)])
+    ref = torch.from_numpy(vals).to(BF16).view(torch.int16).numpy().view(np.uint16)
+    # NaN payloads are not part of the contract (torch's own scalar and
+    # vectorised conversions disagree on them): compare NaN-ness only there.
+    nan = np.isnan(vals)
+    out = oracle.f32_to_bf16(vals)
+    assert np.array_equal(out[~nan], ref[~nan])
+    assert bool(np.isnan(oracle.bf16_to_f32(out[nan])).all())
+    assert all(oracle.f32_to_bf16_c(float(v)) == int(r) for v, r, n in zip(vals[:200], ref[:200], nan[:200]) if not n)
+
+
+# --------------------------------------------------------------------------
+# The pins catch plausible mistakes (planted in CPU-side variants)
+# --------------------------------------------------------------------------
+
+def _dropped_tail(a, w):
+    return oracle.gemm(np.ascontiguousarray(a[:, :-32]), np.ascontiguousarray(w[:, :-32]))
+
+
+def _transposed(a, w):
+    # Interprets W as [K, N] (column-major weight): rows become columns.
+    K = a.shape[1]
+    wt = np.ascontiguousarray(w.reshape(-1)[: w.size].reshape(K, -1).T) if w.shape[0] != K else w.T.copy()
+    return oracle.gemm(a, np.ascontiguousarray(wt[: w.shape[0]]))
+
+
+def _sign_flip(a, w):
+    return oracle.gemm(a, w ^ np.uint16(0x8000))
+
+
+def _swiglu_one_rounding(gu):
+    # silu product rounded once instead of twice (a wrong cast placement).
+    f = oracle.bf16_to_f32(gu)
+    I = f.shape[1] // 2
+    g, u = f[:, :I], f[:, I:]
+    return oracle.f32_to_bf16((g / (1 + np.exp(-g))) * u)
+
+
+def _argmax_last_tie(L):
+    f = oracle.bf16_to_f32(L)
+    ids = f.shape[1] - 1 - np.argmax(f[:, ::-1], axis=1)
+    return ids.astype(np.int64), np.nanmax(f, axis=1).astype(np.float32)
+
+
+@pytest.mark.parametrize("variant", ["dropped_tail", "transposed", "sign_flip"])
+def test_pins_reject_planted_gemm_mistakes(variant):
+    fn = {"dropped_tail": _dropped_tail, "transposed": _transposed, "sign_flip": _sign_flip}[variant]
+    caught = (not _check_gemm_exact_integers(fn)) or (not _check_gemm_vs_torch(fn, 8, 96, 96, seed=1))
+    assert caught
+
+
+def test_pins_reject_planted_swiglu_and_argmax_mistakes():
+    assert not _check_swiglu(_swiglu_one_rounding)
+    assert not _check_argmax(_argmax_last_tie)
