@@ -17,7 +17,8 @@
  * the end, as torch F.linear / the reference's tl.dot + `.to(bf16)` path.
  *
  * Alignment: A, W (and Wg/Wu) must be 16-byte aligned and lda/ldw multiples
- * of 8 elements; K must be a multiple of 32.  M may be 0 (nothing is enqueued).
+ * of 8 elements; K must be a multiple of 32.  M may be 0: nothing is enqueued
+ * and the data pointers may then be NULL.
  *
  * Workspace: ops that need device scratch take (ws, ws_bytes); query the size
  * with sk_workspace_bytes() for the same op/shape/config and allocate it once
@@ -135,8 +136,9 @@ int sk_lm_argmax_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t l
                       int64_t* ids, float* maxv, int M, int V, int K,
                       const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
 
-/* Argmax over materialised bf16 logits L[M,V] (row stride ld), same tie and
- * NaN rules as sk_lm_argmax_bf16.  Replaces `logits.argmax(dim=-1)`
+/* Argmax over materialised bf16 logits L[M,V] (row stride ld, any alignment;
+ * 16-byte aligned rows are read with vector loads), same tie and NaN rules as
+ * sk_lm_argmax_bf16.  Replaces `logits.argmax(dim=-1)`
  * (engine/engine.py:207) and fast_topk rank 0 (engine/kernels/topk.py:17-37).
  * Needs a workspace (sk_workspace_bytes(SK_OP_ARGMAX, M, V, 0, NULL)). */
 int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, float* maxv,

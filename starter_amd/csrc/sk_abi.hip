@@ -283,11 +283,11 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, co
                     sk_bf16* C, int64_t ldc, int64_t* ids, float* maxv, int M, int N, int K, const sk_config* cfg,
                     void* ws, size_t ws_bytes, hipStream_t stream) {
   if (M < 0 || N < 1 || K < 32) return SK_ERR_SHAPE;
+  if (M == 0) return SK_OK;   // empty batch: nothing to read or write (pointers may be NULL)
   if (!A || !W0 || (op == SK_OP_GATEUP && !W1)) return SK_ERR_NULL;
   if (op == SK_OP_LM_ARGMAX ? (!ids || !maxv) : !C) return SK_ERR_NULL;
   if ((K & 31) != 0 || lda < K || ldw < K || (op != SK_OP_LM_ARGMAX && ldc < N)) return SK_ERR_SHAPE;
   if (!aligned16(A) || !aligned16(W0) || (W1 && !aligned16(W1)) || (lda & 7) || (ldw & 7)) return SK_ERR_ALIGN;
-  if (M == 0) return SK_OK;
   // Validate every chunk's plan before enqueuing anything.
   Plan plans[2];
   int chunk_rows[2] = {M < kMaxM ? M : kMaxM, M % kMaxM};
@@ -423,9 +423,8 @@ int sk_lm_argmax_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t l
 int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, float* maxv, void* ws, size_t ws_bytes,
                    hipStream_t stream) {
   if (M < 0 || V < 1 || ld < V) return SK_ERR_SHAPE;
-  if (!L || !ids || !maxv) return SK_ERR_NULL;
-  if (!aligned16(L) || (ld & 7)) return SK_ERR_ALIGN;
   if (M == 0) return SK_OK;
+  if (!L || !ids || !maxv) return SK_ERR_NULL;
   if (M > 65535) return SK_ERR_SHAPE;
   const int chunks = cdiv(V, kArgmaxChunk);
   const size_t need = (size_t)chunks * M * sizeof(unsigned long long);
@@ -434,7 +433,8 @@ int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, flo
   int st = device_info(&num_cu);
   if (st) return st;
   unsigned long long* best = static_cast<unsigned long long*>(ws);
-  sk::argmax_partial_kernel<<<dim3(chunks, M), dim3(256), 0, stream>>>(L, ld, M, V, kArgmaxChunk, best);
+  const int vec = (aligned16(L) && (ld & 7) == 0) ? 1 : 0;
+  sk::argmax_partial_kernel<<<dim3(chunks, M), dim3(256), 0, stream>>>(L, ld, M, V, kArgmaxChunk, vec, best);
   if ((st = launch_status())) return st;
   sk::argmax_final_kernel<<<dim3(M), dim3(256), 0, stream>>>(best, chunks, M, ids, maxv);
   return launch_status();
@@ -443,10 +443,10 @@ int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, flo
 int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, float eps, sk_bf16* xout, sk_bf16* out,
                         int M, int K, int64_t ld, hipStream_t stream) {
   if (M < 0 || K < 8 || (K & 7) || K > sk::RMS_THREADS * 8 * sk::RMS_MAX_CHUNKS || ld < K) return SK_ERR_SHAPE;
+  if (M == 0) return SK_OK;
   if (!x || !y || !w || !xout || !out) return SK_ERR_NULL;
   if (!aligned16(x) || !aligned16(y) || !aligned16(w) || !aligned16(xout) || !aligned16(out) || (ld & 7))
     return SK_ERR_ALIGN;
-  if (M == 0) return SK_OK;
   if (M > 65535) return SK_ERR_SHAPE;
   // xout may be x or y itself (each element is read before the same thread
   // writes it), but must not partially overlap them; out overlaps nothing.
@@ -463,8 +463,8 @@ int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, fl
 
 int sk_swiglu_bf16(const sk_bf16* gu, int64_t ld_gu, sk_bf16* out, int64_t ld_out, int M, int I, hipStream_t stream) {
   if (M < 0 || I < 1 || ld_gu < 2 * (int64_t)I || ld_out < I) return SK_ERR_SHAPE;
-  if (!gu || !out) return SK_ERR_NULL;
   if (M == 0) return SK_OK;
+  if (!gu || !out) return SK_ERR_NULL;
   const size_t in_bytes = ((size_t)(M - 1) * ld_gu + 2 * (size_t)I) * sizeof(sk_bf16);
   const size_t out_bytes = ((size_t)(M - 1) * ld_out + I) * sizeof(sk_bf16);
   if (overlaps(out, out_bytes, gu, in_bytes)) return SK_ERR_ALIAS;

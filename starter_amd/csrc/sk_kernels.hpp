@@ -123,11 +123,15 @@ __device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// Eight bf16 products summed into acc with four v_dot2_f32_bf16.  The pairs are
+// taken as .s01/.s23/.. of a bf16x8 view: hipcc 7.2 folds a per-component
+// __builtin_bit_cast(bf16x2, v.y) of a u32x4 back to component 0.
 __device__ __forceinline__ float dot8(u32x4 w, u32x4 a, float acc) {
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.x), __builtin_bit_cast(bf16x2, a.x), acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.y), __builtin_bit_cast(bf16x2, a.y), acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.z), __builtin_bit_cast(bf16x2, a.z), acc, false);
-  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w.w), __builtin_bit_cast(bf16x2, a.w), acc, false);
+  const bf16x8 wb = __builtin_bit_cast(bf16x8, w), ab = __builtin_bit_cast(bf16x8, a);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(wb.s01, ab.s01, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(wb.s23, ab.s23, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(wb.s45, ab.s45, acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(wb.s67, ab.s67, acc, false);
   return acc;
 }
 
@@ -509,14 +513,16 @@ __global__ void __launch_bounds__(256) argmax_final_kernel(const unsigned long l
 
 // Argmax over materialised bf16 logits: workgroup (c, m) scans chunk c of row m.
 __global__ void __launch_bounds__(256) argmax_partial_kernel(const uint16_t* __restrict__ L, int64_t ld, int M, int V,
-                                                             int chunk, unsigned long long* __restrict__ best) {
+                                                             int chunk, int vec, unsigned long long* __restrict__ best) {
   __shared__ unsigned long long red[256];
   const int m = blockIdx.y, c = blockIdx.x;
   const uint16_t* row = L + (int64_t)m * ld;
   const int lo = c * chunk, hi = min(lo + chunk, V);
   unsigned long long b = 0ull;
-  // 8-column vector loads over the aligned body (ld % 8 == 0 and lo % 8 == 0).
-  const int vhi = lo + ((hi - lo) & ~7);
+  // 8-column vector loads over the body when rows are 16-byte aligned
+  // (vec: L aligned and ld % 8 == 0; lo is a multiple of chunk, itself of 8),
+  // scalar loads for the tail and for unaligned layouts.
+  const int vhi = vec ? lo + ((hi - lo) & ~7) : lo;
   for (int k = lo + 8 * threadIdx.x; k < vhi; k += 8 * blockDim.x) {
     const u32x4 v = ld16(row + k);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};

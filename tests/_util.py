@@ -50,3 +50,70 @@ def reference_tolerance_ok(out: torch.Tensor, ref: torch.Tensor) -> bool:
     (tests/test_kernels.py:123, engine/kernels/gemm.py:542-543)."""
     o, r = out.detach().cpu().float(), ref.detach().cpu().float()
     return (o - r).abs().max().item() <= 0.02 * r.abs().max().item() + 1e-3
+
+
+def gateup_violations(out: torch.Tensor, x_bits: np.ndarray, wg_bits: np.ndarray, wu_bits: np.ndarray,
+                      rtol: float = RTOL, tau: float = TAU) -> tuple[int, int, float]:
+    """Parity of a gate/up + SwiGLU output against the oracle.
+
+    The epilogue rounds g and u to bf16 before silu and the product
+    (engine/kernels/gemm.py:115-121), so an fp32 summation-order difference
+    that straddles a bf16 rounding midpoint of g or u legitimately moves the
+    output by up to three bf16 roundings (> 1e-2 relative on rare elements;
+    the reference's own pipeline on two devices does the same).  An element is
+    "midpoint-ambiguous" when the oracle's fp32 g or u lies within
+    delta = 4 * sqrt(K) * 2^-24 * rms(row) of a bf16 rounding midpoint (4x the
+    typical fp32 accumulation noise).  Rule:
+      * every element within rtol * max(|ref|, tau * rms(row)) of the oracle,
+        or ambiguous and within that bound of the epilogue applied to one of
+        the admissible roundings of g and u;
+      * non-ambiguous elements bit-exact (the cast placement is pinned: a
+        one-rounding epilogue is only ~72% exact there).
+    Returns (violations, ambiguous count, bit-exact fraction of the rest)."""
+    import oracle
+
+    K = x_bits.shape[1]
+    g = oracle.gemm_f32(x_bits, wg_bits)
+    u = oracle.gemm_f32(x_bits, wu_bits)
+    ref_bits = oracle.swiglu(np.concatenate([oracle.f32_to_bf16(g), oracle.f32_to_bf16(u)], 1))
+    ref = oracle.bf16_to_f32(ref_bits)
+    o = out.detach().float().cpu().numpy()
+    rms = np.sqrt((ref.astype(np.float64) ** 2).mean(-1, keepdims=True))
+
+    def ok(cand):
+        return np.abs(o - cand) <= rtol * np.maximum(np.abs(cand), tau * rms)
+
+    def alts(v):
+        d = 4.0 * np.sqrt(K) * 2.0 ** -24 * np.sqrt((v.astype(np.float64) ** 2).mean(-1, keepdims=True))
+        return oracle.f32_to_bf16((v - d).astype(np.float32)), oracle.f32_to_bf16((v + d).astype(np.float32))
+
+    g_lo, g_hi = alts(g)
+    u_lo, u_hi = alts(u)
+    amb = (g_lo != g_hi) | (u_lo != u_hi)
+    good = ok(ref)
+    # Over an interval this narrow the epilogue is monotone in g and in u, so
+    # every admissible rounding (the band can span several ulps when |g| or
+    # |u| is far below its row rms) gives an output between the extremes of
+    # the four corner cases.
+    corners = [oracle.bf16_to_f32(oracle.swiglu(np.concatenate([gb, ub], 1)))
+               for gb in (g_lo, g_hi) for ub in (u_lo, u_hi)]
+    lo, hi = np.minimum.reduce(corners), np.maximum.reduce(corners)
+    tol_lo = rtol * np.maximum(np.abs(lo), tau * rms)
+    tol_hi = rtol * np.maximum(np.abs(hi), tau * rms)
+    good |= amb & (o >= lo - tol_lo) & (o <= hi + tol_hi)
+    exact = (bits(out) == ref_bits)[~amb]
+    detail = ""
+    if (~good).any():
+        m, n = (int(i[0]) for i in np.nonzero(~good))
+        detail = (f"first at [{m},{n}]: out {o[m, n]!r} ref {ref[m, n]!r} g32 {g[m, n]!r} u32 {u[m, n]!r} "
+                  f"g bf16 {oracle.bf16_to_f32(g_lo[m:m+1, n])[0]!r}/{oracle.bf16_to_f32(g_hi[m:m+1, n])[0]!r} "
+                  f"u bf16 {oracle.bf16_to_f32(u_lo[m:m+1, n])[0]!r}/{oracle.bf16_to_f32(u_hi[m:m+1, n])[0]!r}")
+    gateup_violations.last_detail = detail
+    return int((~good).sum()), int(amb.sum()), float(exact.mean()) if exact.size else 1.0
+
+
+def assert_gateup_parity(out, x_bits, wg_bits, wu_bits, what: str = "") -> None:
+    bad, amb, exact = gateup_violations(out, x_bits, wg_bits, wu_bits)
+    assert bad == 0, (f"{what}: {bad} elements outside the gate/up parity rule ({amb} midpoint-ambiguous); "
+                      f"{gateup_violations.last_detail}")
+    assert exact >= 0.999, f"{what}: only {exact:.4f} of non-ambiguous elements bit-exact"

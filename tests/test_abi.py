@@ -108,6 +108,7 @@ def test_argument_validation_precedes_any_device_work():
     assert _gemm(lib, ldc=100) == SK_ERR_SHAPE
     assert _gemm(lib, M=-1) == SK_ERR_SHAPE
     assert _gemm(lib, M=0) == SK_OK               # empty batch: nothing enqueued
+    assert _gemm(lib, M=0, A=None, C=None) == SK_OK
     split = SkConfig.make(SK_PATH_MFMA, 4, 10, 16, 2)
     assert _gemm(lib, cfg=split) == SK_ERR_WORKSPACE
     assert _gemm(lib, cfg=split, ws=FAKE, wsb=16) == SK_ERR_WORKSPACE
@@ -115,7 +116,7 @@ def test_argument_validation_precedes_any_device_work():
     assert lib.sk_lm_argmax_bf16(FAKE, 2560, FAKE, 2560, FAKE, FAKE, 8, 151936, 2560, None, None, 0, None) \
         == SK_ERR_WORKSPACE
     assert lib.sk_argmax_bf16(FAKE, 151936, 4, 151936, FAKE, FAKE, None, 0, None) == SK_ERR_WORKSPACE
-    assert lib.sk_argmax_bf16(FAKE, 151937, 4, 151936, FAKE, FAKE, FAKE, 1 << 20, None) == SK_ERR_ALIGN
+    assert lib.sk_argmax_bf16(FAKE, 151935, 4, 151936, FAKE, FAKE, FAKE, 1 << 20, None) == SK_ERR_SHAPE
     X, Y, XO, OUT = FAKE, FAKE + (1 << 20), FAKE + (2 << 20), FAKE + (3 << 20)
     rms = lambda x, y, xo, out: lib.sk_add_rmsnorm_bf16(x, y, FAKE, 1e-6, xo, out, 4, 2560, 2560, None)
     assert rms(X, Y, X + 64, OUT) == 8            # SK_ERR_ALIAS: xout partially overlaps x

@@ -22,7 +22,8 @@ import oracle
 from starter_amd import kernels as K
 from starter_amd._lib import (SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_SHAPE, SK_ERR_WORKSPACE, SK_OP_GATEUP, SK_OP_GEMM,
                               SK_PATH_GEMV, SK_PATH_MFMA, SkConfig, SkError)
-from tests._util import BF16, assert_parity, bits, from_bits, randn_bf16, reference_tolerance_ok
+from tests._util import (BF16, assert_gateup_parity, assert_parity, bits, from_bits, randn_bf16,
+                         reference_tolerance_ok)
 
 pytestmark = pytest.mark.gpu
 
@@ -102,7 +103,7 @@ GEMM_CONFIGS = [
     SkConfig.make(SK_PATH_MFMA, waves=4, ku=20, rows=16),
     SkConfig.make(SK_PATH_MFMA, waves=8, ku=10, rows=16),
     SkConfig.make(SK_PATH_MFMA, waves=16, ku=5, rows=16),
-    SkConfig.make(SK_PATH_MFMA, waves=4, ku=10, rows=32),
+    SkConfig.make(SK_PATH_MFMA, waves=8, ku=10, rows=32),
     SkConfig.make(SK_PATH_MFMA, waves=2, ku=20, rows=16, split=2),
     SkConfig.make(SK_PATH_MFMA, waves=4, ku=5, rows=16, split=4),
     SkConfig.make(SK_PATH_MFMA, waves=4, ku=20, rows=16, grid=64),
@@ -165,8 +166,7 @@ def test_gateup_qwen_default_config(M):
     x = _acts(M, Kd, seed=17)
     wd = _gpu(wgu)
     out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:])
-    ref = from_bits(oracle.gateup_swiglu(bits(x), bits(wgu[:I]), bits(wgu[I:])))
-    assert_parity(out, ref, f"gateup M={M}")
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup M={M}")
 
 
 GATEUP_CONFIGS = [
@@ -186,8 +186,7 @@ def test_gateup_every_config(cfg, M):
     x = _acts(M, Kd, seed=23)
     wd = wgu.to(DEV)
     out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:], config=cfg)
-    ref = from_bits(oracle.gateup_swiglu(bits(x), bits(wgu[:I]), bits(wgu[I:])))
-    assert_parity(out, ref, f"gateup config {cfg}")
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup config {cfg}")
 
 
 def test_gateup_reference_grid_m16():
@@ -199,7 +198,7 @@ def test_gateup_reference_grid_m16():
     out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:])
     ref = F.silu(F.linear(x, wgu[:I])) * F.linear(x, wgu[I:])
     assert reference_tolerance_ok(out, ref)
-    assert_parity(out, ref, "gateup vs torch CPU")
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), "gateup M=16")
 
 
 # ---------------------------------------------------------------------------

@@ -291,3 +291,20 @@ def test_pins_reject_planted_gemm_mistakes(variant):
 def test_pins_reject_planted_swiglu_and_argmax_mistakes():
     assert not _check_swiglu(_swiglu_one_rounding)
     assert not _check_argmax(_argmax_last_tie)
+
+
+def test_gateup_parity_rule_accepts_reference_pipeline_and_rejects_wrong_epilogue():
+    """The gate/up rule used by the GPU tests: torch's own pipeline (another
+    fp32 summation order) passes; a one-rounding epilogue does not."""
+    from tests._util import gateup_violations
+
+    g = torch.Generator().manual_seed(4)
+    x = randn_bf16((4, 2560), 1.0, g)
+    w = randn_bf16((2 * 9728, 2560), 0.02, g)
+    xb, wg, wu = bits(x), bits(w[:9728]), bits(w[9728:])
+    good = F.silu(F.linear(x, w[:9728])) * F.linear(x, w[9728:])
+    bad, _, exact = gateup_violations(good, xb, wg, wu)
+    assert bad == 0 and exact == 1.0
+    wrong = (F.silu(F.linear(x, w[:9728]).float()) * F.linear(x, w[9728:]).float()).to(BF16)
+    _, _, exact = gateup_violations(wrong, xb, wg, wu)
+    assert exact < 0.9
