@@ -21,8 +21,12 @@
  * and the data pointers may then be NULL.
  *
  * Workspace: ops that need device scratch take (ws, ws_bytes); query the size
- * with sk_workspace_bytes() for the same op/shape/config and allocate it once
- * (outside graph capture).  Calls that share one workspace must not overlap.
+ * with sk_workspace_bytes() for the same op/shape/config and allocate it once,
+ * zero-filled (outside graph capture).  Its first bytes hold arrival counters
+ * that let the last workgroup of a tile finish a split-K sum or an argmax in
+ * the same kernel; every call leaves them at zero again, so the workspace is
+ * reused without clearing.  Calls that share one workspace must not overlap
+ * (same stream, or ordered by events).
  */
 #ifndef STARTER_AMD_H
 #define STARTER_AMD_H
@@ -73,8 +77,9 @@ typedef enum sk_path {
  *            their fp32 partials are summed in LDS in fixed wave order
  *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns)
  *   rows   : weight rows per workgroup tile (MFMA: 16 or 32; GEMV: 1..8)
- *   split  : global K splits; >1 writes fp32 partials to the workspace that a
- *            second kernel sums in fixed split order (no atomics)
+ *   split  : global K splits; >1 writes fp32 partials to the workspace and
+ *            the last workgroup to finish a tile sums them in fixed split
+ *            order (no floating-point atomics, no second kernel)
  *   grid   : workgroups to launch (0 = derive from the device's CU count)
  */
 typedef struct sk_config {

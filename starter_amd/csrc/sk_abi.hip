@@ -106,9 +106,28 @@ struct Plan {
   int tm = 0, tn = 0, tku = 0;  // template parameters: MT|MR, NT|R, KU bound
   int nrb = 0;                  // tiles along N
   int slice_units = 0;
-  size_t lds = 0;
+  int out_rows = 0;             // output columns per tile
+  size_t parts_lds = 0;         // double-buffered fp32 partial tiles
+  size_t stage_elem = 0;        // LDS bytes per staged tile (0: argmax keeps 8*M bytes)
+  size_t lds = 0;               // total dynamic LDS (set once the grid is known)
   sk::KernelFn fn = nullptr;
 };
+
+// Staged output bytes per element of each epilogue (see EpiTraits).
+size_t stage_bytes(int epi) {
+  switch (epi) {
+    case sk::EPI_STORE: case sk::EPI_SWIGLU: return 2;
+    case sk::EPI_PART: return 4;
+    case sk::EPI_PART_GU: return 8;
+  }
+  return 0;
+}
+
+// Dynamic LDS of a plan whose workgroups each own at most tiles_per tiles.
+size_t plan_lds(const Plan& pl, int M, int tiles_per) {
+  if (pl.epi == sk::EPI_ARGMAX) return pl.parts_lds + 8 * (size_t)M + 16;
+  return pl.parts_lds + (size_t)tiles_per * pl.stage_elem;
+}
 
 int bucket(const int* list, int n, int v) {
   for (int i = 0; i < n; ++i)
@@ -159,10 +178,14 @@ int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
   if ((long)c.waves * c.ku < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
   if (c.split > 1 && (c.split - 1) * pl->slice_units >= units) return SK_ERR_CONFIG;  // empty split
   const int out_rows = (c.path == SK_PATH_MFMA) ? (gateup ? 16 : c.rows) : c.rows;
+  pl->out_rows = out_rows;
   pl->nrb = cdiv(N, out_rows);
-  pl->lds = (size_t)2 * c.waves * M * partial_rows * sizeof(float) + (op == SK_OP_LM_ARGMAX ? 8 * (size_t)M : 0);
-  if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
+  pl->parts_lds = (size_t)2 * c.waves * M * partial_rows * sizeof(float);
+  pl->stage_elem = stage_bytes(pl->epi) * (size_t)M * out_rows;
   if (c.grid > 0 && (c.grid % c.split) != 0) return SK_ERR_CONFIG;
+  const int tiles_per = c.grid > 0 ? cdiv(pl->nrb, c.grid / c.split) : 1;
+  pl->lds = plan_lds(*pl, M, tiles_per);
+  if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
   return SK_OK;
 }
 
@@ -172,9 +195,15 @@ int grid_bound(const Plan& pl) {
   return pl.cfg.split * (pl.nrb < kMaxGrid ? pl.nrb : kMaxGrid);
 }
 
+// Workspace layout: [arrival counters, padded to 256 B][partials or argmax
+// candidates].  The counters must be zero before the first call (allocate the
+// workspace zero-filled); every call returns them to zero.
+size_t ticket_bytes(int n) { return (((size_t)n * sizeof(unsigned)) + 255) & ~(size_t)255; }
+
 size_t plan_workspace(int op, int M, int N, const Plan& pl) {
-  if (op == SK_OP_LM_ARGMAX) return (size_t)grid_bound(pl) * M * sizeof(unsigned long long);
-  if (pl.cfg.split > 1) return (size_t)(op == SK_OP_GATEUP ? 2 : 1) * pl.cfg.split * M * (size_t)N * sizeof(float);
+  if (op == SK_OP_LM_ARGMAX) return ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
+  if (pl.cfg.split > 1)
+    return ticket_bytes(pl.nrb) + (size_t)(op == SK_OP_GATEUP ? 2 : 1) * pl.cfg.split * M * (size_t)N * sizeof(float);
   return 0;
 }
 
@@ -245,25 +274,34 @@ int bind_plan(Plan* pl, int num_cu, int* grid) {
   if (st) return st;
   const int threads = 64 * pl->cfg.waves;
   if (threads > fi.max_threads) return SK_ERR_CONFIG;
-  if (pl->lds > 64 * 1024 &&
-      hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)pl->lds) != hipSuccess)
-    return SK_ERR_CONFIG;
   pl->fn = fn;
   const int S = pl->cfg.split;
   if (pl->cfg.grid > 0) {
     *grid = pl->cfg.grid;
-    return SK_OK;
+  } else {
+    // Resident workgroups per K split from the occupancy at one staged tile,
+    // then as many tiles per workgroup as that needs (evened out so the last
+    // round is not a partial one), shrunk while the staging exceeds the
+    // preferred LDS budget.
+    const int per_cu = occupancy(reinterpret_cast<const void*>(fn), threads, pl->lds);
+    long cap = (long)per_cu * num_cu / S;
+    if (cap < 1) cap = 1;
+    int per_split = pl->nrb < cap ? pl->nrb : (int)cap;
+    if (per_split > kMaxGrid) per_split = kMaxGrid;
+    int tiles_per = cdiv(pl->nrb, per_split);
+    if (pl->epi != sk::EPI_ARGMAX)
+      while (tiles_per > 1 && pl->parts_lds + (size_t)tiles_per * pl->stage_elem > kPrefLds) --tiles_per;
+    per_split = cdiv(pl->nrb, tiles_per);
+    if (per_split > kMaxGrid) return SK_ERR_CONFIG;
+    *grid = per_split * S;
   }
-  const int per_cu = occupancy(reinterpret_cast<const void*>(fn), threads, pl->lds);
-  long cap = (long)per_cu * num_cu / S;   // resident workgroups per K split
-  if (cap < 1) cap = 1;
-  int per_split = pl->nrb < cap ? pl->nrb : (int)cap;
-  if (per_split > kMaxGrid) per_split = kMaxGrid;
-  // Even out tiles per workgroup so the last round is not a partial one.
-  const int tiles_per = cdiv(pl->nrb, per_split);
-  per_split = cdiv(pl->nrb, tiles_per);
-  *grid = per_split * S;
+  const int tiles_per = cdiv(pl->nrb, *grid / S);
+  pl->lds = pl->epi == sk::EPI_ARGMAX ? pl->lds : pl->parts_lds + (size_t)tiles_per * pl->stage_elem;
+  if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
+  if (pl->lds > 64 * 1024 &&
+      hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)pl->lds) != hipSuccess)
+    return SK_ERR_CONFIG;
   return SK_OK;
 }
 
@@ -309,7 +347,6 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, co
   for (int i = 0; i < nplans; ++i) {
     st = bind_plan(&plans[i], num_cu, &grids[i]);
     if (st) return st;
-    if (op == SK_OP_LM_ARGMAX && grids[i] > grid_bound(plans[i])) return SK_ERR_CONFIG;
   }
   for (int m0 = 0; m0 < M; m0 += kMaxM) {
     const int rows = (M - m0) < kMaxM ? (M - m0) : kMaxM;
@@ -321,8 +358,16 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, co
     a.W0 = W0;
     a.W1 = W1;
     a.C = C ? C + (int64_t)m0 * ldc : nullptr;
-    a.part = static_cast<float*>(ws);
-    a.best = static_cast<unsigned long long*>(ws);
+    if (ws) {
+      const size_t tb = ticket_bytes(op == SK_OP_LM_ARGMAX ? 1 : pl.nrb);
+      a.tickets = static_cast<unsigned*>(ws);
+      a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + tb);
+      a.best = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + tb);
+    }
+    if (op == SK_OP_LM_ARGMAX) {   // the fused argmax finishes into ids / maxv
+      a.C = reinterpret_cast<sk_bf16*>(ids + m0);
+      a.part = maxv + m0;
+    }
     a.lda = lda;
     a.ldw = ldw;
     a.ldc = ldc;
@@ -333,19 +378,10 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, co
     a.slice_units = pl.slice_units;
     a.ku = pl.cfg.ku;
     a.nrb = pl.nrb;
+    a.nw = pl.cfg.waves;
+    a.grid = grid;
+    a.rbstep = grid / pl.cfg.split;
     pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
-    if ((st = launch_status())) return st;
-    if (op == SK_OP_LM_ARGMAX) {
-      sk::argmax_final_kernel<<<dim3(rows), dim3(256), 0, stream>>>(a.best, grid, rows, ids + m0, maxv + m0);
-    } else if (pl.cfg.split > 1) {
-      const long total = (long)rows * N;
-      int g = (int)((total + 255) / 256);
-      if (g > 4 * num_cu * 8) g = 4 * num_cu * 8;
-      if (op == SK_OP_GATEUP)
-        sk::splitk_reduce_kernel<true><<<dim3(g), dim3(256), 0, stream>>>(a.part, a.C, ldc, rows, N, pl.cfg.split);
-      else
-        sk::splitk_reduce_kernel<false><<<dim3(g), dim3(256), 0, stream>>>(a.part, a.C, ldc, rows, N, pl.cfg.split);
-    }
     if ((st = launch_status())) return st;
   }
   return SK_OK;
@@ -390,7 +426,7 @@ int sk_check_config(int op, int M, int N, int K, const sk_config* cfg) {
 size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg) {
   if (op == SK_OP_ARGMAX) {
     if (M < 1 || N < 1) return 0;
-    return (size_t)cdiv(N, kArgmaxChunk) * M * sizeof(unsigned long long);
+    return ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
   }
   if (M < 1) return 0;
   const int Mk = M > kMaxM ? kMaxM : M;
@@ -427,16 +463,16 @@ int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, flo
   if (!L || !ids || !maxv) return SK_ERR_NULL;
   if (M > 65535) return SK_ERR_SHAPE;
   const int chunks = cdiv(V, kArgmaxChunk);
-  const size_t need = (size_t)chunks * M * sizeof(unsigned long long);
+  const size_t need = ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
   if (!ws || ws_bytes < need) return SK_ERR_WORKSPACE;
   int num_cu = 0;
   int st = device_info(&num_cu);
   if (st) return st;
-  unsigned long long* best = static_cast<unsigned long long*>(ws);
+  unsigned* ticket = static_cast<unsigned*>(ws);
+  unsigned long long* best = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + ticket_bytes(1));
   const int vec = (aligned16(L) && (ld & 7) == 0) ? 1 : 0;
-  sk::argmax_partial_kernel<<<dim3(chunks, M), dim3(256), 0, stream>>>(L, ld, M, V, kArgmaxChunk, vec, best);
-  if ((st = launch_status())) return st;
-  sk::argmax_final_kernel<<<dim3(M), dim3(256), 0, stream>>>(best, chunks, M, ids, maxv);
+  sk::argmax_kernel<<<dim3(chunks, M), dim3(sk::ARGMAX_THREADS), 0, stream>>>(L, ld, M, V, kArgmaxChunk, vec, best,
+                                                                             ticket, ids, maxv);
   return launch_status();
 }
 

@@ -24,14 +24,17 @@
 // In both paths the waves of a workgroup share a tile and split its K range;
 // their fp32 partials meet in LDS and are summed in wave order 0..W-1 by the
 // epilogue (double-buffered, one barrier per tile).  A global split over
-// workgroups writes fp32 partials that sk_splitk_reduce sums in split order
-// 0..S-1.  No floating-point atomics anywhere: results are bitwise
-// reproducible run to run.  The lm_head epilogue folds a greedy argmax in,
-// using a packed (order key, ~index) 64-bit max that is order independent.
+// workgroups writes fp32 partials to a workspace; the last workgroup to
+// arrive at a tile sums them in split order 0..S-1 inside the same kernel.
+// No floating-point atomics anywhere: results are bitwise reproducible run to
+// run.  The lm_head epilogue folds a greedy argmax in, using a packed
+// (order key, ~index) 64-bit max that is order independent.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace sk {
 
@@ -55,13 +58,17 @@ struct Args {
   const uint16_t* W1;     // up half for gate/up, else unused
   uint16_t* C;            // bf16 output [M, N], row stride ldc
   float* part;            // split-K partials [S][M][N] (gate/up: [2S][M][N])
-  unsigned long long* best;  // argmax partials [gridDim.x][M]
+  unsigned long long* best;  // argmax: per-row packed best [M]; zero between calls
+  unsigned* tickets;      // arrival counters (one per tile, or one for argmax); zero between calls
   int64_t lda, ldw, ldc;
   int M, N, K;            // N = output columns (I for gate/up)
-  int S;                  // global K splits (gridDim.x % S == 0)
+  int S;                  // global K splits (grid % S == 0)
   int slice_units;        // K units per global split
   int ku;                 // K units per wave
   int nrb;                // row blocks (tiles) along N
+  int nw;                 // waves per workgroup (blockDim.x / 64)
+  int grid;               // workgroups launched (gridDim.x)
+  int rbstep;             // grid / S: tile stride of one workgroup
 };
 
 // ---------------------------------------------------------------------------
@@ -165,52 +172,167 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// Shared epilogue: the waves' partial tiles sit in LDS as P[w][m][row]
-// (ROWS rows per tile); sum them in wave order and finish the tile.
+// Shared tile epilogue.  The waves' partial tiles sit in LDS as P[w][m][row]
+// (ROWS rows per tile); they are summed in wave order and the finished values
+// go to an LDS staging area (or, for argmax, into a per-row running best).
+// Nothing here touches global memory: the weight-streaming loop then issues
+// only weight loads, so the compiler can keep all of them in flight (global
+// stores would share the vmcnt counter with those loads).
 // ---------------------------------------------------------------------------
+template <int EPI>
+struct EpiTraits {
+  static constexpr bool gateup = (EPI == EPI_SWIGLU || EPI == EPI_PART_GU);
+  // bytes per staged output element (PART_GU stages gate and up fp32 sums)
+  static constexpr int stage_bytes = EPI == EPI_STORE || EPI == EPI_SWIGLU ? 2 : (EPI == EPI_PART ? 4 : 8);
+};
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Sum the partials of tile j (output columns rb*OUT_ROWS + r) into staging.
 template <int ROWS, int EPI>
-__device__ __forceinline__ void tile_epilogue(const Args& p, const float* P, int nw, int rb, int slice,
-                                              unsigned long long* lds_best) {
+__device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int nw, int rb, int j, void* stage,
+                                            unsigned long long* lds_best) {
+  constexpr bool GU = EpiTraits<EPI>::gateup;
+  constexpr int OUT_ROWS = GU ? ROWS / 2 : ROWS;
   const int M = p.M;
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  if constexpr (EPI == EPI_SWIGLU || EPI == EPI_PART_GU) {
-    constexpr int HALF = ROWS / 2;
-    const int nout = M * HALF;
-    for (int idx = tid; idx < nout; idx += nthr) {
-      const int m = idx / HALF, r = idx - (idx / HALF) * HALF;
-      float g = 0.f, u = 0.f;
-      for (int w = 0; w < nw; ++w) {
-        g += P[(w * M + m) * ROWS + r];
-        u += P[(w * M + m) * ROWS + r + HALF];
-      }
-      const int n = rb * HALF + r;
-      if (n < p.N) {
-        if constexpr (EPI == EPI_SWIGLU) {
-          p.C[(int64_t)m * p.ldc + n] = swiglu_bf(g, u);
-        } else {
-          p.part[((int64_t)slice * M + m) * p.N + n] = g;
-          p.part[((int64_t)(p.S + slice) * M + m) * p.N + n] = u;
-        }
-      }
+  const int tid = threadIdx.x, nthr = 64 * p.nw;
+  const int nout = M * OUT_ROWS;
+  for (int idx = tid; idx < nout; idx += nthr) {
+    const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
+    float g = 0.f, u = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      g += P[(w * M + m) * ROWS + r];
+      if constexpr (GU) u += P[(w * M + m) * ROWS + r + OUT_ROWS];
     }
-  } else {
-    const int nout = M * ROWS;
-    for (int idx = tid; idx < nout; idx += nthr) {
-      const int m = idx / ROWS, r = idx - (idx / ROWS) * ROWS;
-      float s = 0.f;
-      for (int w = 0; w < nw; ++w) s += P[(w * M + m) * ROWS + r];
-      const int n = rb * ROWS + r;
-      if (n < p.N) {
-        if constexpr (EPI == EPI_STORE) {
-          p.C[(int64_t)m * p.ldc + n] = f2bf(s);
-        } else if constexpr (EPI == EPI_PART) {
-          p.part[((int64_t)slice * M + m) * p.N + n] = s;
-        } else {  // EPI_ARGMAX
-          atomicMax(&lds_best[m], argmax_key(f2bf(s), n));
-        }
-      }
+    const int sidx = (j * M + m) * OUT_ROWS + r;
+    if constexpr (EPI == EPI_STORE) {
+      static_cast<uint16_t*>(stage)[sidx] = f2bf(g);
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      static_cast<uint16_t*>(stage)[sidx] = swiglu_bf(g, u);
+    } else if constexpr (EPI == EPI_PART) {
+      static_cast<float*>(stage)[sidx] = g;
+    } else if constexpr (EPI == EPI_PART_GU) {
+      static_cast<float*>(stage)[2 * sidx] = g;
+      static_cast<float*>(stage)[2 * sidx + 1] = u;
+    } else {   // EPI_ARGMAX
+      const int n = rb * OUT_ROWS + r;
+      if (n < p.N) atomicMax(&lds_best[m], argmax_key(f2bf(g), n));
     }
   }
+}
+
+// Device-coherent (agent scope) accesses for data exchanged between
+// workgroups: they bypass the non-coherent per-XCD L2 state (sc1), so no
+// full-L2 writeback/invalidate fence is needed around them.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Write the staged outputs of this workgroup's tiles (after the stream).
+// Split-K partials are stored device-coherent for the fixup below.
+template <int OUT_ROWS, int EPI>
+__device__ __forceinline__ void flush_stage(const Args& p, const void* stage, int ntiles, int rb0, int slice) {
+  const int M = p.M;
+  const int total = ntiles * M * OUT_ROWS;
+  for (int idx = threadIdx.x; idx < total; idx += 64 * p.nw) {
+    const int r = idx % OUT_ROWS;
+    const int jm = idx / OUT_ROWS;
+    const int m = jm % M, j = jm / M;
+    const int n = (rb0 + j * p.rbstep) * OUT_ROWS + r;
+    if (n >= p.N) continue;
+    if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
+      p.C[(int64_t)m * p.ldc + n] = static_cast<const uint16_t*>(stage)[idx];
+    } else if constexpr (EPI == EPI_PART) {
+      store_agent(&p.part[((int64_t)slice * M + m) * p.N + n], static_cast<const float*>(stage)[idx]);
+    } else if constexpr (EPI == EPI_PART_GU) {
+      store_agent(&p.part[((int64_t)slice * M + m) * p.N + n], static_cast<const float*>(stage)[2 * idx]);
+      store_agent(&p.part[((int64_t)(p.S + slice) * M + m) * p.N + n], static_cast<const float*>(stage)[2 * idx + 1]);
+    }
+  }
+}
+
+// Cross-workgroup completion without a second kernel.  Every workgroup
+// publishes its partial results with device-coherent stores (or, for argmax,
+// a device-scope 64-bit atomic max of its packed candidates), waits until they
+// are performed, then takes a ticket on an arrival counter.  The workgroup
+// that arrives last for a tile (or, for argmax, for the whole grid) reads
+// every contribution with device-coherent loads and finishes the output,
+// then resets what it used to zero for the next call.  Split-K sums run in
+// fixed split order s = 0..S-1 and the key max is order independent, so the
+// result never depends on which workgroup arrives last; no workgroup waits.
+__device__ __forceinline__ bool take_ticket(unsigned* ticket, unsigned expected) {
+  const unsigned old = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool last = (old == expected - 1u);
+  if (last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
+template <int OUT_ROWS, int EPI>
+__device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0, int* lds_flags) {
+  const int M = p.M, S = p.S;
+  const int64_t MN = (int64_t)M * p.N;
+  __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores are performed
+  __syncthreads();
+  // Tickets of up to `cap` tiles per round (the flags reuse the partials' LDS).
+  const int cap = 2 * p.nw * M * OUT_ROWS;
+  for (int j0 = 0; j0 < ntiles; j0 += cap) {
+    const int jn = min(ntiles - j0, cap);
+    if (threadIdx.x == 0)
+      for (int j = 0; j < jn; ++j)
+        lds_flags[j] = take_ticket(&p.tickets[rb0 + (j0 + j) * p.rbstep], (unsigned)S) ? 1 : 0;
+    __syncthreads();
+    for (int j = 0; j < jn; ++j) {
+      if (!lds_flags[j]) continue;
+      const int rb = rb0 + (j0 + j) * p.rbstep;
+      for (int idx = threadIdx.x; idx < M * OUT_ROWS; idx += 64 * p.nw) {
+        const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
+        const int n = rb * OUT_ROWS + r;
+        if (n >= p.N) continue;
+        const int64_t e = (int64_t)m * p.N + n;
+        float g = 0.f, u = 0.f;
+        for (int s = 0; s < S; ++s) {
+          g += load_agent(&p.part[s * MN + e]);
+          if constexpr (EPI == EPI_PART_GU) u += load_agent(&p.part[(S + s) * MN + e]);
+        }
+        p.C[(int64_t)m * p.ldc + n] = (EPI == EPI_PART_GU) ? swiglu_bf(g, u) : f2bf(g);
+      }
+    }
+    __syncthreads();   // flags are rewritten by the next round
+  }
+}
+
+// Final argmax: every workgroup folds its per-row best into best[m] with a
+// device-scope atomic max; the last to arrive decodes best[m] into ids/maxv
+// (passed through p.C as int64* and p.part as float*) and clears best[m].
+__device__ __forceinline__ void argmax_fixup(const Args& p, const unsigned long long* lds_best, int* lds_flag) {
+  const int M = p.M;
+  if ((int)threadIdx.x < M)
+    __hip_atomic_fetch_max(&p.best[threadIdx.x], lds_best[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) *lds_flag = take_ticket(&p.tickets[0], (unsigned)p.grid) ? 1 : 0;
+  __syncthreads();
+  if (!*lds_flag) return;
+  if ((int)threadIdx.x < M) {
+    const unsigned long long b =
+        __hip_atomic_exchange(&p.best[threadIdx.x], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    reinterpret_cast<int64_t*>(p.C)[threadIdx.x] = argmax_key_index(b);
+    p.part[threadIdx.x] = argmax_key_value(b);
+  }
+}
+
+// LDS layout of both kernel families:
+//   [partials: 2 buffers x nw x M x ROWS fp32][staging or argmax best]
+// Tiles of workgroup b: rb = b/S + j*(gridDim.x/S), j < ntiles.
+__device__ __forceinline__ int wg_tiles(int rb0, int rbstep, int nrb) {
+  return rb0 < nrb ? (nrb - 1 - rb0) / rbstep + 1 : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -218,110 +340,117 @@ __device__ __forceinline__ void tile_epilogue(const Args& p, const float* P, int
 //   MT : activation row tiles of 16 (M <= 16*MT)
 //   NT : weight row tiles of 16 per workgroup tile (gate/up: 2 = gate + up)
 //   KU : compile-time bound on K units (32 columns) per wave
+// The per-tile loop is branch-free: every wave always issues NT*KU weight
+// loads (units past the wave's range reload its last unit and meet zero
+// activations), and the last tile is peeled so that its iteration issues no
+// prefetch.  The compiler can then keep the next tile's NT*KU loads in flight
+// while the current tile's MFMAs run.
 // ---------------------------------------------------------------------------
 template <int MT, int NT, int KU, int EPI>
 __device__ __forceinline__ void mfma_body(Args p) {
-  constexpr bool GATEUP = (EPI == EPI_SWIGLU || EPI == EPI_PART_GU);
+  constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int ROWS = 16 * NT;                  // partial rows per tile in LDS
-  constexpr int WROWS = GATEUP ? 16 : 16 * NT;   // output columns per tile
+  constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
   static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
 
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nw = blockDim.x >> 6;
+  const int nw = p.nw;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int M = p.M;
 
   const int S = p.S;
   const int slice = blockIdx.x % S;
-  const int rbstep = gridDim.x / S;
+  const int rbstep = p.rbstep;
+  const int rb0 = blockIdx.x / S;
+  const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
   const int units = p.K >> 5;
   const int s_lo = slice * p.slice_units;
   const int s_hi = min(s_lo + p.slice_units, units);
   const int u_lo = s_lo + wave * p.ku;
-  const int u_hi = min(u_lo + p.ku, s_hi);
-  const int nu = __builtin_amdgcn_readfirstlane(max(0, u_hi - u_lo));
-  const int kb = u_lo * 32 + 8 * g4;
+  const int nu = __builtin_amdgcn_readfirstlane(max(0, min(u_lo + p.ku, s_hi) - u_lo));
 
-  unsigned long long* lds_best = nullptr;
   float* parts = lds;
   const int part_floats = nw * M * ROWS;
+  void* stage = lds + 2 * part_floats;
+  unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
   if constexpr (EPI == EPI_ARGMAX) {
-    lds_best = reinterpret_cast<unsigned long long*>(lds + 2 * part_floats);
     if (tid < M) lds_best[tid] = 0ull;
   }
 
-  // Activation fragments: lane holds A[16*mt + r16][kb + 32u .. +8].
+  // Column (element) of unit u for this lane; padding units repeat the wave's
+  // last unit (always inside the matrix).
+  int kcol[KU];
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int uu = min(max(u_lo + min(u, nu - 1), 0), units - 1);
+    kcol[u] = uu * 32 + 8 * g4;
+  }
+
+  // Activation fragments: lane holds A[16*mt + r16][kcol[u] .. +8], zero for
+  // rows >= M and padding units.
   bf16x8 af[MT][KU];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + r16;
-    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda + kb;
+    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda;
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (u < nu) v = ld16(ap + 32 * u);
-      if (m >= M) v = u32x4{0u, 0u, 0u, 0u};
+      u32x4 v = ld16(ap + kcol[u]);
+      if (m >= M || u >= nu) v = u32x4{0u, 0u, 0u, 0u};
       af[mt][u] = __builtin_bit_cast(bf16x8, v);
     }
   }
 
-  // Weight row pointers of a tile (rows past N are clamped to N-1: the loads
-  // stay in bounds and those columns are never stored).
+  // Weight row base of tile rb (rows past N clamp to N-1: in bounds, unused).
   auto wrow = [&](int rb, int nt) -> const uint16_t* {
     if constexpr (GATEUP) {
       const int row = min(rb * 16 + r16, p.N - 1);
-      return (nt == 0 ? p.W0 : p.W1) + (int64_t)row * p.ldw + kb;
+      return (nt == 0 ? p.W0 : p.W1) + (int64_t)row * p.ldw;
     } else {
       const int row = min(rb * ROWS + 16 * nt + r16, p.N - 1);
-      return p.W0 + (int64_t)row * p.ldw + kb;
+      return p.W0 + (int64_t)row * p.ldw;
     }
   };
 
   u32x4 wf[NT][KU];
-  int rb = blockIdx.x / S;
-  if (rb < p.nrb) {
+  if (ntiles > 0) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const uint16_t* wp = wrow(rb, nt);
+      const uint16_t* wp = wrow(rb0, nt);
 #pragma unroll
-      for (int u = 0; u < KU; ++u)
-        if (u < nu) wf[nt][u] = ld16_stream(wp + 32 * u);
+      for (int u = 0; u < KU; ++u) wf[nt][u] = ld16_stream(wp + kcol[u]);
     }
   }
 
-  int buf = 0;
-  for (; rb < p.nrb; rb += rbstep) {
-    const int rbn = rb + rbstep;
-    const bool more = rbn < p.nrb;
+  auto tile = [&](int j, auto prefetch) {
+    constexpr bool PF = decltype(prefetch)::value;
+    const int rb = rb0 + j * rbstep;
     const uint16_t* wpn[NT];
+    if constexpr (PF) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) wpn[nt] = wrow(more ? rbn : rb, nt);
-
+      for (int nt = 0; nt < NT; ++nt) wpn[nt] = wrow(rb + rbstep, nt);
+    }
     f32x4 acc[NT][MT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      if (u < nu) {
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const bf16x8 wv = __builtin_bit_cast(bf16x8, wf[nt][u]);
+      for (int nt = 0; nt < NT; ++nt) {
+        const bf16x8 wv = __builtin_bit_cast(bf16x8, wf[nt][u]);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[mt][u], acc[nt][mt], 0, 0, 0);
-          if (more) wf[nt][u] = ld16_stream(wpn[nt] + 32 * u);
-        }
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[mt][u], acc[nt][mt], 0, 0, 0);
+        if constexpr (PF) wf[nt][u] = ld16_stream(wpn[nt] + kcol[u]);
       }
     }
-
     // Lane holds tile rows 16*nt + 4*g4 + {0..3} for activation row 16*mt + r16.
-    float* P = parts + buf * part_floats;
+    float* P = parts + (j & 1) * part_floats;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -329,15 +458,20 @@ __device__ __forceinline__ void mfma_body(Args p) {
         const int m = 16 * mt + r16;
         if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
       }
-    __syncthreads();
-    tile_epilogue<ROWS, EPI>(p, P, nw, rb, slice, lds_best);
-    buf ^= 1;
-    (void)WROWS;
-  }
+    lds_barrier();
+    tile_reduce<ROWS, EPI>(p, P, nw, rb, j, stage, lds_best);
+  };
 
+  int j = 0;
+  for (; j + 1 < ntiles; ++j) tile(j, std::integral_constant<bool, true>{});
+  if (ntiles > 0) tile(j, std::integral_constant<bool, false>{});
+  lds_barrier();
   if constexpr (EPI == EPI_ARGMAX) {
-    __syncthreads();
-    if (tid < M) p.best[(int64_t)blockIdx.x * M + tid] = lds_best[tid];
+    argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
+  } else {
+    flush_stage<OUT_ROWS, EPI>(p, stage, ntiles, rb0, slice);
+    if constexpr (EPI == EPI_PART || EPI == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, EPI>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
   }
 }
 
@@ -346,48 +480,61 @@ __device__ __forceinline__ void mfma_body(Args p) {
 //   MR : compile-time bound on activation rows (M <= MR)
 //   R  : weight rows per tile (gate/up: R gate rows + R up rows)
 //   KU : compile-time bound on K units (512 columns) per wave
+// Same loop structure as the MFMA path: branch-free loads, peeled last tile,
+// outputs staged in LDS.  Columns past the K slice read a clamped in-bounds
+// chunk and meet zero activations.
 // ---------------------------------------------------------------------------
 template <int MR, int R, int KU, int EPI>
 __device__ __forceinline__ void gemv_body(Args p) {
-  constexpr bool GATEUP = (EPI == EPI_SWIGLU || EPI == EPI_PART_GU);
+  constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int RR = GATEUP ? 2 * R : R;   // partial rows per tile
+  constexpr int OUT_ROWS = R;
 
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nw = blockDim.x >> 6;
+  const int nw = p.nw;
   const int M = p.M;
 
   const int S = p.S;
   const int slice = blockIdx.x % S;
-  const int rbstep = gridDim.x / S;
+  const int rbstep = p.rbstep;
+  const int rb0 = blockIdx.x / S;
+  const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
   const int units = (p.K + 511) >> 9;
   const int s_lo = slice * p.slice_units;
   const int s_hi = min(s_lo + p.slice_units, units);
   const int u_lo = s_lo + wave * p.ku;
-  const int u_hi = min(u_lo + p.ku, s_hi);
-  const int nu = __builtin_amdgcn_readfirstlane(max(0, u_hi - u_lo));
-  const int kb = u_lo * 512 + 8 * lane;
+  const int nu = __builtin_amdgcn_readfirstlane(max(0, min(u_lo + p.ku, s_hi) - u_lo));
   const int kend = min(s_hi * 512, p.K);
 
-  unsigned long long* lds_best = nullptr;
   float* parts = lds;
   const int part_floats = nw * M * RR;
+  void* stage = lds + 2 * part_floats;
+  unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
   if constexpr (EPI == EPI_ARGMAX) {
-    lds_best = reinterpret_cast<unsigned long long*>(lds + 2 * part_floats);
     if (tid < M) lds_best[tid] = 0ull;
   }
 
-  // Activation chunks: lane holds A[m][kb + 512u .. +8] (zero past the slice).
+  // Lane's column of unit u (clamped in bounds) and whether it is real data.
+  int kcol[KU];
+  bool kok[KU];
+#pragma unroll
+  for (int u = 0; u < KU; ++u) {
+    const int k = (u_lo + u) * 512 + 8 * lane;
+    kok[u] = (u < nu) && (k < kend);
+    kcol[u] = min(max(k, 0), p.K - 8);
+  }
+
   u32x4 af[MR][KU];
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
-    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda + kb;
+    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda;
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < M && u < nu && kb + 512 * u < kend) v = ld16(ap + 512 * u);
+      u32x4 v = ld16(ap + kcol[u]);
+      if (m >= M || !kok[u]) v = u32x4{0u, 0u, 0u, 0u};
       af[m][u] = v;
     }
   }
@@ -395,54 +542,41 @@ __device__ __forceinline__ void gemv_body(Args p) {
   auto wrow = [&](int rb, int rr) -> const uint16_t* {
     if constexpr (GATEUP) {
       const int row = min(rb * R + (rr % R), p.N - 1);
-      return (rr < R ? p.W0 : p.W1) + (int64_t)row * p.ldw + kb;
+      return (rr < R ? p.W0 : p.W1) + (int64_t)row * p.ldw;
     } else {
       const int row = min(rb * R + rr, p.N - 1);
-      return p.W0 + (int64_t)row * p.ldw + kb;
+      return p.W0 + (int64_t)row * p.ldw;
     }
   };
 
   u32x4 wf[RR][KU];
-  int rb = blockIdx.x / S;
-  if (rb < p.nrb) {
+  if (ntiles > 0) {
 #pragma unroll
     for (int rr = 0; rr < RR; ++rr) {
-      const uint16_t* wp = wrow(rb, rr);
+      const uint16_t* wp = wrow(rb0, rr);
 #pragma unroll
-      for (int u = 0; u < KU; ++u) {
-        wf[rr][u] = u32x4{0u, 0u, 0u, 0u};
-        if (u < nu && kb + 512 * u < kend) wf[rr][u] = ld16_stream(wp + 512 * u);
-      }
+      for (int u = 0; u < KU; ++u) wf[rr][u] = ld16_stream(wp + kcol[u]);
     }
   }
 
-  int buf = 0;
-  for (; rb < p.nrb; rb += rbstep) {
-    const int rbn = rb + rbstep;
-    const bool more = rbn < p.nrb;
-
+  auto tile = [&](int j, auto prefetch) {
+    constexpr bool PF = decltype(prefetch)::value;
+    const int rb = rb0 + j * rbstep;
     float acc[RR][MR];
 #pragma unroll
     for (int rr = 0; rr < RR; ++rr)
 #pragma unroll
       for (int m = 0; m < MR; ++m) acc[rr][m] = 0.f;
-
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
-      if (u < nu) {
 #pragma unroll
-        for (int rr = 0; rr < RR; ++rr) {
+      for (int rr = 0; rr < RR; ++rr) {
 #pragma unroll
-          for (int m = 0; m < MR; ++m) acc[rr][m] = dot8(wf[rr][u], af[m][u], acc[rr][m]);
-          if (more) {
-            wf[rr][u] = u32x4{0u, 0u, 0u, 0u};
-            if (kb + 512 * u < kend) wf[rr][u] = ld16_stream(wrow(rbn, rr) + 512 * u);
-          }
-        }
+        for (int m = 0; m < MR; ++m) acc[rr][m] = dot8(wf[rr][u], af[m][u], acc[rr][m]);
+        if constexpr (PF) wf[rr][u] = ld16_stream(wrow(rb + rbstep, rr) + kcol[u]);
       }
     }
-
-    float* P = parts + buf * part_floats;
+    float* P = parts + (j & 1) * part_floats;
 #pragma unroll
     for (int rr = 0; rr < RR; ++rr)
 #pragma unroll
@@ -450,80 +584,45 @@ __device__ __forceinline__ void gemv_body(Args p) {
         const float s = wave_sum(acc[rr][m]);
         if (m < M && lane == 0) P[(wave * M + m) * RR + rr] = s;
       }
-    __syncthreads();
-    tile_epilogue<RR, EPI>(p, P, nw, rb, slice, lds_best);
-    buf ^= 1;
-  }
+    lds_barrier();
+    tile_reduce<RR, EPI>(p, P, nw, rb, j, stage, lds_best);
+  };
 
+  int j = 0;
+  for (; j + 1 < ntiles; ++j) tile(j, std::integral_constant<bool, true>{});
+  if (ntiles > 0) tile(j, std::integral_constant<bool, false>{});
+  lds_barrier();
   if constexpr (EPI == EPI_ARGMAX) {
-    __syncthreads();
-    if (tid < M) p.best[(int64_t)blockIdx.x * M + tid] = lds_best[tid];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Global split-K reduction: C = bf16(sum_{s=0..S-1} part[s]) (gate/up: swiglu
-// of the two sums), the order of the reference's _sum_kernel /
-// _sum_gateup_kernel (engine/kernels/gemm.py:104-112, 171-181).
-// ---------------------------------------------------------------------------
-template <bool GATEUP>
-__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ part, uint16_t* __restrict__ C,
-                                                            int64_t ldc, int M, int N, int S) {
-  const int64_t MN = (int64_t)M * N;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN; i += (int64_t)gridDim.x * blockDim.x) {
-    float g = 0.f, u = 0.f;
-    for (int s = 0; s < S; ++s) {
-      g += part[s * MN + i];
-      if constexpr (GATEUP) u += part[(S + s) * MN + i];
-    }
-    const int m = (int)(i / N), n = (int)(i - (int64_t)(i / N) * N);
-    C[(int64_t)m * ldc + n] = GATEUP ? swiglu_bf(g, u) : f2bf(g);
+    argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
+  } else {
+    flush_stage<OUT_ROWS, EPI>(p, stage, ntiles, rb0, slice);
+    if constexpr (EPI == EPI_PART || EPI == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, EPI>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
   }
 }
 
 #ifdef SK_AUX_KERNELS
 // Non-template kernels: defined only in the translation unit that launches
 // them (sk_abi.hip), so every other unit can include this header.
-// Final argmax over G per-workgroup candidates best[g*M + m]; one workgroup
-// per row.  The packed-key max is order independent, so any reduction tree
-// gives the same (value, lowest index).
-__global__ void __launch_bounds__(256) argmax_final_kernel(const unsigned long long* __restrict__ best, int G, int M,
-                                                           int64_t* __restrict__ ids, float* __restrict__ maxv) {
-  __shared__ unsigned long long red[256];
-  const int m = blockIdx.x;
-  unsigned long long b = 0ull;
-  for (int g = threadIdx.x; g < G; g += blockDim.x) {
-    const unsigned long long v = best[(int64_t)g * M + m];
-    b = v > b ? v : b;
-  }
-  red[threadIdx.x] = b;
-  __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      const unsigned long long o = red[threadIdx.x + s];
-      if (o > red[threadIdx.x]) red[threadIdx.x] = o;
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    ids[m] = argmax_key_index(red[0]);
-    maxv[m] = argmax_key_value(red[0]);
-  }
-}
+// Argmax over materialised bf16 logits: workgroup (c, m) scans chunk c of row
+// m; the last workgroup to arrive reduces every chunk's candidate.  Rows that
+// are 16-byte aligned (vec) are read with 8-column vector loads.
+constexpr int ARGMAX_THREADS = 256;
 
-// Argmax over materialised bf16 logits: workgroup (c, m) scans chunk c of row m.
-__global__ void __launch_bounds__(256) argmax_partial_kernel(const uint16_t* __restrict__ L, int64_t ld, int M, int V,
-                                                             int chunk, int vec, unsigned long long* __restrict__ best) {
-  __shared__ unsigned long long red[256];
-  const int m = blockIdx.y, c = blockIdx.x;
+__global__ void __launch_bounds__(ARGMAX_THREADS) argmax_kernel(const uint16_t* __restrict__ L, int64_t ld, int M,
+                                                                int V, int chunk, int vec,
+                                                                unsigned long long* __restrict__ best,
+                                                                unsigned* __restrict__ ticket, int64_t* __restrict__ ids,
+                                                                float* __restrict__ maxv) {
+  __shared__ unsigned long long red[ARGMAX_THREADS];
+  __shared__ int flag;
+  const int m = blockIdx.y, c = blockIdx.x, tid = threadIdx.x;
+  const int chunks = gridDim.x;
   const uint16_t* row = L + (int64_t)m * ld;
   const int lo = c * chunk, hi = min(lo + chunk, V);
   unsigned long long b = 0ull;
-  // 8-column vector loads over the body when rows are 16-byte aligned
-  // (vec: L aligned and ld % 8 == 0; lo is a multiple of chunk, itself of 8),
-  // scalar loads for the tail and for unaligned layouts.
   const int vhi = vec ? lo + ((hi - lo) & ~7) : lo;
-  for (int k = lo + 8 * threadIdx.x; k < vhi; k += 8 * blockDim.x) {
+  for (int k = lo + 8 * tid; k < vhi; k += 8 * ARGMAX_THREADS) {
     const u32x4 v = ld16(row + k);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -534,20 +633,29 @@ __global__ void __launch_bounds__(256) argmax_partial_kernel(const uint16_t* __r
       b = k1 > b ? k1 : b;
     }
   }
-  for (int k = vhi + threadIdx.x; k < hi; k += blockDim.x) {
+  for (int k = vhi + tid; k < hi; k += ARGMAX_THREADS) {
     const unsigned long long kk = argmax_key(row[k], k);
     b = kk > b ? kk : b;
   }
-  red[threadIdx.x] = b;
+  red[tid] = b;
   __syncthreads();
-  for (int s = blockDim.x / 2; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) {
-      const unsigned long long o = red[threadIdx.x + s];
-      if (o > red[threadIdx.x]) red[threadIdx.x] = o;
-    }
+  for (int sft = ARGMAX_THREADS / 2; sft > 0; sft >>= 1) {
+    if (tid < sft && red[tid + sft] > red[tid]) red[tid] = red[tid + sft];
     __syncthreads();
   }
-  if (threadIdx.x == 0) best[(int64_t)c * M + m] = red[0];
+  if (tid == 0) {
+    __hip_atomic_fetch_max(&best[m], red[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    flag = take_ticket(ticket, (unsigned)(chunks * M)) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!flag) return;
+  // Last workgroup of the grid: decode every row and clear best[] for the next call.
+  for (int mm = tid; mm < M; mm += ARGMAX_THREADS) {
+    const unsigned long long bb = __hip_atomic_exchange(&best[mm], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ids[mm] = argmax_key_index(bb);
+    maxv[mm] = argmax_key_value(bb);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -37,7 +37,7 @@ BF16 = torch.bfloat16
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "LmArgmax", "gemm", "gateup_swiglu", "lm_argmax", "argmax",
     "add_rms_norm", "swiglu", "pick_matmul", "pick_gateup", "pick_normed", "pick_lm_argmax", "SkConfig",
-    "SK_PATH_MFMA", "SK_PATH_GEMV",
+    "SK_PATH_MFMA", "SK_PATH_GEMV", "SK_OP_GEMM", "SK_OP_GATEUP", "SK_OP_LM_ARGMAX", "SK_OP_ARGMAX",
 ]
 
 
@@ -62,8 +62,10 @@ def _device_guard(t: torch.Tensor) -> None:
 
 
 def _workspace(op: int, M: int, N: int, K: int, cfg: SkConfig | None, device) -> torch.Tensor | None:
+    """Zero-filled once: the library's arrival counters live at its start and
+    every call leaves them at zero again."""
     n = _lib.workspace_bytes(op, M, N, K, cfg)
-    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
+    return torch.zeros(n, dtype=torch.uint8, device=device) if n else None
 
 
 def _ws_args(ws: torch.Tensor | None):

@@ -59,11 +59,12 @@ def test_default_config_is_valid_for_every_decode_shape(name, M):
     assert cfg.waves * cfg.ku * cfg.split >= units
     ws = _lib.workspace_bytes(op, M, N, K, cfg)
     if op == SK_OP_LM_ARGMAX:
-        assert ws >= 8 * min(M, 64)
+        assert ws == _tickets(1) + 8 * min(M, 64)
     elif cfg.split == 1:
         assert ws == 0
     else:
-        assert ws == (2 if op == SK_OP_GATEUP else 1) * cfg.split * min(M, 64) * N * 4
+        tiles = -(-N // 16)
+        assert ws == _tickets(tiles) + (2 if op == SK_OP_GATEUP else 1) * cfg.split * min(M, 64) * N * 4
 
 
 def test_default_config_prefers_no_global_split_at_decode_m():
@@ -125,12 +126,19 @@ def test_argument_validation_precedes_any_device_work():
     assert lib.sk_swiglu_bf16(FAKE, 100, FAKE, 50, 2, 60, None) == SK_ERR_SHAPE
 
 
+def _tickets(n):
+    return (4 * n + 255) // 256 * 256
+
+
 def test_workspace_bytes():
-    assert _lib.workspace_bytes(SK_OP_ARGMAX, 4, 151936, 0) == 4 * ((151936 + 4095) // 4096) * 8
+    """[arrival counters padded to 256 B][partials | argmax candidates]."""
+    assert _lib.workspace_bytes(SK_OP_ARGMAX, 4, 151936, 0) == _tickets(1) + 4 * 8
     assert _lib.workspace_bytes(SK_OP_GEMM, 0, 6144, 2560) == 0
     cfg = SkConfig.make(SK_PATH_MFMA, 4, 10, 16, 2)
-    assert _lib.workspace_bytes(SK_OP_GEMM, 8, 6144, 2560, cfg) == 2 * 8 * 6144 * 4
-    assert _lib.workspace_bytes(SK_OP_GATEUP, 8, 9728, 2560, cfg) == 2 * 2 * 8 * 9728 * 4
+    assert _lib.workspace_bytes(SK_OP_GEMM, 8, 6144, 2560, cfg) == _tickets(6144 // 16) + 2 * 8 * 6144 * 4
+    assert _lib.workspace_bytes(SK_OP_GATEUP, 8, 9728, 2560, cfg) == _tickets(9728 // 16) + 2 * 2 * 8 * 9728 * 4
+    lm = SkConfig.make(SK_PATH_MFMA, 4, 20, 16, 1, 500)
+    assert _lib.workspace_bytes(SK_OP_LM_ARGMAX, 8, 151936, 2560, lm) == _tickets(1) + 8 * 8
 
 
 def test_valid_call_without_gpu_fails_loudly():
