@@ -63,7 +63,8 @@ typedef enum sk_op {
 typedef enum sk_path {
   SK_PATH_AUTO = 0,
   SK_PATH_MFMA = 1,       /* v_mfma_f32_16x16x32_bf16 tiles, 16 weight rows per wave tile */
-  SK_PATH_GEMV = 2        /* VALU v_dot2_f32_bf16, lanes span K, DPP/shuffle lane reduction */
+  SK_PATH_GEMV = 2,       /* VALU v_dot2_f32_bf16, lanes span K, DPP/shuffle lane reduction */
+  SK_PATH_MFMA_LDS = 3    /* MFMA fed from LDS: weight rows loaded 1 KiB-contiguous, transposed in LDS */
 } sk_path;
 
 /*
@@ -75,7 +76,8 @@ typedef enum sk_path {
  *   path   : SK_PATH_MFMA or SK_PATH_GEMV
  *   waves  : wavefronts per workgroup; they split the workgroup's K slice and
  *            their fp32 partials are summed in LDS in fixed wave order
- *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns)
+ *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns;
+ *            MFMA_LDS: 16 or 8, i.e. one 512- or 256-column chunk per wave)
  *   rows   : weight rows per workgroup tile (MFMA: 16 or 32; GEMV: 1..8)
  *   split  : global K splits; >1 writes fp32 partials to the workspace and
  *            the last workgroup to finish a tile sums them in fixed split

@@ -42,6 +42,7 @@ def _units() -> list[tuple[Path, list[str], Path]]:
     for epi in range(N_EPI):
         units.append((CSRC / "sk_inst_mfma.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfma_{epi}.o"))
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
+        units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
     return units
 
 

@@ -107,6 +107,7 @@ struct Plan {
   int nrb = 0;                  // tiles along N
   int slice_units = 0;
   int out_rows = 0;             // output columns per tile
+  size_t pre_lds = 0;           // per-wave weight staging (LDS-transposed MFMA path)
   size_t parts_lds = 0;         // double-buffered fp32 partial tiles
   size_t stage_elem = 0;        // LDS bytes per staged tile (0: argmax keeps 8*M bytes)
   size_t lds = 0;               // total dynamic LDS (set once the grid is known)
@@ -125,8 +126,8 @@ size_t stage_bytes(int epi) {
 
 // Dynamic LDS of a plan whose workgroups each own at most tiles_per tiles.
 size_t plan_lds(const Plan& pl, int M, int tiles_per) {
-  if (pl.epi == sk::EPI_ARGMAX) return pl.parts_lds + 8 * (size_t)M + 16;
-  return pl.parts_lds + (size_t)tiles_per * pl.stage_elem;
+  if (pl.epi == sk::EPI_ARGMAX) return pl.pre_lds + pl.parts_lds + 8 * (size_t)M + 16;
+  return pl.pre_lds + pl.parts_lds + (size_t)tiles_per * pl.stage_elem;
 }
 
 int bucket(const int* list, int n, int v) {
@@ -160,6 +161,18 @@ int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
     partial_rows = 16 * pl->tn;
     if (c.waves > sk::max_waves_for_regs(sk::mfma_regs(pl->tm, pl->tn, pl->tku < 0 ? 20 : pl->tku)))
       return SK_ERR_CONFIG;
+  } else if (c.path == SK_PATH_MFMA_LDS) {
+    // One K chunk of KW = 32*ku columns (512 or 256) per wave.
+    if (gateup ? c.rows != 16 : (c.rows != 16 && c.rows != 32)) return SK_ERR_CONFIG;
+    if (c.ku != 16 && c.ku != 8) return SK_ERR_CONFIG;
+    const int KW = 32 * c.ku;
+    units = cdiv(K, KW);
+    pl->tm = cdiv(M, 16);
+    pl->tn = gateup ? 2 : c.rows / 16;
+    pl->tku = KW;
+    partial_rows = 16 * pl->tn;
+    if (c.waves > sk::max_waves_for_regs(sk::mfmt_regs(pl->tm, pl->tn, KW))) return SK_ERR_CONFIG;
+    pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
     if (M > 8) return SK_ERR_CONFIG;
@@ -174,8 +187,14 @@ int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
     return SK_ERR_CONFIG;
   }
   if (pl->tku < 0) return SK_ERR_CONFIG;
+  // The instance must be compiled (the lookup is host-side table code).
+  sk::KernelFn inst = c.path == SK_PATH_MFMA       ? sk::mfma_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku)
+                      : c.path == SK_PATH_MFMA_LDS ? sk::mfmt_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku)
+                                                   : sk::gemv_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
+  if (!inst) return SK_ERR_CONFIG;
   pl->slice_units = cdiv(units, c.split);
-  if ((long)c.waves * c.ku < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
+  const long per_wave = c.path == SK_PATH_MFMA_LDS ? 1 : c.ku;
+  if ((long)c.waves * per_wave < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
   if (c.split > 1 && (c.split - 1) * pl->slice_units >= units) return SK_ERR_CONFIG;  // empty split
   const int out_rows = (c.path == SK_PATH_MFMA) ? (gateup ? 16 : c.rows) : c.rows;
   pl->out_rows = out_rows;
@@ -207,7 +226,121 @@ size_t plan_workspace(int op, int M, int N, const Plan& pl) {
   return 0;
 }
 
-int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
+// Offline-tuned launch table for the Qwen3-4B decode shapes (the reference
+// picks a Triton config per shape at warmup: engine/kernels/gemm.py:516-660).
+// Each entry is the fastest configuration measured on one MI355X for that
+// shape at that row count, timed as graph replays of back-to-back launches
+// over 24 distinct weight copies (so HBM, not the 256 MB MALL, serves the
+// weights).  Fields: {path, waves, ku, rows, split, grid}.
+struct Tuned {
+  int op, N, K, M;
+  sk_config cfg;
+};
+
+const Tuned kTuned[] = {
+    {SK_OP_GEMM, 6144, 2560, 1, {2, 1, 5, 2, 1, 0}},  // qkv        7.29 us  4315 GB/s
+    {SK_OP_GEMM, 6144, 2560, 2, {3, 10, 8, 16, 1, 0}},  // qkv        8.27 us  3807 GB/s
+    {SK_OP_GEMM, 6144, 2560, 4, {3, 10, 8, 16, 1, 0}},  // qkv        8.44 us  3733 GB/s
+    {SK_OP_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 0}},  // qkv        8.75 us  3612 GB/s
+    {SK_OP_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv        9.71 us  3268 GB/s
+    {SK_OP_GEMM, 6144, 2560, 32, {3, 5, 16, 16, 1, 0}},  // qkv       13.87 us  2308 GB/s
+    {SK_OP_GEMM, 6144, 2560, 40, {1, 16, 5, 16, 1, 0}},  // qkv       17.01 us  1890 GB/s
+    {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
+    {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
+    {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     6.57 us  3196 GB/s
+    {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     7.22 us  2912 GB/s
+    {SK_OP_GEMM, 2560, 4096, 8, {3, 16, 8, 16, 1, 0}},  // o_proj     7.77 us  2712 GB/s
+    {SK_OP_GEMM, 2560, 4096, 16, {3, 8, 16, 16, 1, 0}},  // o_proj     9.39 us  2256 GB/s
+    {SK_OP_GEMM, 2560, 4096, 32, {3, 8, 16, 16, 1, 0}},  // o_proj    13.42 us  1594 GB/s
+    {SK_OP_GEMM, 2560, 4096, 40, {3, 8, 8, 32, 2, 0}},  // o_proj    15.86 us  1356 GB/s
+    {SK_OP_GEMM, 2560, 4096, 64, {3, 8, 8, 16, 2, 0}},  // o_proj    20.33 us  1073 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // gate_up   17.94 us  5553 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 2, {3, 5, 16, 16, 1, 0}},  // gate_up   18.39 us  5421 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 4, {3, 5, 16, 16, 1, 0}},  // gate_up   18.67 us  5340 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 8, {3, 5, 16, 16, 1, 0}},  // gate_up   19.36 us  5155 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 16, {3, 5, 16, 16, 1, 0}},  // gate_up   20.53 us  4872 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 32, {3, 5, 8, 16, 2, 0}},  // gate_up   32.85 us  3056 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 40, {1, 8, 10, 16, 1, 0}},  // gate_up   35.69 us  2819 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 64, {1, 5, 8, 16, 2, 0}},  // gate_up   56.95 us  1777 GB/s
+    {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
+    {SK_OP_GEMM, 2560, 9728, 2, {2, 2, 10, 2, 1, 0}},  // down      13.01 us  3831 GB/s
+    {SK_OP_GEMM, 2560, 9728, 4, {2, 4, 5, 2, 1, 0}},  // down      12.89 us  3870 GB/s
+    {SK_OP_GEMM, 2560, 9728, 8, {3, 7, 16, 32, 3, 0}},  // down      14.74 us  3393 GB/s
+    {SK_OP_GEMM, 2560, 9728, 16, {3, 13, 8, 16, 3, 0}},  // down      16.79 us  2990 GB/s
+    {SK_OP_GEMM, 2560, 9728, 32, {3, 7, 16, 16, 3, 0}},  // down      23.23 us  2178 GB/s
+    {SK_OP_GEMM, 2560, 9728, 40, {1, 16, 5, 16, 4, 0}},  // down      26.15 us  1942 GB/s
+    {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 16, 5, 0}},  // down      36.59 us  1404 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 5, 16, 16, 1, 0}},  // lm_head  114.77 us  6778 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 4, {3, 10, 8, 16, 1, 0}},  // lm_head  114.94 us  6768 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 8, {3, 10, 8, 16, 1, 0}},  // lm_head  115.46 us  6738 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 16, {3, 5, 16, 16, 1, 0}},  // lm_head  115.83 us  6717 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 32, {3, 5, 16, 16, 1, 0}},  // lm_head  119.79 us  6495 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 40, {1, 8, 10, 16, 1, 0}},  // lm_head  160.11 us  4860 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {1, 8, 10, 16, 1, 0}},  // lm_head  190.38 us  4088 GB/s
+};
+
+// Tuned entry for op/N/K at the smallest tuned row count >= M (rows beyond
+// 64 run in 64-row chunks).  The lm_head logits GEMM shares the fused
+// argmax entries.
+const Tuned* tuned_lookup(int op, int M, int N, int K) {
+  for (int pass = 0; pass < 2; ++pass) {
+    const int want = pass == 0 ? op : (op == SK_OP_GEMM ? SK_OP_LM_ARGMAX : -1);
+    if (want < 0) break;
+    const Tuned* best = nullptr;
+    for (const Tuned& t : kTuned)
+      if (t.op == want && t.N == N && t.K == K && t.M >= M && (!best || t.M < best->M)) best = &t;
+    if (best) return best;
+  }
+  return nullptr;
+}
+
+// Heuristic for shapes outside the table: VALU GEMV for M <= 4 when K is a
+// multiple of 512; otherwise the LDS-transposed MFMA path with one K chunk per
+// wave and the fewest global splits that keep the waves within the compiled
+// register budget; the register-fragment MFMA path as a last resort.
+int heuristic_config(int op, int M, int N, int K, sk_config* out) {
+  const bool gateup = (op == SK_OP_GATEUP);
+  sk_config c;
+  memset(&c, 0, sizeof(c));
+  Plan pl;
+  if (M <= 4 && op != SK_OP_LM_ARGMAX) {
+    const int units = cdiv(K, 512);
+    c.path = SK_PATH_GEMV;
+    c.rows = 2;
+    c.split = 1;
+    c.waves = units < 4 ? units : 4;
+    c.ku = cdiv(units, c.waves);
+    if (plan_shape(op, M, N, K, c, &pl) == SK_OK && pl.lds <= kPrefLds) {
+      *out = c;
+      return SK_OK;
+    }
+  }
+  const int MT = cdiv(M, 16);
+  for (int ku : {16, 8}) {
+    if (MT > 2 && ku == 16) continue;
+    const int KW = 32 * ku;
+    const int chunks = cdiv(K, KW);
+    for (int split = 1; split <= 16; ++split) {
+      if (op == SK_OP_LM_ARGMAX && split > 1) break;
+      const int waves = cdiv(chunks, split);
+      if (split > 1 && (split - 1) * waves >= chunks) break;
+      c.path = SK_PATH_MFMA_LDS;
+      c.rows = 16;
+      c.split = split;
+      c.waves = waves;
+      c.ku = ku;
+      if (plan_shape(op, M, N, K, c, &pl) == SK_OK && pl.lds <= kMaxLds) {
+        *out = c;
+        return SK_OK;
+      }
+    }
+  }
+  (void)gateup;
+  return SK_ERR_SHAPE;
+}
+
+int mfma_search_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   (void)num_cu;   // the table is tuned for the MI355X's 256 CUs
   if (M < 1 || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
   if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
@@ -250,6 +383,21 @@ int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   return SK_ERR_SHAPE;
 }
 
+int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
+  if (M < 1 || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
+  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+  const int Mk = M > kMaxM ? kMaxM : M;
+  Plan pl;
+  if (const Tuned* t = tuned_lookup(op, Mk, N, K)) {
+    if (plan_shape(op, Mk, N, K, t->cfg, &pl) == SK_OK) {
+      *out = t->cfg;
+      return SK_OK;
+    }
+  }
+  if (heuristic_config(op, Mk, N, K, out) == SK_OK) return SK_OK;
+  return mfma_search_config(op, M, N, K, num_cu, out);
+}
+
 int resolve_config(int op, int M, int N, int K, const sk_config* cfg, sk_config* out) {
   if (cfg) {
     *out = *cfg;
@@ -266,8 +414,10 @@ int resolve_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
 
 // Bind the kernel instance and compute the launch grid.
 int bind_plan(Plan* pl, int num_cu, int* grid) {
-  sk::KernelFn fn = (pl->cfg.path == SK_PATH_MFMA) ? sk::mfma_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku)
-                                                    : sk::gemv_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
+  sk::KernelFn fn = nullptr;
+  if (pl->cfg.path == SK_PATH_MFMA) fn = sk::mfma_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
+  else if (pl->cfg.path == SK_PATH_MFMA_LDS) fn = sk::mfmt_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
+  else fn = sk::gemv_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
   if (!fn) return SK_ERR_CONFIG;
   FnInfo fi;
   int st = fn_info(reinterpret_cast<const void*>(fn), &fi);
@@ -289,14 +439,16 @@ int bind_plan(Plan* pl, int num_cu, int* grid) {
     int per_split = pl->nrb < cap ? pl->nrb : (int)cap;
     if (per_split > kMaxGrid) per_split = kMaxGrid;
     int tiles_per = cdiv(pl->nrb, per_split);
-    if (pl->epi != sk::EPI_ARGMAX)
-      while (tiles_per > 1 && pl->parts_lds + (size_t)tiles_per * pl->stage_elem > kPrefLds) --tiles_per;
+    if (pl->epi != sk::EPI_ARGMAX) {
+      const size_t budget = pl->pre_lds + pl->parts_lds > kPrefLds ? kMaxLds : kPrefLds;
+      while (tiles_per > 1 && plan_lds(*pl, 0, tiles_per) > budget) --tiles_per;
+    }
     per_split = cdiv(pl->nrb, tiles_per);
     if (per_split > kMaxGrid) return SK_ERR_CONFIG;
     *grid = per_split * S;
   }
   const int tiles_per = cdiv(pl->nrb, *grid / S);
-  pl->lds = pl->epi == sk::EPI_ARGMAX ? pl->lds : pl->parts_lds + (size_t)tiles_per * pl->stage_elem;
+  pl->lds = pl->epi == sk::EPI_ARGMAX ? pl->lds : plan_lds(*pl, 0, tiles_per);
   if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
   if (pl->lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -1,0 +1,37 @@
+// LDS-transposed MFMA kernel instances for one epilogue (-DSK_EPI=<0..4>).
+#include "sk_registry.hpp"
+
+#ifndef SK_EPI
+#error "build with -DSK_EPI=<epilogue id>"
+#endif
+
+#define SK_CAT2(a, b) a##b
+#define SK_CAT(a, b) SK_CAT2(a, b)
+
+namespace sk {
+
+template <int MT, int NT, int KW, int EPI>
+__global__ void __launch_bounds__(64 * max_waves_for_regs(mfmt_regs(MT, NT, KW)))
+mfmt_entry(Args p) {
+  mfmt_body<MT, NT, KW, EPI>(p);
+}
+
+#define SK_C(MT, NT, KW) \
+  case MT * 100000 + NT * 1000 + KW: return &mfmt_entry<MT, NT, KW, SK_EPI>;
+#define SK_LIST(NT) \
+  SK_C(1, NT, 512) SK_C(2, NT, 512) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(3, NT, 256) SK_C(4, NT, 256)
+
+KernelFn SK_CAT(mfmt_for_epi, SK_EPI)(int MT, int NT, int KW) {
+  switch (MT * 100000 + NT * 1000 + KW) {
+#if SK_EPI == 1 || SK_EPI == 4   // gate/up: 16 gate rows + 16 up rows
+    SK_LIST(2)
+#else
+    SK_LIST(1)
+    SK_LIST(2)
+#endif
+    default: break;
+  }
+  return nullptr;
+}
+
+}  // namespace sk

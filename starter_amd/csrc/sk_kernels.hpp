@@ -476,6 +476,180 @@ __device__ __forceinline__ void mfma_body(Args p) {
 }
 
 // ---------------------------------------------------------------------------
+// MFMA path with LDS-transposed weight rows ("rows through LDS").
+//   MT : activation row tiles of 16 (M <= 16*MT)
+//   NT : weight row tiles of 16 per workgroup tile (gate/up: 2 = gate + up)
+//   KW : K columns per wave (512 or 256): one K chunk per wave per slice
+// A wave streams its chunk of every tile row with the GEMV access pattern
+// (one load instruction = 1 KiB contiguous of one row for KW = 512, or
+// 512 B of each of two rows for KW = 256), writes the rows into a
+// wave-private LDS region (row pitch 2*KW + 16 bytes: the 16 rows a
+// fragment read touches fall on distinct banks), and reads them back as
+// MFMA A fragments (lane: row l%16, 8 columns at 8*(l/16)).  The next tile's
+// rows are loaded into registers while the current tile is multiplied.
+// ---------------------------------------------------------------------------
+template <int MT, int NT, int KW, int EPI>
+__device__ __forceinline__ void mfmt_body(Args p) {
+  constexpr bool GATEUP = EpiTraits<EPI>::gateup;
+  constexpr int ROWS = 16 * NT;                  // weight rows per tile
+  constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
+  constexpr int UNITS = KW / 32;                 // MFMA K steps per wave
+  constexpr int LPR = KW / 8;                    // lanes per row in a load instruction
+  constexpr int RPI = 64 / LPR;                  // rows per load instruction
+  constexpr int NLD = ROWS / RPI;                // load instructions per tile (all NT row tiles)
+  constexpr int PASSES = KW / 256;               // a 512-column chunk is staged in two halves
+  constexpr int PITCH = 2 * 256 + 16;            // LDS bytes per staged row (256 columns)
+  static_assert(KW == 512 || KW == 256, "one or two rows per load instruction");
+  static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
+
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = p.nw;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int M = p.M;
+
+  const int S = p.S;
+  const int slice = blockIdx.x % S;
+  const int rbstep = p.rbstep;
+  const int rb0 = blockIdx.x / S;
+  const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
+  const int chunks = (p.K + KW - 1) / KW;
+  const int c_lo = slice * p.slice_units;
+  const int c_hi = min(c_lo + p.slice_units, chunks);
+  const int chunk = c_lo + wave;                        // this wave's K chunk
+  const bool has_chunk = chunk < c_hi;                  // wave-uniform
+  const int k0 = min(chunk, chunks - 1) * KW;
+
+  // Wave-private staging of 16 rows x 256 columns; the NT row tiles (and the
+  // two halves of a 512-column chunk) pass through it in turn.
+  char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
+  float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
+  const int part_floats = nw * M * ROWS;
+  void* stage = parts + 2 * part_floats;
+  unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
+  if constexpr (EPI == EPI_ARGMAX) {
+    if (tid < M) lds_best[tid] = 0ull;
+  }
+
+  // Activation fragments of this chunk: lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8];
+  // zero for rows >= M, columns >= K and waves without a chunk.
+  bf16x8 af[MT][UNITS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + r16;
+    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda;
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      const int k = k0 + 32 * u + 8 * g4;
+      u32x4 v = ld16(ap + min(k, p.K - 8));
+      if (m >= M || k >= p.K || !has_chunk) v = u32x4{0u, 0u, 0u, 0u};
+      af[mt][u] = __builtin_bit_cast(bf16x8, v);
+    }
+  }
+
+  // Load instruction i covers tile rows i*RPI + lane/LPR, columns k0 + 8*(lane%LPR).
+  const int lrow = lane / LPR;
+  const int lcol = min(k0 + 8 * (lane % LPR), p.K - 8);
+  (void)lrow;
+  auto wsrc = [&](int rb, int i) -> const uint16_t* {
+    const int t = i * RPI + lrow;             // row within the tile
+    if constexpr (GATEUP) {
+      const int row = min(rb * 16 + (t & 15), p.N - 1);
+      return (t < 16 ? p.W0 : p.W1) + (int64_t)row * p.ldw + lcol;
+    } else {
+      const int row = min(rb * ROWS + t, p.N - 1);
+      return p.W0 + (int64_t)row * p.ldw + lcol;
+    }
+  };
+  // Staging address of this lane's 16 bytes.  Every staged register holds 256
+  // columns of two rows (lanes 0-31: row 2j, lanes 32-63: row 2j+1): a
+  // KW = 256 load already has that layout; for KW = 512 (one 512-column row
+  // per load) v_permlane32_swap of rows 2j and 2j+1 produces it, one register
+  // for columns 0-255 and one for 256-511, so every staging store is
+  // unconditional.
+  char* const wdst = tr + (lane >> 5) * PITCH + 16 * (lane & 31);
+  constexpr int NLD16 = 16 / RPI;                 // load instructions per 16-row tile
+
+  u32x4 wf[NLD];
+  if (ntiles > 0) {
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) wf[i] = ld16_stream(wsrc(rb0, i));
+  }
+
+  auto tile = [&](int j, auto prefetch) {
+    constexpr bool PF = decltype(prefetch)::value;
+    const int rb = rb0 + j * rbstep;
+    f32x4 acc[NT][MT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // Stage this 16-row tile (256 columns per pass) in LDS and read it back
+      // as MFMA fragments.  The region is private to the wave and the LDS
+      // accesses of one wave execute in order, so no barrier is needed.
+      u32x4 half[PASSES][8];   // [pass][row pair]: 256 columns of rows 2j, 2j+1
+#pragma unroll
+      for (int jp = 0; jp < 8; ++jp) {
+        if constexpr (KW == 256) {
+          half[0][jp] = wf[nt * NLD16 + jp];
+        } else {
+          const u32x4 x = wf[nt * NLD16 + 2 * jp], y = wf[nt * NLD16 + 2 * jp + 1];
+          u32x4 lo, hi;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const auto r = __builtin_amdgcn_permlane32_swap(x[c], y[c], false, false);
+            lo[c] = r[0];
+            hi[c] = r[1];
+          }
+          half[0][jp] = lo;
+          half[PASSES - 1][jp] = hi;
+        }
+      }
+      if constexpr (PF) {   // the row registers are free: load the next tile's rows
+#pragma unroll
+        for (int i = 0; i < NLD16; ++i) wf[nt * NLD16 + i] = ld16_stream(wsrc(rb + rbstep, nt * NLD16 + i));
+      }
+#pragma unroll
+      for (int h = 0; h < PASSES; ++h) {
+#pragma unroll
+        for (int jp = 0; jp < 8; ++jp) *reinterpret_cast<u32x4*>(wdst + 2 * jp * PITCH) = half[h][jp];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const bf16x8 wv = *reinterpret_cast<const bf16x8*>(tr + r16 * PITCH + 64 * u + 16 * g4);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[mt][8 * h + u], acc[nt][mt], 0, 0, 0);
+        }
+      }
+    }
+    float* P = parts + (j & 1) * part_floats;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r16;
+        if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
+      }
+    lds_barrier();
+    tile_reduce<ROWS, EPI>(p, P, nw, rb, j, stage, lds_best);
+  };
+
+  int j = 0;
+  for (; j + 1 < ntiles; ++j) tile(j, std::integral_constant<bool, true>{});
+  if (ntiles > 0) tile(j, std::integral_constant<bool, false>{});
+  lds_barrier();
+  if constexpr (EPI == EPI_ARGMAX) {
+    argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
+  } else {
+    flush_stage<OUT_ROWS, EPI>(p, stage, ntiles, rb0, slice);
+    if constexpr (EPI == EPI_PART || EPI == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, EPI>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+  }
+}
+
+// ---------------------------------------------------------------------------
 // GEMV path (VALU).
 //   MR : compile-time bound on activation rows (M <= MR)
 //   R  : weight rows per tile (gate/up: R gate rows + R up rows)

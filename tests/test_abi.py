@@ -17,7 +17,7 @@ import pytest
 from starter_amd import _lib
 from starter_amd._lib import (SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_DEVICE, SK_ERR_NULL, SK_ERR_SHAPE, SK_ERR_WORKSPACE,
                               SK_OK, SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_PATH_GEMV,
-                              SK_PATH_MFMA, SkConfig)
+                              SK_PATH_MFMA, SK_PATH_MFMA_LDS, SkConfig)
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "starter_amd.h"
 QWEN = {"qkv": (SK_OP_GEMM, 6144, 2560), "o": (SK_OP_GEMM, 2560, 4096), "gu": (SK_OP_GATEUP, 9728, 2560),
@@ -54,17 +54,45 @@ def test_default_config_is_valid_for_every_decode_shape(name, M):
         pytest.skip("lm_argmax takes at most 64 rows per call")
     cfg = _lib.default_config(op, M, N, K)
     assert _lib.check_config(op, M, N, K, cfg) == SK_OK, cfg
-    # The wave count covers the K slice and the workspace exists only where needed.
-    units = K // 32
-    assert cfg.waves * cfg.ku * cfg.split >= units
+    # The waves cover K (per path: 32-column units, 512-column units, or one
+    # 32*ku-column chunk per wave) and the workspace exists only where needed.
+    if cfg.path == SK_PATH_MFMA:
+        assert cfg.waves * cfg.ku * cfg.split >= K // 32
+    elif cfg.path == SK_PATH_GEMV:
+        assert cfg.waves * cfg.ku * cfg.split >= -(-K // 512)
+    else:
+        assert cfg.path == SK_PATH_MFMA_LDS
+        assert cfg.waves * cfg.split >= -(-K // (32 * cfg.ku))
     ws = _lib.workspace_bytes(op, M, N, K, cfg)
     if op == SK_OP_LM_ARGMAX:
         assert ws == _tickets(1) + 8 * min(M, 64)
     elif cfg.split == 1:
         assert ws == 0
     else:
-        tiles = -(-N // 16)
+        # output columns per tile: 16 for MFMA gate/up (16 gate + 16 up rows), else `rows`
+        out_rows = 16 if (op == SK_OP_GATEUP and cfg.path != SK_PATH_GEMV) else cfg.rows
+        tiles = -(-N // out_rows)
         assert ws == _tickets(tiles) + (2 if op == SK_OP_GATEUP else 1) * cfg.split * min(M, 64) * N * 4
+
+
+def test_tuned_table_drives_the_decode_shapes():
+    """Measured winners: VALU GEMV at M = 1, LDS-transposed MFMA at M = 8."""
+    assert _lib.default_config(SK_OP_GEMM, 1, 6144, 2560).path == SK_PATH_GEMV
+    assert _lib.default_config(SK_OP_GEMM, 8, 6144, 2560).path == SK_PATH_MFMA_LDS
+    assert _lib.default_config(SK_OP_GATEUP, 8, 9728, 2560).as_dict() == \
+        {"path": SK_PATH_MFMA_LDS, "waves": 5, "ku": 16, "rows": 16, "split": 1, "grid": 0}
+    assert _lib.default_config(SK_OP_LM_ARGMAX, 8, 151936, 2560).path == SK_PATH_MFMA_LDS
+    # the lm_head logits GEMM shares the argmax entries; M = 5 takes the M = 8 entry
+    assert _lib.default_config(SK_OP_GEMM, 5, 151936, 2560).as_dict() == \
+        _lib.default_config(SK_OP_LM_ARGMAX, 8, 151936, 2560).as_dict()
+
+
+def test_heuristic_for_untuned_shapes():
+    assert _lib.default_config(SK_OP_GEMM, 2, 1536, 2560).path == SK_PATH_GEMV
+    c = _lib.default_config(SK_OP_GEMM, 24, 1536, 2560)
+    assert c.path == SK_PATH_MFMA_LDS and _lib.check_config(SK_OP_GEMM, 24, 1536, 2560, c) == SK_OK
+    c = _lib.default_config(SK_OP_GEMM, 8, 777, 96)        # K not a multiple of the chunk
+    assert _lib.check_config(SK_OP_GEMM, 8, 777, 96, c) == SK_OK
 
 
 def test_default_config_prefers_no_global_split_at_decode_m():

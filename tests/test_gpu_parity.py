@@ -21,7 +21,7 @@ import torch.nn.functional as F
 import oracle
 from starter_amd import kernels as K
 from starter_amd._lib import (SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_SHAPE, SK_ERR_WORKSPACE, SK_OP_GATEUP, SK_OP_GEMM,
-                              SK_PATH_GEMV, SK_PATH_MFMA, SkConfig, SkError)
+                              SK_PATH_GEMV, SK_PATH_MFMA, SK_PATH_MFMA_LDS, SkConfig, SkError)
 from tests._util import (BF16, assert_gateup_parity, assert_parity, bits, from_bits, randn_bf16,
                          reference_tolerance_ok)
 
@@ -111,6 +111,11 @@ GEMM_CONFIGS = [
     SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=8),
     SkConfig.make(SK_PATH_GEMV, waves=2, ku=3, rows=2),
     SkConfig.make(SK_PATH_GEMV, waves=1, ku=2, rows=4, split=3),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=16, rows=16),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=3, ku=16, rows=32, split=2),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=3, ku=16, rows=16, split=2),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=16, rows=16, grid=40),
 ]
 
 
@@ -175,6 +180,9 @@ GATEUP_CONFIGS = [
     SkConfig.make(SK_PATH_MFMA, waves=4, ku=10, rows=16, split=2),
     SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=4),
     SkConfig.make(SK_PATH_GEMV, waves=2, ku=3, rows=2),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=16, rows=16),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=8, rows=16, split=2),
+    SkConfig.make(SK_PATH_MFMA_LDS, waves=3, ku=16, rows=16, split=2),
 ]
 
 
@@ -221,15 +229,24 @@ def _check_argmax_rows(ids, maxv, logits_bits: np.ndarray, o_ids, o_maxv, what: 
             assert ids[m] == o_ids[m], f"{what}: row {m} tie not broken to the lowest index"
 
 
+LM_CONFIGS = {"default": None, "mfma_lds": SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=16, rows=16),
+              "gemv": SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=4)}
+
+
+@pytest.mark.parametrize("cfg", list(LM_CONFIGS))
 @pytest.mark.parametrize("M", [1, 8, 32, 64])
-def test_lm_argmax_full_vocab(M):
+def test_lm_argmax_full_vocab(M, cfg):
+    if cfg == "gemv" and M > 8:
+        pytest.skip("the GEMV path takes at most 8 rows")
+    if cfg == "mfma_lds" and M > 32:
+        pytest.skip("no unsplit LDS-path instance for 64 rows (argmax cannot split K)")
     V, Kd = LM
     w = _weights(V, Kd, seed=7)
     x = _acts(M, Kd, seed=11)
-    ids, maxv = K.lm_argmax(x.to(DEV), _gpu(w))
+    ids, maxv = K.lm_argmax(x.to(DEV), _gpu(w), config=LM_CONFIGS[cfg])
     logits = oracle.gemm(bits(x), bits(w))
     o_ids, o_maxv = oracle.argmax(logits)
-    _check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax M={M}")
+    _check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax M={M} {cfg}")
 
 
 def test_lm_argmax_exact_ties_across_workgroups():
@@ -408,3 +425,46 @@ def test_workspace_counters_reset_between_calls():
     for _ in range(3):
         ids, _ = K.argmax(L, ws=ws)
         assert torch.equal(ids.cpu(), torch.argmax(L.cpu(), -1))
+
+
+MFMT_CASES = {  # shape, K-chunk units (16: 512 columns, 8: 256), rows, global split
+    "qkv": (QKV, 16, 16, 1),
+    "o_proj": (O, 16, 16, 1),
+    "down": (D, 16, 16, 3),
+    "qkv_kw256_rows32": (QKV, 8, 32, 2),
+}
+
+
+def mfmt_config(Kd: int, ku: int, rows: int, split: int, M: int) -> SkConfig:
+    """One K chunk per wave; above 32 rows use 256-column chunks and enough
+    splits that at most 8 waves share a tile."""
+    if M > 32:
+        ku, rows = 8, 16
+        split = max(split, 1)
+        while -(-(Kd // 256) // split) > 8:
+            split += 1
+    chunks = -(-Kd // (32 * ku))
+    return SkConfig.make(SK_PATH_MFMA_LDS, waves=-(-chunks // split), ku=ku, rows=rows, split=split)
+
+
+@pytest.mark.parametrize("case", list(MFMT_CASES))
+@pytest.mark.parametrize("M", [1, 8, 16, 40, 64])
+def test_mfma_lds_path_qwen_shapes(case, M):
+    (N, Kd), ku, rows, split = MFMT_CASES[case]
+    cfg = mfmt_config(Kd, ku, rows, split, M)
+    w = _weights(N, Kd, seed=N + Kd)
+    x = _acts(M, Kd, seed=N)
+    out = K.gemm(x.to(DEV), _gpu(w), config=cfg)
+    assert_parity(out, _oracle_gemm(x, w), f"mfma_lds {case} M={M} {cfg}")
+
+
+@pytest.mark.parametrize("M", [1, 8, 40])
+def test_mfma_lds_path_gateup(M):
+    I2, Kd = GU
+    I = I2 // 2
+    wgu = _weights(I2, Kd, seed=17)
+    x = _acts(M, Kd, seed=17)
+    wd = _gpu(wgu)
+    cfg = mfmt_config(Kd, 16, 16, 1, M)
+    out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:], config=cfg)
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"mfma_lds gateup M={M}")
