@@ -170,6 +170,17 @@ class Workload:
         return statistics.median(t) * 1000.0 / launches
 
 
+def _cpu_model() -> str:
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
 def cpu_baseline(M: int, samples: int) -> dict:
     """The reference's own CPU path for one step: torch F.linear (bf16 in,
     fp32 accumulate, bf16 out; engine/kernels/gemm.py:527 `a @ w.t()`) for QKV,
@@ -204,18 +215,124 @@ def cpu_baseline(M: int, samples: int) -> dict:
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
     step_bytes = sum(alg_bytes(n, M) for n in ("qkv", "o_proj", "gate_up", "down"))
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    cpu = _cpu_model()
     return {"value": round(step_bytes / t / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "reference",
             "sample": f"{samples} steps (median) of the M={M} layer workload via torch F.linear/F.silu on CPU "
                       f"(the reference's a @ w.t() baseline path), {t * 1e3:.2f} ms/step, {cpu}"}
+
+
+def cpu_port(M: int, samples: int) -> dict:
+    """The CPU restatement of the hot path (oracle/, kind "port": plain C,
+    fp32 accumulation, OpenMP over output rows) timed on this box's host
+    cores for the same layer step: QKV, o_proj, gate_up+SwiGLU and down at
+    M rows.  Median of `samples` steps after one warmup.  The reference's
+    own path is Triton on a GPU and has no CPU build to time."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0)
+
+    def bits(*shape, scale=1.0):
+        return oracle.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32) * scale)
+
+    w = {n: bits(N, K, scale=0.02) for n, (N, K, k) in SHAPES.items() if k == "gemm"}
+    wg, wu = bits(9728, 2560, scale=0.02), bits(9728, 2560, scale=0.02)
+    x, attn, act = bits(M, 2560), bits(M, 4096), bits(M, 9728)
+
+    def step():
+        oracle.gemm(x, w["qkv"])
+        oracle.gemm(attn, w["o_proj"])
+        oracle.gateup_swiglu(x, wg, wu)
+        oracle.gemm(act, w["down"])
+
+    step()
+    ts = []
+    for _ in range(samples):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    step_bytes = sum(alg_bytes(n, M) for n in ("qkv", "o_proj", "gate_up", "down"))
+    cpu = _cpu_model()
+    return {"value": round(step_bytes / t / 1e9, 2), "unit": "GB/s", "cores": oracle.threads(),
+            "kind": "port",
+            "sample": f"{samples} steps (median) of the M={M} layer workload (qkv, o_proj, gate_up+swiglu, down) "
+                      f"through the C oracle, {t * 1e3:.2f} ms/step, {oracle.threads()} OpenMP threads, {cpu}"}
+
+
+PROBE_LAUNCHES = 24
+PROBE_COPY_BYTES = 512 << 20
+
+
+def probe(M: int) -> int:
+    """Untimed launches for the hardware-counter passes: PROBE_LAUNCHES
+    gate_up+SwiGLU launches at M rows over 12 rotating layers (1.2 GB of
+    weights, so no launch finds its weights in the MALL), then three copies of
+    PROBE_COPY_BYTES with torch's copy kernel as the calibration of known size."""
+    import torch
+
+    wl = Workload(12, M)
+    wl.launch("gate_up", 0)
+    torch.cuda.synchronize()
+    log(f"probe: {PROBE_LAUNCHES} gate_up launches at M={M}")
+    for i in range(PROBE_LAUNCHES):
+        wl.launch("gate_up", i % wl.L)
+    torch.cuda.synchronize()
+    src = torch.empty(PROBE_COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    log(f"probe: 3 copies of {PROBE_COPY_BYTES} bytes")
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log("probe: done")
+    return 0
+
+
+def _counter_rows(folder: str, counter: str) -> list[tuple[str, float]]:
+    """(kernel name, counter value) per dispatch, in dispatch order, from
+    rocprofv3's counter_collection.csv under folder."""
+    import csv
+
+    files = sorted(Path(folder).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {folder}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name") == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    return [(n, v) for _, n, v in sorted(rows)]
+
+
+def traffic_summary(fetch_dir: str, write_dir: str, M: int) -> int:
+    """HBM bytes per gate_up launch from FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch), each scaled by copy_bytes / (what the counter reads for the
+    PROBE_COPY_BYTES copy), written next to the profiles it came from."""
+    out = {"M": M, "copy_bytes": PROBE_COPY_BYTES}
+    total = 0.0
+    for key, folder, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        rows = _counter_rows(folder, counter)
+        gu = [v for n, v in rows if "sk::" in n]   # the probe launches no other library kernel
+        cp = [v for n, v in rows if "copy" in n.lower()][-3:]   # the probe ends with its three copies
+        if not gu or not cp:
+            raise SystemExit(f"{counter}: gate_up dispatches {len(gu)}, copy dispatches {len(cp)} in {folder}")
+        gu = gu[1:] if len(gu) > 1 else gu     # first launch warms code and workspace
+        kib = statistics.median(gu)
+        copy_kib = statistics.median(cp)
+        factor = (PROBE_COPY_BYTES / 1024.0) / copy_kib
+        out[key] = {"counter": counter, "kib_per_launch": kib, "copy_kib": copy_kib, "factor": round(factor, 4),
+                    "bytes_per_launch": round(kib * 1024.0 * factor)}
+        total += kib * 1024.0 * factor
+    out["hbm_bytes_per_launch"] = round(total)
+    out["algorithmic_bytes_per_launch"] = alg_bytes("gate_up", M)
+    out["ratio"] = round(total / alg_bytes("gate_up", M), 4)
+    path = ROOT / "profiles" / f"traffic_gate_up_m{M}.json"
+    path.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return 0
 
 
 def main() -> int:
@@ -228,7 +345,14 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time all five shapes at M in 1..64 (BASELINE config 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-samples", type=int, default=20)
+    ap.add_argument("--probe", action="store_true",
+                    help="launch gate_up at --M (untimed) and a 512 MiB copy, for rocprofv3 --pmc passes")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc output folders of --probe (FETCH_SIZE, WRITE_SIZE) into "
+                         "profiles/traffic_gate_up_m<M>.json and exit")
     args = ap.parse_args()
+    if args.traffic_from:
+        return traffic_summary(args.traffic_from[0], args.traffic_from[1], args.M)
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures the single-GPU hot path "
@@ -249,6 +373,8 @@ def main() -> int:
         log("no ROCm GPU visible")
         return 1
     torch.cuda.set_device(0)
+    if args.probe:
+        return probe(args.M)
     log(f"device {torch.cuda.get_device_name(0)}; building workload (36 layers of weights)")
     wl = Workload(args.layers, args.M)
 
@@ -303,8 +429,8 @@ def main() -> int:
 
     dom = per_gemm["gate_up"][f"M{args.M}"]
     traffic = None
-    tfile = ROOT / "profiles" / "traffic_gate_up_m8.json"
-    if tfile.exists() and args.M == 8:
+    tfile = ROOT / "profiles" / f"traffic_gate_up_m{args.M}.json"
+    if tfile.exists():
         try:
             traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
         except (OSError, ValueError):
@@ -314,10 +440,12 @@ def main() -> int:
                 "kernel": f"gate_up+swiglu M={args.M} ({alg_bytes('gate_up', args.M)} algorithmic bytes/launch, "
                           f"{dom['us']} us/launch)"}
 
-    cpu = None
+    cpu = port = None
     if not args.no_cpu:
         log("timing the CPU baseline")
         cpu = cpu_baseline(args.M, args.cpu_samples)
+        log("timing the C oracle on the CPU")
+        port = cpu_port(args.M, max(3, args.cpu_samples // 4))
 
     line = {
         "metric": METRIC,
@@ -339,6 +467,7 @@ def main() -> int:
                    "frac_peak_hbm": round(value / PEAK_HBM_GBS, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_port": port,
         "per_gemm": per_gemm,
     }
     if sweep is not None:

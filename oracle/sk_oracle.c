@@ -49,6 +49,30 @@ static float dot_bf16(const uint16_t* a, const uint16_t* w, int K) {
   return ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
 }
 
+/* dot_bf16 of one weight row against rows m0..m0+mc-1 of A (mc <= 16), with
+ * exactly dot_bf16's operation order per output; the weight row is converted
+ * once per 8 columns and shared by the rows (cache reuse only). */
+#define DOT_MC 16
+static void dot_rows_bf16(const uint16_t* A, int64_t lda, int mc, const uint16_t* w, int K, float* out) {
+  float p[DOT_MC][8];
+  for (int m = 0; m < mc; ++m)
+    for (int j = 0; j < 8; ++j) p[m][j] = 0.0f;
+  int k = 0;
+  for (; k + 8 <= K; k += 8) {
+    float wf[8];
+    for (int j = 0; j < 8; ++j) wf[j] = bf2f(w[k + j]);
+    for (int m = 0; m < mc; ++m) {
+      const uint16_t* a = A + (int64_t)m * lda + k;
+      for (int j = 0; j < 8; ++j) p[m][j] += bf2f(a[j]) * wf[j];
+    }
+  }
+  for (int m = 0; m < mc; ++m) {
+    const uint16_t* a = A + (int64_t)m * lda;
+    for (int kk = k, j = 0; kk < K; ++kk, ++j) p[m][j] += bf2f(a[kk]) * bf2f(w[kk]);
+    out[m] = ((p[m][0] + p[m][1]) + (p[m][2] + p[m][3])) + ((p[m][4] + p[m][5]) + (p[m][6] + p[m][7]));
+  }
+}
+
 /* bf16 round of fp32 value (exported for the tests' rounding checks). */
 uint16_t oracle_f32_to_bf16(float f) { return f2bf(f); }
 
@@ -58,7 +82,12 @@ void oracle_gemm_f32(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t 
                      int threads) {
 #pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
   for (int n = 0; n < N; ++n)
-    for (int m = 0; m < M; ++m) C[(int64_t)m * N + n] = dot_bf16(A + (int64_t)m * lda, W + (int64_t)n * ldw, K);
+    for (int m0 = 0; m0 < M; m0 += DOT_MC) {
+      const int mc = M - m0 < DOT_MC ? M - m0 : DOT_MC;
+      float d[DOT_MC];
+      dot_rows_bf16(A + (int64_t)m0 * lda, lda, mc, W + (int64_t)n * ldw, K, d);
+      for (int m = 0; m < mc; ++m) C[(int64_t)(m0 + m) * N + n] = d[m];
+    }
 }
 
 /* C = bf16(A @ W^T): SkinnyMatmul (gemm.py:98-99, 104-112) and `a @ w.t()`. */
@@ -66,8 +95,12 @@ void oracle_gemm_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, int64_t
                       int N, int K, int threads) {
 #pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
   for (int n = 0; n < N; ++n)
-    for (int m = 0; m < M; ++m)
-      C[(int64_t)m * ldc + n] = f2bf(dot_bf16(A + (int64_t)m * lda, W + (int64_t)n * ldw, K));
+    for (int m0 = 0; m0 < M; m0 += DOT_MC) {
+      const int mc = M - m0 < DOT_MC ? M - m0 : DOT_MC;
+      float d[DOT_MC];
+      dot_rows_bf16(A + (int64_t)m0 * lda, lda, mc, W + (int64_t)n * ldw, K, d);
+      for (int m = 0; m < mc; ++m) C[(int64_t)(m0 + m) * ldc + n] = f2bf(d[m]);
+    }
 }
 
 /* _swiglu_epilogue (gemm.py:115-121) / _swiglu_kernel (swiglu.py:21-24):
@@ -94,10 +127,12 @@ void oracle_gateup_swiglu_bf16(const uint16_t* A, int64_t lda, const uint16_t* W
                                uint16_t* out, int64_t ldo, int M, int I, int K, int threads) {
 #pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
   for (int n = 0; n < I; ++n)
-    for (int m = 0; m < M; ++m) {
-      const float g = dot_bf16(A + (int64_t)m * lda, Wg + (int64_t)n * ldw, K);
-      const float u = dot_bf16(A + (int64_t)m * lda, Wu + (int64_t)n * ldw, K);
-      out[(int64_t)m * ldo + n] = swiglu_bf(g, u);
+    for (int m0 = 0; m0 < M; m0 += DOT_MC) {
+      const int mc = M - m0 < DOT_MC ? M - m0 : DOT_MC;
+      float g[DOT_MC], u[DOT_MC];
+      dot_rows_bf16(A + (int64_t)m0 * lda, lda, mc, Wg + (int64_t)n * ldw, K, g);
+      dot_rows_bf16(A + (int64_t)m0 * lda, lda, mc, Wu + (int64_t)n * ldw, K, u);
+      for (int m = 0; m < mc; ++m) out[(int64_t)(m0 + m) * ldo + n] = swiglu_bf(g[m], u[m]);
     }
 }
 
