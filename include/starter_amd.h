@@ -57,7 +57,10 @@ typedef enum sk_op {
   SK_OP_GEMM = 0,         /* C = A @ W^T                                  */
   SK_OP_GATEUP = 1,       /* Out = swiglu(A @ Wg^T, A @ Wu^T)             */
   SK_OP_LM_ARGMAX = 2,    /* ids/maxv = argmax_n bf16(A @ W^T)[m, n]      */
-  SK_OP_ARGMAX = 3        /* ids/maxv = argmax over given bf16 logits     */
+  SK_OP_ARGMAX = 3,       /* ids/maxv = argmax over given bf16 logits     */
+  SK_OP_RMSNORM_GEMM = 4,       /* SK_OP_GEMM with A = rmsnorm(x + y)      */
+  SK_OP_RMSNORM_GATEUP = 5,     /* SK_OP_GATEUP with A = rmsnorm(x + y)    */
+  SK_OP_RMSNORM_LM_ARGMAX = 6   /* SK_OP_LM_ARGMAX with A = rmsnorm(x + y) */
 } sk_op;
 
 typedef enum sk_path {
@@ -159,6 +162,36 @@ int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, flo
 int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, float eps,
                         sk_bf16* xout, sk_bf16* out, int M, int K, int64_t ld,
                         hipStream_t stream);
+
+/*
+ * Residual add + RMSNorm fused in front of a projection: the call sites
+ * mm["qkv"](x, y, w_norm, xout, w), mm["gu"](...) and mm["lm"](...)
+ * (engine/model.py:202-210, built by pick_normed, engine/kernels/gemm.py:
+ * 602-660; prologue _norm_stats/_normed_tile gemm.py:28-56 and
+ * _row_rstd/_normed_row gemm.py:184-208).
+ *   xout = bf16(x + y)                                  (written, bit-exact)
+ *   A    = bf16(w_norm * bf16(xout * rstd)),  rstd = 1/sqrt(mean(xout^2) + eps)
+ * then the projection of A exactly as sk_gemm_bf16 / sk_gateup_swiglu_bf16 /
+ * sk_lm_argmax_bf16.  x, y and xout are [M, K] with row stride ldx; w_norm is
+ * [K].  xout must not overlap x or y, and the outputs must not overlap x, y
+ * or xout.  With a one-split configuration of the LDS-fed MFMA or GEMV path
+ * the prologue runs inside the projection kernel (each workgroup normalises
+ * the activation columns it loads; workgroup 0 writes xout); otherwise a
+ * separate add+norm kernel writes A into the workspace first.  Query the
+ * workspace with SK_OP_RMSNORM_* ops.
+ */
+int sk_rmsnorm_gemm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps, sk_bf16* xout,
+                         int64_t ldx, const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N, int K,
+                         const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+int sk_rmsnorm_gateup_swiglu_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps,
+                                  sk_bf16* xout, int64_t ldx, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw,
+                                  sk_bf16* Out, int64_t ldo, int M, int I, int K, const sk_config* cfg, void* ws,
+                                  size_t ws_bytes, hipStream_t stream);
+
+int sk_rmsnorm_lm_argmax_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps, sk_bf16* xout,
+                              int64_t ldx, const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M, int V,
+                              int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /* Out[M,I] = bf16(bf16(silu(g)) * u) for gu[M, 2I] = [g | u] (row stride ld_gu).
  * Replaces swiglu (engine/kernels/swiglu.py:14-33). */

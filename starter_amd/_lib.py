@@ -28,6 +28,9 @@ SK_OP_GEMM = 0
 SK_OP_GATEUP = 1
 SK_OP_LM_ARGMAX = 2
 SK_OP_ARGMAX = 3
+SK_OP_RMSNORM_GEMM = 4
+SK_OP_RMSNORM_GATEUP = 5
+SK_OP_RMSNORM_LM_ARGMAX = 6
 
 SK_PATH_AUTO = 0
 SK_PATH_MFMA = 1
@@ -39,6 +42,7 @@ EXPORTS = (
     "sk_version", "sk_strerror", "sk_default_config", "sk_check_config", "sk_workspace_bytes",
     "sk_gemm_bf16", "sk_gateup_swiglu_bf16", "sk_lm_argmax_bf16", "sk_argmax_bf16",
     "sk_add_rmsnorm_bf16", "sk_swiglu_bf16",
+    "sk_rmsnorm_gemm_bf16", "sk_rmsnorm_gateup_swiglu_bf16", "sk_rmsnorm_lm_argmax_bf16",
 )
 
 
@@ -94,6 +98,13 @@ _SIGNATURES = {
     "sk_argmax_bf16": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
     "sk_add_rmsnorm_bf16": (_i32, [_p, _p, _p, ctypes.c_float, _p, _p, _i32, _i32, _i64, _p]),
     "sk_swiglu_bf16": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p]),
+    # x, y, w_norm, eps, xout, ldx, then the projection's own arguments
+    "sk_rmsnorm_gemm_bf16": (_i32, [_p, _p, _p, ctypes.c_float, _p, _i64,
+                                    _p, _i64, _p, _i64, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
+    "sk_rmsnorm_gateup_swiglu_bf16": (_i32, [_p, _p, _p, ctypes.c_float, _p, _i64,
+                                             _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
+    "sk_rmsnorm_lm_argmax_bf16": (_i32, [_p, _p, _p, ctypes.c_float, _p, _i64,
+                                         _p, _i64, _p, _p, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
 }
 
 

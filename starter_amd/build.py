@@ -34,7 +34,8 @@ COMMON = [
     f"-I{ROOT / 'include'}", f"-I{CSRC}",
 ]
 
-N_EPI = 5  # EPI_STORE, EPI_SWIGLU, EPI_ARGMAX, EPI_PART, EPI_PART_GU
+N_EPI = 5       # EPI_STORE, EPI_SWIGLU, EPI_ARGMAX, EPI_PART, EPI_PART_GU
+NORM_EPIS = (5, 6, 7)   # the first three with the norm prologue (LDS-fed MFMA and GEMV only)
 
 
 def _units() -> list[tuple[Path, list[str], Path]]:
@@ -43,19 +44,34 @@ def _units() -> list[tuple[Path, list[str], Path]]:
         units.append((CSRC / "sk_inst_mfma.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfma_{epi}.o"))
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
         units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
+    for epi in NORM_EPIS:
+        units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
+        units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
     return units
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> list[tuple[str, int]]:
+    """Run one hipcc command; returns (kernel, VGPR spill count) of every
+    kernel whose resource-usage remark reports spilled registers."""
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    # hipcc's host pass warns about the device-only target feature; anything
-    # else is surfaced.
+    # hipcc's host pass warns about the device-only target feature and the
+    # resource-usage remarks are parsed, not printed; anything else is surfaced.
     noise = ("packed-fp32-ops", "warning: feature flag", "1 warning generated", "warnings generated")
+    spills, name = [], None
     for line in (r.stderr or "").splitlines():
+        if "kernel-resource-usage" in line:
+            if "Function Name:" in line:
+                name = line.split("Function Name:")[1].split("[")[0].strip()
+            elif "VGPRs Spill:" in line:
+                n = int(line.split("VGPRs Spill:")[1].split("[")[0])
+                if n:
+                    spills.append((name, n))
+            continue
         if line.strip() and not any(n in line for n in noise):
             print(line, file=sys.stderr)
+    return spills
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
@@ -69,14 +85,18 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
 
     def compile_one(u):
         src, defs, obj = u
-        cmd = [HIPCC, *COMMON, *defs, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *COMMON, *defs, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
-        _run(cmd)
-        return obj
+        return obj, _run(cmd)
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(compile_one, units))
+        done = list(ex.map(compile_one, units))
+    objs = [o for o, _ in done]
+    spilled = [s for _, sp in done for s in sp]
+    (BUILD / "spills.txt").write_text("".join(f"{n}\t{c}\n" for n, c in spilled))
+    if spilled:
+        print(f"note: {len(spilled)} kernel instances spill VGPRs (list in {BUILD / 'spills.txt'})", file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)

@@ -111,12 +111,25 @@ struct Plan {
   size_t parts_lds = 0;         // double-buffered fp32 partial tiles
   size_t stage_elem = 0;        // LDS bytes per staged tile (0: argmax keeps 8*M bytes)
   size_t lds = 0;               // total dynamic LDS (set once the grid is known)
+  bool norm = false;            // the op has the add + RMSNorm prologue
+  bool fused = false;           // ... and it runs inside the projection kernel
   sk::KernelFn fn = nullptr;
 };
 
+bool is_norm_op(int op) {
+  return op == SK_OP_RMSNORM_GEMM || op == SK_OP_RMSNORM_GATEUP || op == SK_OP_RMSNORM_LM_ARGMAX;
+}
+// The projection an op performs (the norm ops map to GEMM / GATEUP / LM_ARGMAX).
+int base_op(int op) { return is_norm_op(op) ? op - SK_OP_RMSNORM_GEMM : op; }
+bool is_gemm_family(int op) { return op == SK_OP_GEMM || op == SK_OP_GATEUP || op == SK_OP_LM_ARGMAX; }
+
+// The epilogue proper of an instance's epilogue id (the norm-prologue ids
+// 5..7 share the layout of 0..2).
+int epi_base(int epi) { return epi >= sk::EPI_STORE_NORM ? epi - sk::EPI_STORE_NORM : epi; }
+
 // Staged output bytes per element of each epilogue (see EpiTraits).
 size_t stage_bytes(int epi) {
-  switch (epi) {
+  switch (epi_base(epi)) {
     case sk::EPI_STORE: case sk::EPI_SWIGLU: return 2;
     case sk::EPI_PART: return 4;
     case sk::EPI_PART_GU: return 8;
@@ -126,7 +139,7 @@ size_t stage_bytes(int epi) {
 
 // Dynamic LDS of a plan whose workgroups each own at most tiles_per tiles.
 size_t plan_lds(const Plan& pl, int M, int tiles_per) {
-  if (pl.epi == sk::EPI_ARGMAX) return pl.pre_lds + pl.parts_lds + 8 * (size_t)M + 16;
+  if (epi_base(pl.epi) == sk::EPI_ARGMAX) return pl.pre_lds + pl.parts_lds + 8 * (size_t)M + 16;
   return pl.pre_lds + pl.parts_lds + (size_t)tiles_per * pl.stage_elem;
 }
 
@@ -142,15 +155,19 @@ int epi_for(int op, int split) {
   return sk::EPI_ARGMAX;
 }
 
-// Pure host logic: fills everything except fn/grid-from-occupancy.
-int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
-  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+// Pure host logic: fills everything except fn/grid-from-occupancy.  op is a
+// projection (GEMM / GATEUP / LM_ARGMAX); `fused` selects the instances with
+// the norm prologue.
+int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused, Plan* pl) {
+  if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   if (M < 1 || M > kMaxM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
   if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0) return SK_ERR_CONFIG;
   if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
   const bool gateup = (op == SK_OP_GATEUP);
+  if (fused && (c.split != 1 || (c.path != SK_PATH_GEMV && c.path != SK_PATH_MFMA_LDS))) return SK_ERR_CONFIG;
   pl->cfg = c;
-  pl->epi = epi_for(op, c.split);
+  pl->epi = epi_for(op, c.split) + (fused ? sk::EPI_STORE_NORM : 0);
+  pl->fused = fused;
   int units, partial_rows;
   if (c.path == SK_PATH_MFMA) {
     if (gateup ? c.rows != 16 : (c.rows != 16 && c.rows != 32)) return SK_ERR_CONFIG;
@@ -171,8 +188,10 @@ int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
     pl->tn = gateup ? 2 : c.rows / 16;
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
-    if (c.waves > sk::max_waves_for_regs(sk::mfmt_regs(pl->tm, pl->tn, KW))) return SK_ERR_CONFIG;
+    if (c.waves > sk::max_waves_for_regs(sk::mfmt_regs(pl->tm, pl->tn, KW, fused), fused)) return SK_ERR_CONFIG;
     pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
+    // Norm instances keep the norm weights (K bf16, 16-byte padded) in front.
+    if (fused) pl->pre_lds += ((size_t)2 * K + 15) & ~(size_t)15;
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
     if (M > 8) return SK_ERR_CONFIG;
@@ -181,7 +200,7 @@ int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
     pl->tn = c.rows;
     pl->tku = bucket(sk::kGemvKU, (int)(sizeof(sk::kGemvKU) / sizeof(int)), c.ku);
     partial_rows = gateup ? 2 * c.rows : c.rows;
-    if (c.waves > sk::max_waves_for_regs(sk::gemv_regs(pl->tm, partial_rows, pl->tku < 0 ? 10 : pl->tku)))
+    if (c.waves > sk::max_waves_for_regs(sk::gemv_regs(pl->tm, partial_rows, pl->tku < 0 ? 10 : pl->tku, fused), fused))
       return SK_ERR_CONFIG;
   } else {
     return SK_ERR_CONFIG;
@@ -208,6 +227,23 @@ int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
   return SK_OK;
 }
 
+// Plan of any GEMM-family op.  A norm op runs its prologue inside the
+// projection kernel when the configuration allows (one K split, LDS-fed MFMA
+// or GEMV path, a compiled norm instance within the wave limit), else as a
+// separate add+norm launch in front of the plain projection.
+int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
+  const bool norm = is_norm_op(op);
+  const int bop = base_op(op);
+  if (norm && c.split == 1 && (c.path == SK_PATH_GEMV || c.path == SK_PATH_MFMA_LDS) &&
+      plan_shape_impl(bop, M, N, K, c, true, pl) == SK_OK) {
+    pl->norm = true;
+    return SK_OK;
+  }
+  const int st = plan_shape_impl(bop, M, N, K, c, false, pl);
+  pl->norm = norm;
+  return st;
+}
+
 // Upper bound of the workgroups a plan launches (what the workspace covers).
 int grid_bound(const Plan& pl) {
   if (pl.cfg.grid > 0) return pl.cfg.grid;
@@ -220,6 +256,7 @@ int grid_bound(const Plan& pl) {
 size_t ticket_bytes(int n) { return (((size_t)n * sizeof(unsigned)) + 255) & ~(size_t)255; }
 
 size_t plan_workspace(int op, int M, int N, const Plan& pl) {
+  op = base_op(op);
   if (op == SK_OP_LM_ARGMAX) return ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
   if (pl.cfg.split > 1)
     return ticket_bytes(pl.nrb) + (size_t)(op == SK_OP_GATEUP ? 2 : 1) * pl.cfg.split * M * (size_t)N * sizeof(float);
@@ -385,7 +422,8 @@ int mfma_search_config(int op, int M, int N, int K, int num_cu, sk_config* out) 
 
 int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   if (M < 1 || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
-  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+  op = base_op(op);   // a norm op uses its projection's configuration
+  if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   const int Mk = M > kMaxM ? kMaxM : M;
   Plan pl;
   if (const Tuned* t = tuned_lookup(op, Mk, N, K)) {
@@ -439,7 +477,7 @@ int bind_plan(Plan* pl, int num_cu, int* grid) {
     int per_split = pl->nrb < cap ? pl->nrb : (int)cap;
     if (per_split > kMaxGrid) per_split = kMaxGrid;
     int tiles_per = cdiv(pl->nrb, per_split);
-    if (pl->epi != sk::EPI_ARGMAX) {
+    if (epi_base(pl->epi) != sk::EPI_ARGMAX) {
       const size_t budget = pl->pre_lds + pl->parts_lds > kPrefLds ? kMaxLds : kPrefLds;
       while (tiles_per > 1 && plan_lds(*pl, 0, tiles_per) > budget) --tiles_per;
     }
@@ -448,7 +486,7 @@ int bind_plan(Plan* pl, int num_cu, int* grid) {
     *grid = per_split * S;
   }
   const int tiles_per = cdiv(pl->nrb, *grid / S);
-  pl->lds = pl->epi == sk::EPI_ARGMAX ? pl->lds : plan_lds(*pl, 0, tiles_per);
+  pl->lds = epi_base(pl->epi) == sk::EPI_ARGMAX ? pl->lds : plan_lds(*pl, 0, tiles_per);
   if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
   if (pl->lds > 64 * 1024 &&
       hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -467,60 +505,142 @@ int launch_status() {
   return e == hipSuccess ? SK_OK : SK_ERR_LAUNCH;
 }
 
-// Shared driver of the three GEMM-family ops (rows beyond 64 are processed in
-// 64-row chunks, each streaming the weights once more).
-int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, const sk_bf16* W1, int64_t ldw,
-                    sk_bf16* C, int64_t ldc, int64_t* ids, float* maxv, int M, int N, int K, const sk_config* cfg,
-                    void* ws, size_t ws_bytes, hipStream_t stream) {
+// Residual add + RMSNorm prologue inputs of the norm ops (x is the A operand).
+struct NormIn {
+  const sk_bf16* y;
+  const sk_bf16* w;
+  float eps;
+  sk_bf16* xout;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Plans of one call: rows beyond 64 are processed in 64-row chunks (each
+// streaming the weights once more), so a call has at most two distinct
+// chunk sizes.  Also the workspace it needs: the plans' counters and partials,
+// then, when the norm prologue runs as its own launch, the normalised
+// activations [M, K] at offset `norm_off`.
+struct CallPlan {
+  Plan plans[2];
+  int chunk_rows[2] = {0, 0};
+  int nplans = 0;
+  size_t base_need = 0;
+  size_t norm_off = 0;
+  size_t need = 0;
+  bool fused = false;
+};
+
+int plan_call(int op, int M, int N, int K, const sk_config* cfg, CallPlan* cp) {
+  cp->chunk_rows[0] = M < kMaxM ? M : kMaxM;
+  cp->chunk_rows[1] = M % kMaxM;
+  cp->nplans = (M > kMaxM && (M % kMaxM) != 0) ? 2 : 1;
+  for (int i = 0; i < cp->nplans; ++i) {
+    sk_config c;
+    int st = resolve_config(op, cp->chunk_rows[i], N, K, cfg, &c);
+    if (st) return st;
+    st = plan_shape(op, cp->chunk_rows[i], N, K, c, &cp->plans[i]);
+    if (st) return st;
+  }
+  cp->fused = is_norm_op(op) && cp->plans[0].fused && (cp->nplans == 1 || cp->plans[1].fused);
+  if (is_norm_op(op) && !cp->fused) {   // every chunk then takes the separate prologue
+    for (int i = 0; i < cp->nplans; ++i) {
+      const sk_config c = cp->plans[i].cfg;
+      int st = plan_shape_impl(base_op(op), cp->chunk_rows[i], N, K, c, false, &cp->plans[i]);
+      if (st) return st;
+      cp->plans[i].norm = true;
+    }
+  }
+  cp->base_need = 0;
+  for (int i = 0; i < cp->nplans; ++i) {
+    const size_t n = plan_workspace(op, cp->chunk_rows[i], N, cp->plans[i]);
+    if (n > cp->base_need) cp->base_need = n;
+  }
+  cp->need = cp->base_need;
+  if (is_norm_op(op) && !cp->fused) {
+    cp->norm_off = align256(cp->base_need);
+    cp->need = cp->norm_off + (size_t)M * K * sizeof(sk_bf16);
+  }
+  return SK_OK;
+}
+
+// Shared driver of the GEMM-family ops.  nrm != nullptr: A is x and the
+// projection consumes rmsnorm(x + y) (op is then a SK_OP_RMSNORM_* op).
+int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, const sk_bf16* W0, const sk_bf16* W1,
+                    int64_t ldw, sk_bf16* C, int64_t ldc, int64_t* ids, float* maxv, int M, int N, int K,
+                    const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const int bop = base_op(op);
   if (M < 0 || N < 1 || K < 32) return SK_ERR_SHAPE;
   if (M == 0) return SK_OK;   // empty batch: nothing to read or write (pointers may be NULL)
-  if (!A || !W0 || (op == SK_OP_GATEUP && !W1)) return SK_ERR_NULL;
-  if (op == SK_OP_LM_ARGMAX ? (!ids || !maxv) : !C) return SK_ERR_NULL;
-  if ((K & 31) != 0 || lda < K || ldw < K || (op != SK_OP_LM_ARGMAX && ldc < N)) return SK_ERR_SHAPE;
+  if (!A || !W0 || (bop == SK_OP_GATEUP && !W1)) return SK_ERR_NULL;
+  if (bop == SK_OP_LM_ARGMAX ? (!ids || !maxv) : !C) return SK_ERR_NULL;
+  if (nrm && (!nrm->y || !nrm->w || !nrm->xout)) return SK_ERR_NULL;
+  if ((K & 31) != 0 || lda < K || ldw < K || (bop != SK_OP_LM_ARGMAX && ldc < N)) return SK_ERR_SHAPE;
+  if (nrm && K > sk::RMS_THREADS * 8 * sk::RMS_MAX_CHUNKS) return SK_ERR_SHAPE;
   if (!aligned16(A) || !aligned16(W0) || (W1 && !aligned16(W1)) || (lda & 7) || (ldw & 7)) return SK_ERR_ALIGN;
-  // Validate every chunk's plan before enqueuing anything.
-  Plan plans[2];
-  int chunk_rows[2] = {M < kMaxM ? M : kMaxM, M % kMaxM};
-  const int nplans = (M > kMaxM && (M % kMaxM) != 0) ? 2 : 1;
-  for (int i = 0; i < nplans; ++i) {
-    sk_config c;
-    int st = resolve_config(op, chunk_rows[i], N, K, cfg, &c);
-    if (st) return st;
-    st = plan_shape(op, chunk_rows[i], N, K, c, &plans[i]);
-    if (st) return st;
-    const size_t need = plan_workspace(op, chunk_rows[i], N, plans[i]);
-    if (need > 0 && (!ws || ws_bytes < need)) return SK_ERR_WORKSPACE;
+  if (nrm && (!aligned16(nrm->y) || !aligned16(nrm->w) || !aligned16(nrm->xout))) return SK_ERR_ALIGN;
+  if (bop == SK_OP_LM_ARGMAX && M > kMaxM) return SK_ERR_SHAPE;   // ids of one call come from one pass
+  // Outputs are written while other workgroups may still read the inputs.
+  const size_t a_bytes = ((size_t)(M - 1) * lda + K) * sizeof(sk_bf16);
+  const size_t c_bytes = bop == SK_OP_LM_ARGMAX ? 0 : ((size_t)(M - 1) * ldc + N) * sizeof(sk_bf16);
+  if (c_bytes && overlaps(C, c_bytes, A, a_bytes)) return SK_ERR_ALIAS;
+  if (nrm) {
+    if (overlaps(nrm->xout, a_bytes, A, a_bytes) || overlaps(nrm->xout, a_bytes, nrm->y, a_bytes))
+      return SK_ERR_ALIAS;
+    if (c_bytes && (overlaps(C, c_bytes, nrm->y, a_bytes) || overlaps(C, c_bytes, nrm->xout, a_bytes)))
+      return SK_ERR_ALIAS;
   }
-  if (op == SK_OP_LM_ARGMAX && M > kMaxM) return SK_ERR_SHAPE;   // ids of one call come from one pass
+  // Validate every chunk's plan and the workspace before enqueuing anything.
+  CallPlan cp;
+  int st = plan_call(op, M, N, K, cfg, &cp);
+  if (st) return st;
+  if (cp.need > 0 && (!ws || ws_bytes < cp.need)) return SK_ERR_WORKSPACE;
   int num_cu = 0;
-  int st = device_info(&num_cu);
+  st = device_info(&num_cu);
   if (st) return st;
   int grids[2];
-  for (int i = 0; i < nplans; ++i) {
-    st = bind_plan(&plans[i], num_cu, &grids[i]);
+  for (int i = 0; i < cp.nplans; ++i) {
+    st = bind_plan(&cp.plans[i], num_cu, &grids[i]);
     if (st) return st;
+  }
+  // Separate prologue: xout and the normalised rows (in the workspace) first.
+  const sk_bf16* Ause = A;
+  int64_t ldause = lda;
+  if (nrm && !cp.fused) {
+    sk_bf16* nb = reinterpret_cast<sk_bf16*>(static_cast<char*>(ws) + cp.norm_off);
+    sk::add_rmsnorm_kernel<<<dim3(M), dim3(sk::RMS_THREADS), 0, stream>>>(A, nrm->y, nrm->w, nrm->eps, nrm->xout, nb,
+                                                                         K, lda, K);
+    if ((st = launch_status())) return st;
+    Ause = nb;
+    ldause = K;
   }
   for (int m0 = 0; m0 < M; m0 += kMaxM) {
     const int rows = (M - m0) < kMaxM ? (M - m0) : kMaxM;
-    const Plan& pl = plans[rows == chunk_rows[0] ? 0 : 1];
-    const int grid = grids[rows == chunk_rows[0] ? 0 : 1];
+    const int pi = rows == cp.chunk_rows[0] ? 0 : 1;
+    const Plan& pl = cp.plans[pi];
+    const int grid = grids[pi];
     sk::Args a;
     memset(&a, 0, sizeof(a));
-    a.A = A + (int64_t)m0 * lda;
+    a.A = Ause + (int64_t)m0 * ldause;
     a.W0 = W0;
     a.W1 = W1;
     a.C = C ? C + (int64_t)m0 * ldc : nullptr;
     if (ws) {
-      const size_t tb = ticket_bytes(op == SK_OP_LM_ARGMAX ? 1 : pl.nrb);
+      const size_t tb = ticket_bytes(bop == SK_OP_LM_ARGMAX ? 1 : pl.nrb);
       a.tickets = static_cast<unsigned*>(ws);
       a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + tb);
       a.best = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + tb);
     }
-    if (op == SK_OP_LM_ARGMAX) {   // the fused argmax finishes into ids / maxv
+    if (bop == SK_OP_LM_ARGMAX) {   // the fused argmax finishes into ids / maxv
       a.C = reinterpret_cast<sk_bf16*>(ids + m0);
       a.part = maxv + m0;
     }
-    a.lda = lda;
+    if (nrm && cp.fused) {
+      a.Y = nrm->y + (int64_t)m0 * lda;
+      a.NW = nrm->w;
+      a.XO = nrm->xout + (int64_t)m0 * lda;
+      a.eps = nrm->eps;
+    }
+    a.lda = ldause;
     a.ldw = ldw;
     a.ldc = ldc;
     a.M = rows;
@@ -543,7 +663,7 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const sk_bf16* W0, co
 
 extern "C" {
 
-int sk_version(void) { return (0 << 16) | 1; }
+int sk_version(void) { return (0 << 16) | 2; }
 
 const char* sk_strerror(int status) {
   switch (status) {
@@ -562,7 +682,7 @@ const char* sk_strerror(int status) {
 
 int sk_default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   if (!out) return SK_ERR_NULL;
-  if (op != SK_OP_GEMM && op != SK_OP_GATEUP && op != SK_OP_LM_ARGMAX) return SK_ERR_CONFIG;
+  if (!is_gemm_family(base_op(op))) return SK_ERR_CONFIG;
   return default_config(op, M, N, K, num_cu, out);
 }
 
@@ -580,32 +700,54 @@ size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg) {
     if (M < 1 || N < 1) return 0;
     return ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
   }
-  if (M < 1) return 0;
-  const int Mk = M > kMaxM ? kMaxM : M;
-  sk_config c;
-  if (resolve_config(op, Mk, N, K, cfg, &c)) return 0;
-  Plan pl;
-  if (plan_shape(op, Mk, N, K, c, &pl)) return 0;
-  return plan_workspace(op, Mk, N, pl);
+  if (M < 1 || !is_gemm_family(base_op(op))) return 0;
+  CallPlan cp;
+  if (plan_call(op, M, N, K, cfg, &cp)) return 0;
+  return cp.need;
 }
 
 int sk_gemm_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N,
                  int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
-  return run_gemm_family(SK_OP_GEMM, A, lda, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, ws, ws_bytes,
-                         stream);
+  return run_gemm_family(SK_OP_GEMM, A, lda, nullptr, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, ws,
+                         ws_bytes, stream);
 }
 
 int sk_gateup_swiglu_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw,
                           sk_bf16* Out, int64_t ldo, int M, int I, int K, const sk_config* cfg, void* ws,
                           size_t ws_bytes, hipStream_t stream) {
-  return run_gemm_family(SK_OP_GATEUP, A, lda, Wg, Wu, ldw, Out, ldo, nullptr, nullptr, M, I, K, cfg, ws, ws_bytes,
-                         stream);
+  return run_gemm_family(SK_OP_GATEUP, A, lda, nullptr, Wg, Wu, ldw, Out, ldo, nullptr, nullptr, M, I, K, cfg, ws,
+                         ws_bytes, stream);
 }
 
 int sk_lm_argmax_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M,
                       int V, int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
-  return run_gemm_family(SK_OP_LM_ARGMAX, A, lda, W, nullptr, ldw, nullptr, 0, ids, maxv, M, V, K, cfg, ws, ws_bytes,
-                         stream);
+  return run_gemm_family(SK_OP_LM_ARGMAX, A, lda, nullptr, W, nullptr, ldw, nullptr, 0, ids, maxv, M, V, K, cfg, ws,
+                         ws_bytes, stream);
+}
+
+int sk_rmsnorm_gemm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps, sk_bf16* xout,
+                         int64_t ldx, const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N, int K,
+                         const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const NormIn n{y, w_norm, eps, xout};
+  return run_gemm_family(SK_OP_RMSNORM_GEMM, x, ldx, &n, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, ws,
+                         ws_bytes, stream);
+}
+
+int sk_rmsnorm_gateup_swiglu_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps,
+                                  sk_bf16* xout, int64_t ldx, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw,
+                                  sk_bf16* Out, int64_t ldo, int M, int I, int K, const sk_config* cfg, void* ws,
+                                  size_t ws_bytes, hipStream_t stream) {
+  const NormIn n{y, w_norm, eps, xout};
+  return run_gemm_family(SK_OP_RMSNORM_GATEUP, x, ldx, &n, Wg, Wu, ldw, Out, ldo, nullptr, nullptr, M, I, K, cfg, ws,
+                         ws_bytes, stream);
+}
+
+int sk_rmsnorm_lm_argmax_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps, sk_bf16* xout,
+                              int64_t ldx, const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M, int V,
+                              int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const NormIn n{y, w_norm, eps, xout};
+  return run_gemm_family(SK_OP_RMSNORM_LM_ARGMAX, x, ldx, &n, W, nullptr, ldw, nullptr, 0, ids, maxv, M, V, K, cfg, ws,
+                         ws_bytes, stream);
 }
 
 int sk_argmax_bf16(const sk_bf16* L, int64_t ld, int M, int V, int64_t* ids, float* maxv, void* ws, size_t ws_bytes,
@@ -645,7 +787,7 @@ int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, fl
   int num_cu = 0;
   int st = device_info(&num_cu);
   if (st) return st;
-  sk::add_rmsnorm_kernel<<<dim3(M), dim3(sk::RMS_THREADS), 0, stream>>>(x, y, w, eps, xout, out, K, ld);
+  sk::add_rmsnorm_kernel<<<dim3(M), dim3(sk::RMS_THREADS), 0, stream>>>(x, y, w, eps, xout, out, K, ld, ld);
   return launch_status();
 }
 

@@ -1,4 +1,4 @@
-// GEMV (VALU dot2) kernel instances for one epilogue (-DSK_EPI=<0..4>).
+// GEMV (VALU dot2) kernel instances for one epilogue (-DSK_EPI=<0..7>).
 #include "sk_registry.hpp"
 
 #ifndef SK_EPI
@@ -12,7 +12,8 @@ namespace sk {
 
 template <int MR, int R, int KU, int EPI>
 __global__ void __launch_bounds__(
-    64 * max_waves_for_regs(gemv_regs(MR, (EPI == EPI_SWIGLU || EPI == EPI_PART_GU) ? 2 * R : R, KU)))
+    64 * max_waves_for_regs(gemv_regs(MR, EpiTraits<EPI>::gateup ? 2 * R : R, KU, EpiTraits<EPI>::norm),
+                            EpiTraits<EPI>::norm))
 gemv_entry(Args p) {
   gemv_body<MR, R, KU, EPI>(p);
 }

@@ -48,7 +48,12 @@ enum Epi : int {
   EPI_SWIGLU = 1,     // C = bf16(bf16(silu(bf16 g)) * bf16 u)
   EPI_ARGMAX = 2,     // running (max, lowest index) per row, logits never stored
   EPI_PART = 3,       // fp32 partial of one global K split
-  EPI_PART_GU = 4     // fp32 partials of gate and up for one global K split
+  EPI_PART_GU = 4,    // fp32 partials of gate and up for one global K split
+  // The first three again, with the residual-add + RMSNorm prologue applied to
+  // the activation rows as they are loaded (one global K split only).
+  EPI_STORE_NORM = 5,
+  EPI_SWIGLU_NORM = 6,
+  EPI_ARGMAX_NORM = 7
 };
 
 // Kernel arguments, passed by value (one struct keeps the launch ABI simple).
@@ -69,6 +74,13 @@ struct Args {
   int nw;                 // waves per workgroup (blockDim.x / 64)
   int grid;               // workgroups launched (gridDim.x)
   int rbstep;             // grid / S: tile stride of one workgroup
+  // Norm prologue (EPI_*_NORM only): A holds x; the GEMM consumes
+  // bf16(NW * bf16(s * rstd(s))) with s = bf16(x + Y), and workgroup 0 writes
+  // s to XO.  Y and XO share the row stride lda.
+  const uint16_t* Y;
+  const uint16_t* NW;
+  uint16_t* XO;
+  float eps;
 };
 
 // ---------------------------------------------------------------------------
@@ -172,6 +184,51 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // ---------------------------------------------------------------------------
+// Residual add + RMSNorm on packed bf16 (engine/kernels/add_rmsnorm.py:15-29,
+// casts as rmsnorm.py:34-45):  s = bf16(x + y);  rstd = 1/sqrt(sum(s^2)/K + eps)
+// in fp32;  a = bf16(w * bf16(s * rstd)).
+// ---------------------------------------------------------------------------
+// s = bf16(x + y) for 8 columns; adds their squares to sq in column order.
+__device__ __forceinline__ u32x4 add_bf16x8(u32x4 x, u32x4 y, float& sq) {
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint16_t lo = f2bf(bf2f(x[q] & 0xFFFFu) + bf2f(y[q] & 0xFFFFu));
+    const uint16_t hi = f2bf(bf2f(x[q] >> 16) + bf2f(y[q] >> 16));
+    const float flo = bf2f(lo), fhi = bf2f(hi);
+    sq += flo * flo;
+    sq += fhi * fhi;
+    r[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  return r;
+}
+
+__device__ __forceinline__ float rms_rstd(float sumsq, int K, float eps) {
+  return 1.0f / sqrtf(sumsq / (float)K + eps);
+}
+
+// bf16(w * bf16(s * rstd)) for 8 columns.
+__device__ __forceinline__ u32x4 norm_bf16x8(u32x4 s, u32x4 w, float rstd) {
+  // Re-expand s from its packed bits here: an empty asm hides the packed
+  // value's origin, so the compiler does not keep the fp32 copies made when s
+  // was formed alive until now (twice the registers).
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint32_t t = s[q];
+    asm volatile("" : "+v"(t));
+    s[q] = t;
+  }
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint16_t lo = f2bf(bf2f(w[q] & 0xFFFFu) * round_bf(bf2f(s[q] & 0xFFFFu) * rstd));
+    const uint16_t hi = f2bf(bf2f(w[q] >> 16) * round_bf(bf2f(s[q] >> 16) * rstd));
+    r[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------------------
 // Shared tile epilogue.  The waves' partial tiles sit in LDS as P[w][m][row]
 // (ROWS rows per tile); they are summed in wave order and the finished values
 // go to an LDS staging area (or, for argmax, into a per-row running best).
@@ -181,9 +238,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 // ---------------------------------------------------------------------------
 template <int EPI>
 struct EpiTraits {
-  static constexpr bool gateup = (EPI == EPI_SWIGLU || EPI == EPI_PART_GU);
+  static constexpr bool norm = EPI >= EPI_STORE_NORM;
+  static constexpr int base = norm ? EPI - EPI_STORE_NORM : EPI;   // the epilogue proper
+  static constexpr bool gateup = (base == EPI_SWIGLU || base == EPI_PART_GU);
   // bytes per staged output element (PART_GU stages gate and up fp32 sums)
-  static constexpr int stage_bytes = EPI == EPI_STORE || EPI == EPI_SWIGLU ? 2 : (EPI == EPI_PART ? 4 : 8);
+  static constexpr int stage_bytes = base == EPI_STORE || base == EPI_SWIGLU ? 2 : (base == EPI_PART ? 4 : 8);
 };
 
 __device__ __forceinline__ void lds_barrier() {
@@ -349,6 +408,9 @@ __device__ __forceinline__ int wg_tiles(int rb0, int rbstep, int nrb) {
 template <int MT, int NT, int KU, int EPI>
 __device__ __forceinline__ void mfma_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
+  constexpr int BASE = EpiTraits<EPI>::base;   // epilogue without the norm prologue
+  constexpr bool NORM = EpiTraits<EPI>::norm;
+  static_assert(!NORM, "the register-fragment MFMA path has no norm prologue");
   constexpr int ROWS = 16 * NT;                  // partial rows per tile in LDS
   constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
   static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
@@ -376,7 +438,7 @@ __device__ __forceinline__ void mfma_body(Args p) {
   const int part_floats = nw * M * ROWS;
   void* stage = lds + 2 * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
-  if constexpr (EPI == EPI_ARGMAX) {
+  if constexpr (BASE == EPI_ARGMAX) {
     if (tid < M) lds_best[tid] = 0ull;
   }
 
@@ -459,19 +521,19 @@ __device__ __forceinline__ void mfma_body(Args p) {
         if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
       }
     lds_barrier();
-    tile_reduce<ROWS, EPI>(p, P, nw, rb, j, stage, lds_best);
+    tile_reduce<ROWS, BASE>(p, P, nw, rb, j, stage, lds_best);
   };
 
   int j = 0;
   for (; j + 1 < ntiles; ++j) tile(j, std::integral_constant<bool, true>{});
   if (ntiles > 0) tile(j, std::integral_constant<bool, false>{});
   lds_barrier();
-  if constexpr (EPI == EPI_ARGMAX) {
+  if constexpr (BASE == EPI_ARGMAX) {
     argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
   } else {
-    flush_stage<OUT_ROWS, EPI>(p, stage, ntiles, rb0, slice);
-    if constexpr (EPI == EPI_PART || EPI == EPI_PART_GU)
-      splitk_fixup<OUT_ROWS, EPI>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+    flush_stage<OUT_ROWS, BASE>(p, stage, ntiles, rb0, slice);
+    if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
   }
 }
 
@@ -491,6 +553,8 @@ __device__ __forceinline__ void mfma_body(Args p) {
 template <int MT, int NT, int KW, int EPI>
 __device__ __forceinline__ void mfmt_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
+  constexpr int BASE = EpiTraits<EPI>::base;   // epilogue without the norm prologue
+  constexpr bool NORM = EpiTraits<EPI>::norm;
   constexpr int ROWS = 16 * NT;                  // weight rows per tile
   constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
   constexpr int UNITS = KW / 32;                 // MFMA K steps per wave
@@ -522,37 +586,56 @@ __device__ __forceinline__ void mfmt_body(Args p) {
   const bool has_chunk = chunk < c_hi;                  // wave-uniform
   const int k0 = min(chunk, chunks - 1) * KW;
 
-  // Wave-private staging of 16 rows x 256 columns; the NT row tiles (and the
-  // two halves of a 512-column chunk) pass through it in turn.
-  char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
-  float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
+  // LDS: [norm weights, K bf16 (norm instances)][wave-private staging of 16
+  // rows x 256 columns per wave: the NT row tiles (and the two halves of a
+  // 512-column chunk) pass through it in turn][partials][staged outputs].
+  const int nwl_bytes = NORM ? ((2 * p.K + 15) & ~15) : 0;
+  const uint16_t* nwl = reinterpret_cast<const uint16_t*>(lds);
+  char* tr = reinterpret_cast<char*>(lds) + nwl_bytes + wave * (16 * PITCH);
+  float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nwl_bytes + nw * (16 * PITCH));
   const int part_floats = nw * M * ROWS;
   void* stage = parts + 2 * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
-  if constexpr (EPI == EPI_ARGMAX) {
+  if constexpr (BASE == EPI_ARGMAX) {
     if (tid < M) lds_best[tid] = 0ull;
   }
 
   // Activation fragments of this chunk: lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8];
-  // zero for rows >= M, columns >= K and waves without a chunk.
+  // zero for rows >= M, columns >= K and waves without a chunk.  When the
+  // chunk lies inside K (wave-uniform) the loads share one base address with
+  // immediate offsets; otherwise each column is clamped in bounds.  Norm
+  // instances also load the residual rows y at the same positions.
+  const bool full_chunk = has_chunk && k0 + KW <= p.K;
   bf16x8 af[MT][UNITS];
+  u32x4 yf[NORM ? MT : 1][NORM ? UNITS : 1];
+  auto load_acts = [&](auto full) {
+    constexpr bool FULL = decltype(full)::value;
+    auto col = [&](int u) { return FULL ? k0 + 8 * g4 + 32 * u : min(k0 + 32 * u + 8 * g4, p.K - 8); };
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * mt + r16;
-    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r16;
+      const int64_t roff = (int64_t)min(m, M - 1) * p.lda;
 #pragma unroll
-    for (int u = 0; u < UNITS; ++u) {
-      const int k = k0 + 32 * u + 8 * g4;
-      u32x4 v = ld16(ap + min(k, p.K - 8));
-      if (m >= M || k >= p.K || !has_chunk) v = u32x4{0u, 0u, 0u, 0u};
-      af[mt][u] = __builtin_bit_cast(bf16x8, v);
+      for (int u = 0; u < UNITS; ++u) {
+        const int k = k0 + 32 * u + 8 * g4;
+        const bool ok = m < M && (FULL || (k < p.K && has_chunk));
+        u32x4 v = ld16(p.A + roff + col(u));
+        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
+        af[mt][u] = __builtin_bit_cast(bf16x8, v);
+        if constexpr (NORM) {
+          u32x4 yv = ld16(p.Y + roff + col(u));
+          if (!ok) yv = u32x4{0u, 0u, 0u, 0u};
+          yf[mt][u] = yv;
+        }
+      }
     }
-  }
+  };
+  if (full_chunk) load_acts(std::true_type{});
+  else load_acts(std::false_type{});
 
   // Load instruction i covers tile rows i*RPI + lane/LPR, columns k0 + 8*(lane%LPR).
   const int lrow = lane / LPR;
   const int lcol = min(k0 + 8 * (lane % LPR), p.K - 8);
-  (void)lrow;
   auto wsrc = [&](int rb, int i) -> const uint16_t* {
     const int t = i * RPI + lrow;             // row within the tile
     if constexpr (GATEUP) {
@@ -572,10 +655,68 @@ __device__ __forceinline__ void mfmt_body(Args p) {
   char* const wdst = tr + (lane >> 5) * PITCH + 16 * (lane & 31);
   constexpr int NLD16 = 16 / RPI;                 // load instructions per 16-row tile
 
+  // First tile's weight rows.  Norm instances issue them before the prologue
+  // only when the residual fragments and the rows fit the registers together
+  // (then the weight stream's first latency overlaps the prologue's loads).
+  constexpr bool EARLY_W = !NORM || 4 * UNITS * MT * 2 + 4 * NLD <= 160;
   u32x4 wf[NLD];
-  if (ntiles > 0) {
+  auto load_first_tile = [&]() {
+    if (ntiles > 0) {
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) wf[i] = ld16_stream(wsrc(rb0, i));
+      for (int i = 0; i < NLD; ++i) wf[i] = ld16_stream(wsrc(rb0, i));
+    }
+  };
+  if constexpr (EARLY_W) load_first_tile();
+
+  if constexpr (NORM) {
+    // The norm weights go to LDS, once per workgroup (16 bytes per thread and step).
+    for (int c = tid; c < (p.K >> 3); c += 64 * nw)
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(nwl) + 8 * c) = ld16(p.NW + 8 * c);
+    // s = bf16(x + y) replaces x in the fragments; each row's sum of squares
+    // is reduced over the four lanes holding that row (lanes l, l^16, l^32,
+    // l^48), then over the waves in LDS in wave order.  The workgroup covers
+    // all of K (one global split), so every row sum is complete.
+    float sq[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      sq[mt] = 0.f;
+#pragma unroll
+      for (int u = 0; u < UNITS; ++u)
+        af[mt][u] = __builtin_bit_cast(bf16x8, add_bf16x8(__builtin_bit_cast(u32x4, af[mt][u]), yf[mt][u], sq[mt]));
+      sq[mt] += __shfl_xor(sq[mt], 16);
+      sq[mt] += __shfl_xor(sq[mt], 32);
+    }
+    // The second partial buffer is first written by tile 1, after tile 0's barrier.
+    float* red = parts + part_floats;
+    if (g4 == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        if (16 * mt + r16 < M) red[wave * M + 16 * mt + r16] = sq[mt];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + r16;
+      float t = 0.f;
+      for (int w = 0; w < nw; ++w) t += red[w * M + min(m, M - 1)];
+      const float rstd = rms_rstd(t, p.K, p.eps);
+#pragma unroll
+      for (int u = 0; u < UNITS; ++u) {
+        const int k = k0 + 32 * u + 8 * g4;
+        const bool ok = m < M && k < p.K && has_chunk;
+        const u32x4 sv = __builtin_bit_cast(u32x4, af[mt][u]);
+        if (blockIdx.x == 0 && ok) *reinterpret_cast<u32x4*>(p.XO + (int64_t)m * p.lda + k) = sv;
+        const u32x4 wn = *reinterpret_cast<const u32x4*>(nwl + min(k, p.K - 8));
+        u32x4 a = norm_bf16x8(sv, wn, rstd);
+        if (!ok) a = u32x4{0u, 0u, 0u, 0u};
+        af[mt][u] = __builtin_bit_cast(bf16x8, a);
+      }
+    }
+  }
+  if constexpr (!EARLY_W) {
+    // Not hoisted above the prologue by the scheduler.
+    __builtin_amdgcn_sched_barrier(0);
+    load_first_tile();
   }
 
   auto tile = [&](int j, auto prefetch) {
@@ -633,19 +774,19 @@ __device__ __forceinline__ void mfmt_body(Args p) {
         if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
       }
     lds_barrier();
-    tile_reduce<ROWS, EPI>(p, P, nw, rb, j, stage, lds_best);
+    tile_reduce<ROWS, BASE>(p, P, nw, rb, j, stage, lds_best);
   };
 
   int j = 0;
   for (; j + 1 < ntiles; ++j) tile(j, std::integral_constant<bool, true>{});
   if (ntiles > 0) tile(j, std::integral_constant<bool, false>{});
   lds_barrier();
-  if constexpr (EPI == EPI_ARGMAX) {
+  if constexpr (BASE == EPI_ARGMAX) {
     argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
   } else {
-    flush_stage<OUT_ROWS, EPI>(p, stage, ntiles, rb0, slice);
-    if constexpr (EPI == EPI_PART || EPI == EPI_PART_GU)
-      splitk_fixup<OUT_ROWS, EPI>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+    flush_stage<OUT_ROWS, BASE>(p, stage, ntiles, rb0, slice);
+    if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
   }
 }
 
@@ -661,6 +802,8 @@ __device__ __forceinline__ void mfmt_body(Args p) {
 template <int MR, int R, int KU, int EPI>
 __device__ __forceinline__ void gemv_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
+  constexpr int BASE = EpiTraits<EPI>::base;   // epilogue without the norm prologue
+  constexpr bool NORM = EpiTraits<EPI>::norm;
   constexpr int RR = GATEUP ? 2 * R : R;   // partial rows per tile
   constexpr int OUT_ROWS = R;
 
@@ -687,7 +830,7 @@ __device__ __forceinline__ void gemv_body(Args p) {
   const int part_floats = nw * M * RR;
   void* stage = lds + 2 * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
-  if constexpr (EPI == EPI_ARGMAX) {
+  if constexpr (BASE == EPI_ARGMAX) {
     if (tid < M) lds_best[tid] = 0ull;
   }
 
@@ -712,6 +855,23 @@ __device__ __forceinline__ void gemv_body(Args p) {
       af[m][u] = v;
     }
   }
+  // Norm prologue, loads.
+  u32x4 yf[NORM ? MR : 1][NORM ? KU : 1];
+  u32x4 nf[NORM ? KU : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const uint16_t* yp = p.Y + (int64_t)min(m, M - 1) * p.lda;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        u32x4 v = ld16(yp + kcol[u]);
+        if (m >= M || !kok[u]) v = u32x4{0u, 0u, 0u, 0u};
+        yf[m][u] = v;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < KU; ++u) nf[u] = ld16(p.NW + kcol[u]);
+  }
 
   auto wrow = [&](int rb, int rr) -> const uint16_t* {
     if constexpr (GATEUP) {
@@ -723,6 +883,42 @@ __device__ __forceinline__ void gemv_body(Args p) {
     }
   };
 
+  if constexpr (NORM) {
+    // s = bf16(x + y) replaces x; row sums of squares over the wave (DPP),
+    // then over the waves in LDS in wave order (the workgroup covers all of K).
+    float sq[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      sq[m] = 0.f;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) af[m][u] = add_bf16x8(af[m][u], yf[m][u], sq[m]);
+      sq[m] = wave_sum(sq[m]);
+    }
+    float* red = parts + part_floats;   // first written by tile 1, after tile 0's barrier
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M) red[wave * M + m] = sq[m];
+    }
+    lds_barrier();
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float t = 0.f;
+      for (int w = 0; w < nw; ++w) t += red[w * M + min(m, M - 1)];
+      const float rstd = rms_rstd(t, p.K, p.eps);
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const bool ok = m < M && kok[u];
+        if (blockIdx.x == 0 && ok) *reinterpret_cast<u32x4*>(p.XO + (int64_t)m * p.lda + kcol[u]) = af[m][u];
+        u32x4 a = norm_bf16x8(af[m][u], nf[u], rstd);
+        if (!ok) a = u32x4{0u, 0u, 0u, 0u};
+        af[m][u] = a;
+      }
+    }
+  }
+
+  // First tile's weight rows, after the norm prologue (not hoisted above it).
+  if constexpr (NORM) __builtin_amdgcn_sched_barrier(0);
   u32x4 wf[RR][KU];
   if (ntiles > 0) {
 #pragma unroll
@@ -759,19 +955,19 @@ __device__ __forceinline__ void gemv_body(Args p) {
         if (m < M && lane == 0) P[(wave * M + m) * RR + rr] = s;
       }
     lds_barrier();
-    tile_reduce<RR, EPI>(p, P, nw, rb, j, stage, lds_best);
+    tile_reduce<RR, BASE>(p, P, nw, rb, j, stage, lds_best);
   };
 
   int j = 0;
   for (; j + 1 < ntiles; ++j) tile(j, std::integral_constant<bool, true>{});
   if (ntiles > 0) tile(j, std::integral_constant<bool, false>{});
   lds_barrier();
-  if constexpr (EPI == EPI_ARGMAX) {
+  if constexpr (BASE == EPI_ARGMAX) {
     argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
   } else {
-    flush_stage<OUT_ROWS, EPI>(p, stage, ntiles, rb0, slice);
-    if constexpr (EPI == EPI_PART || EPI == EPI_PART_GU)
-      splitk_fixup<OUT_ROWS, EPI>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+    flush_stage<OUT_ROWS, BASE>(p, stage, ntiles, rb0, slice);
+    if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
   }
 }
 
@@ -845,13 +1041,14 @@ __global__ void __launch_bounds__(RMS_THREADS) add_rmsnorm_kernel(const uint16_t
                                                                   const uint16_t* __restrict__ y,
                                                                   const uint16_t* __restrict__ w, float eps,
                                                                   uint16_t* __restrict__ xout,
-                                                                  uint16_t* __restrict__ out, int K, int64_t ld) {
+                                                                  uint16_t* __restrict__ out, int K, int64_t ld,
+                                                                  int64_t ld_out) {
   __shared__ float wsum[RMS_THREADS / 64];
   const int m = blockIdx.x;
   const uint16_t* xr = x + (int64_t)m * ld;
   const uint16_t* yr = y + (int64_t)m * ld;
   uint16_t* xo = xout + (int64_t)m * ld;
-  uint16_t* orow = out + (int64_t)m * ld;
+  uint16_t* orow = out + (int64_t)m * ld_out;
   const int nchunk = K >> 3;
   u32x4 sv[RMS_MAX_CHUNKS];
   float sq = 0.f;
@@ -860,19 +1057,7 @@ __global__ void __launch_bounds__(RMS_THREADS) add_rmsnorm_kernel(const uint16_t
     const int c = threadIdx.x + j * RMS_THREADS;
     sv[j] = u32x4{0u, 0u, 0u, 0u};
     if (c < nchunk) {
-      const u32x4 a = ld16(xr + 8 * c), b = ld16(yr + 8 * c);
-      const uint32_t aa[4] = {a.x, a.y, a.z, a.w}, bb[4] = {b.x, b.y, b.z, b.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint16_t lo = f2bf(bf2f(aa[q] & 0xFFFFu) + bf2f(bb[q] & 0xFFFFu));
-        const uint16_t hi = f2bf(bf2f(aa[q] >> 16) + bf2f(bb[q] >> 16));
-        const float flo = bf2f(lo), fhi = bf2f(hi);
-        sq += flo * flo;
-        sq += fhi * fhi;
-        o[q] = (uint32_t)lo | ((uint32_t)hi << 16);
-      }
-      sv[j] = u32x4{o[0], o[1], o[2], o[3]};
+      sv[j] = add_bf16x8(ld16(xr + 8 * c), ld16(yr + 8 * c), sq);
       *reinterpret_cast<u32x4*>(xo + 8 * c) = sv[j];
     }
   }
@@ -882,22 +1067,11 @@ __global__ void __launch_bounds__(RMS_THREADS) add_rmsnorm_kernel(const uint16_t
   float tot = 0.f;
 #pragma unroll
   for (int i = 0; i < RMS_THREADS / 64; ++i) tot += wsum[i];
-  const float rstd = 1.0f / sqrtf(tot / (float)K + eps);
+  const float rstd = rms_rstd(tot, K, eps);
 #pragma unroll
   for (int j = 0; j < RMS_MAX_CHUNKS; ++j) {
     const int c = threadIdx.x + j * RMS_THREADS;
-    if (c < nchunk) {
-      const u32x4 wv = ld16(w + 8 * c);
-      const uint32_t ss[4] = {sv[j].x, sv[j].y, sv[j].z, sv[j].w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
-      uint32_t o[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint16_t lo = f2bf(bf2f(ww[q] & 0xFFFFu) * round_bf(bf2f(ss[q] & 0xFFFFu) * rstd));
-        const uint16_t hi = f2bf(bf2f(ww[q] >> 16) * round_bf(bf2f(ss[q] >> 16) * rstd));
-        o[q] = (uint32_t)lo | ((uint32_t)hi << 16);
-      }
-      *reinterpret_cast<u32x4*>(orow + 8 * c) = u32x4{o[0], o[1], o[2], o[3]};
-    }
+    if (c < nchunk) *reinterpret_cast<u32x4*>(orow + 8 * c) = norm_bf16x8(sv[j], ld16(w + 8 * c), rstd);
   }
 }
 

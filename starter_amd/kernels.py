@@ -12,7 +12,9 @@ SkinnyGateUp  gemm.py:315    SkinnyGateUp (sk_gateup_swiglu_bf16)
 Gemv          gemm.py:259    Gemv (sk_gemm_bf16 / sk_gateup_swiglu_bf16, GEMV path)
 pick_matmul   gemm.py:516    pick_matmul (offline table instead of warmup timing)
 pick_gateup   gemm.py:561    pick_gateup
-pick_normed   gemm.py:602    pick_normed
+pick_normed   gemm.py:602    pick_normed (sk_rmsnorm_gemm_bf16 / sk_rmsnorm_gateup_swiglu_bf16)
+_norm_stats + _normed_tile   rmsnorm_gemm / rmsnorm_gateup_swiglu / rmsnorm_lm_argmax
+  gemm.py:28-56, 184-208     (norm prologue fused into the projection kernel)
 add_rms_norm  add_rmsnorm.py add_rms_norm (sk_add_rmsnorm_bf16)
 swiglu        swiglu.py      swiglu (sk_swiglu_bf16)
 fast_topk[0]  topk.py:40     argmax (sk_argmax_bf16)
@@ -29,15 +31,18 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._lib import (SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_PATH_GEMV, SK_PATH_MFMA, SkConfig,
-                   check, cfg_ptr, lib)
+from ._lib import (SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_OP_RMSNORM_GATEUP,
+                   SK_OP_RMSNORM_GEMM, SK_OP_RMSNORM_LM_ARGMAX, SK_PATH_GEMV, SK_PATH_MFMA, SkConfig, check, cfg_ptr,
+                   lib)
 
 BF16 = torch.bfloat16
 
 __all__ = [
     "SkinnyMatmul", "SkinnyGateUp", "Gemv", "LmArgmax", "gemm", "gateup_swiglu", "lm_argmax", "argmax",
+    "rmsnorm_gemm", "rmsnorm_gateup_swiglu", "rmsnorm_lm_argmax",
     "add_rms_norm", "swiglu", "pick_matmul", "pick_gateup", "pick_normed", "pick_lm_argmax", "SkConfig",
     "SK_PATH_MFMA", "SK_PATH_GEMV", "SK_OP_GEMM", "SK_OP_GATEUP", "SK_OP_LM_ARGMAX", "SK_OP_ARGMAX",
+    "SK_OP_RMSNORM_GEMM", "SK_OP_RMSNORM_GATEUP", "SK_OP_RMSNORM_LM_ARGMAX",
 ]
 
 
@@ -149,6 +154,87 @@ def lm_argmax(a: torch.Tensor, w: torch.Tensor, config: SkConfig | None = None, 
     return ids, maxv
 
 
+def _norm_inputs(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, xout: torch.Tensor) -> None:
+    _mat(x, "x")
+    _mat(y, "y")
+    _mat(xout, "xout")
+    _need(y.shape == x.shape and y.stride(0) == x.stride(0), "y must match x (shape and row stride)")
+    _need(xout.shape == x.shape and xout.stride(0) == x.stride(0), "xout must match x (shape and row stride)")
+    _need(w_norm.dtype == BF16 and w_norm.is_contiguous() and w_norm.numel() == x.shape[1], "w_norm must be bf16 [K]")
+
+
+def rmsnorm_gemm(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, eps: float, xout: torch.Tensor,
+                 w: torch.Tensor, out: torch.Tensor | None = None, config: SkConfig | None = None,
+                 ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``xout = x + y``; ``out = rms_norm(xout, w_norm) @ w.T`` in one kernel when the
+    configuration allows (engine/kernels/gemm.py:602-660, prologue 28-56)."""
+    _norm_inputs(x, y, w_norm, xout)
+    _mat(w, "w")
+    M, K = x.shape
+    N = w.shape[0]
+    _need(w.shape[1] == K, f"K mismatch: x {tuple(x.shape)} vs w {tuple(w.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=BF16, device=x.device)
+    _mat(out, "out")
+    _need(tuple(out.shape) == (M, N), "out shape")
+    if ws is None and _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, M, N, K, config):
+        ws = _workspace(SK_OP_RMSNORM_GEMM, M, N, K, config, x.device)
+    _device_guard(x)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_rmsnorm_gemm_bf16(x.data_ptr(), y.data_ptr(), w_norm.data_ptr(), float(eps), xout.data_ptr(),
+                                     x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0), M, N, K,
+                                     cfg_ptr(config), wp, wn, _stream(x)), "sk_rmsnorm_gemm_bf16")
+    return out
+
+
+def rmsnorm_gateup_swiglu(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, eps: float, xout: torch.Tensor,
+                          wg: torch.Tensor, wu: torch.Tensor, out: torch.Tensor | None = None,
+                          config: SkConfig | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``xout = x + y``; ``out = swiglu(h @ wg.T, h @ wu.T)`` with ``h = rms_norm(xout, w_norm)``."""
+    _norm_inputs(x, y, w_norm, xout)
+    _mat(wg, "wg")
+    _mat(wu, "wu")
+    M, K = x.shape
+    I = wg.shape[0]
+    _need(wg.shape == wu.shape and wg.shape[1] == K and wg.stride(0) == wu.stride(0), "gate/up weight shapes")
+    if out is None:
+        out = torch.empty((M, I), dtype=BF16, device=x.device)
+    _mat(out, "out")
+    _need(tuple(out.shape) == (M, I), "out shape")
+    if ws is None and _lib.workspace_bytes(SK_OP_RMSNORM_GATEUP, M, I, K, config):
+        ws = _workspace(SK_OP_RMSNORM_GATEUP, M, I, K, config, x.device)
+    _device_guard(x)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_rmsnorm_gateup_swiglu_bf16(x.data_ptr(), y.data_ptr(), w_norm.data_ptr(), float(eps),
+                                              xout.data_ptr(), x.stride(0), wg.data_ptr(), wu.data_ptr(),
+                                              wg.stride(0), out.data_ptr(), out.stride(0), M, I, K, cfg_ptr(config),
+                                              wp, wn, _stream(x)), "sk_rmsnorm_gateup_swiglu_bf16")
+    return out
+
+
+def rmsnorm_lm_argmax(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, eps: float, xout: torch.Tensor,
+                      w: torch.Tensor, config: SkConfig | None = None, ws: torch.Tensor | None = None,
+                      ids: torch.Tensor | None = None, maxv: torch.Tensor | None = None):
+    """``xout = x + y``; greedy token per row of ``rms_norm(xout, w_norm) @ w.T``.
+    Returns ``(ids int64 [M], maxv float32 [M])``."""
+    _norm_inputs(x, y, w_norm, xout)
+    _mat(w, "w")
+    M, K = x.shape
+    V = w.shape[0]
+    _need(w.shape[1] == K, "K mismatch")
+    ids = torch.empty((M,), dtype=torch.int64, device=x.device) if ids is None else ids
+    maxv = torch.empty((M,), dtype=torch.float32, device=x.device) if maxv is None else maxv
+    if ws is None:
+        ws = _workspace(SK_OP_RMSNORM_LM_ARGMAX, M, V, K, config, x.device)
+    _device_guard(x)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_rmsnorm_lm_argmax_bf16(x.data_ptr(), y.data_ptr(), w_norm.data_ptr(), float(eps),
+                                          xout.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), ids.data_ptr(),
+                                          maxv.data_ptr(), M, V, K, cfg_ptr(config), wp, wn, _stream(x)),
+          "sk_rmsnorm_lm_argmax_bf16")
+    return ids, maxv
+
+
 def argmax(logits: torch.Tensor, ws: torch.Tensor | None = None):
     """``(logits.argmax(-1), logits.max(-1).float())`` over bf16 logits, lowest index on ties."""
     _mat(logits, "logits")
@@ -203,9 +289,17 @@ def swiglu(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 
 class _Planned:
-    op = SK_OP_GEMM
+    """Fixed (M, N, K) and config.  ``normed=True`` also plans the norm-prologue
+    variant (its workspace is allocated here, outside any graph capture); a
+    call with ``norm=(y, w_norm, xout, eps)`` then runs ``xout = a + y`` and
+    the projection of ``rms_norm(xout, w_norm)``, fused into one kernel when
+    the configuration allows (engine/kernels/gemm.py:363-366)."""
 
-    def __init__(self, M: int, N: int, K: int, device, config: SkConfig | None = None, **cfg_kw):
+    op = SK_OP_GEMM
+    norm_op = SK_OP_RMSNORM_GEMM
+
+    def __init__(self, M: int, N: int, K: int, device, config: SkConfig | None = None, normed: bool = False,
+                 **cfg_kw):
         self.M, self.N, self.K = M, N, K
         self.device = torch.device(device)
         self.config = _config(config, cfg_kw)
@@ -214,13 +308,20 @@ class _Planned:
             if st != _lib.SK_OK:
                 raise _lib.SkError(st, f"config {self.config} for op {self.op} at M={M} N={N} K={K}")
         self.ws = _workspace(self.op, M, N, K, self.config, self.device) if M > 0 else None
-        self._h = None   # normed activation buffer of the norm prologue
+        self.ws_norm = None
+        self._norm_planned = False
+        if normed:
+            self._plan_norm()
 
-    def _normed(self, a: torch.Tensor, norm) -> torch.Tensor:
-        y, wn, xout, eps = norm
-        if self._h is None or self._h.shape != a.shape:
-            self._h = torch.empty_like(a)
-        return add_rms_norm(a, y, wn, eps, xout, out=self._h)
+    def _plan_norm(self) -> None:
+        if self.M > 0:
+            self.ws_norm = _workspace(self.norm_op, self.M, self.N, self.K, self.config, self.device)
+        self._norm_planned = True
+
+    def _norm_ws(self):
+        if not self._norm_planned:
+            self._plan_norm()
+        return self.ws_norm
 
 
 class SkinnyMatmul(_Planned):
@@ -230,10 +331,12 @@ class SkinnyMatmul(_Planned):
     in front, like the reference's fused prologue (gemm.py:363-366)."""
 
     op = SK_OP_GEMM
+    norm_op = SK_OP_RMSNORM_GEMM
 
     def __call__(self, a: torch.Tensor, w: torch.Tensor, norm=None) -> torch.Tensor:
         if norm is not None:
-            a = self._normed(a, norm)
+            y, wn, xout, eps = norm
+            return rmsnorm_gemm(a, y, wn, eps, xout, w, config=self.config, ws=self._norm_ws())
         return gemm(a, w, config=self.config, ws=self.ws)
 
 
@@ -242,10 +345,12 @@ class SkinnyGateUp(_Planned):
     (engine/kernels/gemm.py:315-346)."""
 
     op = SK_OP_GATEUP
+    norm_op = SK_OP_RMSNORM_GATEUP
 
     def __call__(self, a: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, norm=None) -> torch.Tensor:
         if norm is not None:
-            a = self._normed(a, norm)
+            y, wn, xout, eps = norm
+            return rmsnorm_gateup_swiglu(a, y, wn, eps, xout, wg, wu, config=self.config, ws=self._norm_ws())
         return gateup_swiglu(a, wg, wu, config=self.config, ws=self.ws)
 
 
@@ -256,20 +361,24 @@ class Gemv(_Planned):
     (2, 4, 8), ``ku`` 512-column units per wave, ``waves`` per workgroup."""
 
     def __init__(self, M: int, N: int, K: int, device, gateup: bool = False, config: SkConfig | None = None,
-                 **cfg_kw):
+                 normed: bool = False, **cfg_kw):
         if M > 8:
             raise ValueError("Gemv handles at most 8 rows")
         self.op = SK_OP_GATEUP if gateup else SK_OP_GEMM
+        self.norm_op = SK_OP_RMSNORM_GATEUP if gateup else SK_OP_RMSNORM_GEMM
         self.gateup = gateup
         if config is None and not cfg_kw:
             cfg_kw = dict(path=SK_PATH_GEMV, waves=1, ku=(K + 511) // 512, rows=4)
         elif cfg_kw:
             cfg_kw.setdefault("path", SK_PATH_GEMV)
-        super().__init__(M, N, K, device, config, **cfg_kw)
+        super().__init__(M, N, K, device, config, normed=normed, **cfg_kw)
 
     def __call__(self, a: torch.Tensor, w: torch.Tensor, w2: torch.Tensor | None = None, norm=None) -> torch.Tensor:
         if norm is not None:
-            a = self._normed(a, norm)
+            y, wn, xout, eps = norm
+            if self.gateup:
+                return rmsnorm_gateup_swiglu(a, y, wn, eps, xout, w, w2, config=self.config, ws=self._norm_ws())
+            return rmsnorm_gemm(a, y, wn, eps, xout, w, config=self.config, ws=self._norm_ws())
         if self.gateup:
             return gateup_swiglu(a, w, w2, config=self.config, ws=self.ws)
         return gemm(a, w, config=self.config, ws=self.ws)
@@ -279,10 +388,12 @@ class LmArgmax(_Planned):
     """lm_head projection fused with the greedy argmax: ``(ids, maxv)``."""
 
     op = SK_OP_LM_ARGMAX
+    norm_op = SK_OP_RMSNORM_LM_ARGMAX
 
     def __call__(self, a: torch.Tensor, w: torch.Tensor, norm=None):
         if norm is not None:
-            a = self._normed(a, norm)
+            y, wn, xout, eps = norm
+            return rmsnorm_lm_argmax(a, y, wn, eps, xout, w, config=self.config, ws=self._norm_ws())
         return lm_argmax(a, w, config=self.config, ws=self.ws)
 
 
@@ -323,12 +434,12 @@ def pick_normed(kind: str, x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tenso
     ``xout = x + y`` (engine/kernels/gemm.py:602-660).  ``kind``: "matmul" or "gateup"."""
     M, K = x.shape
     if kind == "matmul":
-        mm = SkinnyMatmul(M, w.shape[0], K, x.device)
+        mm = SkinnyMatmul(M, w.shape[0], K, x.device, normed=True)
         _log_choice(log, "normed matmul", SK_OP_GEMM, M, w.shape[0], K)
         return lambda x, y, w_norm, xout, w: mm(x, w, norm=(y, w_norm, xout, eps))
     if kind == "gateup":
         I = w.shape[0] // 2
-        mm = SkinnyGateUp(M, I, K, x.device)
+        mm = SkinnyGateUp(M, I, K, x.device, normed=True)
         _log_choice(log, "normed gateup", SK_OP_GATEUP, M, I, K)
         return lambda x, y, w_norm, xout, w: mm(x, w[:I], w[I:], norm=(y, w_norm, xout, eps))
     raise ValueError(f"unknown kind {kind!r}")
@@ -338,6 +449,6 @@ def pick_lm_argmax(x: torch.Tensor, w: torch.Tensor, eps: float, log=None):
     """``f(x, y, w_norm, xout, w) -> (ids, maxv)``: the normed lm_head with the
     greedy argmax fused in (replaces ``mm["lm"](...).argmax(-1)``)."""
     M, K = x.shape
-    mm = LmArgmax(M, w.shape[0], K, x.device)
+    mm = LmArgmax(M, w.shape[0], K, x.device, normed=True)
     _log_choice(log, "normed lm_argmax", SK_OP_LM_ARGMAX, M, w.shape[0], K)
     return lambda x, y, w_norm, xout, w: mm(x, w, norm=(y, w_norm, xout, eps))

@@ -15,8 +15,9 @@ from pathlib import Path
 import pytest
 
 from starter_amd import _lib
-from starter_amd._lib import (SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_DEVICE, SK_ERR_NULL, SK_ERR_SHAPE, SK_ERR_WORKSPACE,
-                              SK_OK, SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_PATH_GEMV,
+from starter_amd._lib import (SK_ERR_ALIAS, SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_DEVICE, SK_ERR_NULL, SK_ERR_SHAPE,
+                              SK_ERR_WORKSPACE, SK_OK, SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX,
+                              SK_OP_RMSNORM_GATEUP, SK_OP_RMSNORM_GEMM, SK_OP_RMSNORM_LM_ARGMAX, SK_PATH_GEMV,
                               SK_PATH_MFMA, SK_PATH_MFMA_LDS, SkConfig)
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "starter_amd.h"
@@ -122,7 +123,10 @@ def test_check_config(cfg, op, M, N, K, expect):
     assert _lib.check_config(op, M, N, K, cfg) == expect
 
 
-def _gemm(lib, A=FAKE, lda=2560, W=FAKE, ldw=2560, C=FAKE, ldc=6144, M=8, N=6144, K=2560, cfg=None, ws=None,
+A0, W0, C0 = FAKE, FAKE + (1 << 26), FAKE + (1 << 27)   # disjoint fake operands
+
+
+def _gemm(lib, A=A0, lda=2560, W=W0, ldw=2560, C=C0, ldc=6144, M=8, N=6144, K=2560, cfg=None, ws=None,
           wsb=0):
     return lib.sk_gemm_bf16(A, lda, W, ldw, C, ldc, M, N, K, _lib.cfg_ptr(cfg), ws, wsb, None)
 
@@ -131,7 +135,8 @@ def test_argument_validation_precedes_any_device_work():
     lib = _lib.lib()
     assert _gemm(lib, A=None) == SK_ERR_NULL
     assert _gemm(lib, C=None) == SK_ERR_NULL
-    assert _gemm(lib, A=FAKE + 2) == SK_ERR_ALIGN
+    assert _gemm(lib, A=A0 + 2) == SK_ERR_ALIGN
+    assert _gemm(lib, C=A0 + 4096) == SK_ERR_ALIAS   # output overlaps the activations
     assert _gemm(lib, lda=2564) == SK_ERR_ALIGN
     assert _gemm(lib, K=2568, lda=2568, ldw=2568) == SK_ERR_SHAPE
     assert _gemm(lib, ldc=100) == SK_ERR_SHAPE
@@ -142,7 +147,7 @@ def test_argument_validation_precedes_any_device_work():
     assert _gemm(lib, cfg=split) == SK_ERR_WORKSPACE
     assert _gemm(lib, cfg=split, ws=FAKE, wsb=16) == SK_ERR_WORKSPACE
     assert _gemm(lib, cfg=SkConfig.make(SK_PATH_MFMA, 4, 10, 16)) == SK_ERR_CONFIG
-    assert lib.sk_lm_argmax_bf16(FAKE, 2560, FAKE, 2560, FAKE, FAKE, 8, 151936, 2560, None, None, 0, None) \
+    assert lib.sk_lm_argmax_bf16(A0, 2560, W0, 2560, C0, C0 + 512, 8, 151936, 2560, None, None, 0, None) \
         == SK_ERR_WORKSPACE
     assert lib.sk_argmax_bf16(FAKE, 151936, 4, 151936, FAKE, FAKE, None, 0, None) == SK_ERR_WORKSPACE
     assert lib.sk_argmax_bf16(FAKE, 151935, 4, 151936, FAKE, FAKE, FAKE, 1 << 20, None) == SK_ERR_SHAPE
@@ -174,3 +179,78 @@ def test_valid_call_without_gpu_fails_loudly():
     if torch.cuda.is_available():
         pytest.skip("a GPU is present; the GPU tests exercise this path")
     assert _gemm(_lib.lib()) == SK_ERR_DEVICE
+    assert _rms_gemm(_lib.lib()) == SK_ERR_DEVICE
+
+
+# ---------------------------------------------------------------------------
+# Residual add + RMSNorm prologue ops
+# ---------------------------------------------------------------------------
+
+NORMED = {"qkv": (SK_OP_RMSNORM_GEMM, 6144, 2560), "gu": (SK_OP_RMSNORM_GATEUP, 9728, 2560),
+          "lm": (SK_OP_RMSNORM_GEMM, 151936, 2560), "lm_argmax": (SK_OP_RMSNORM_LM_ARGMAX, 151936, 2560)}
+BASE = {SK_OP_RMSNORM_GEMM: SK_OP_GEMM, SK_OP_RMSNORM_GATEUP: SK_OP_GATEUP, SK_OP_RMSNORM_LM_ARGMAX: SK_OP_LM_ARGMAX}
+X0, Y0, XO0, NW0 = FAKE + (1 << 28), FAKE + (1 << 28) + (1 << 22), FAKE + (1 << 28) + (2 << 22), FAKE + (3 << 22)
+
+
+def _rms_gemm(lib, x=X0, y=Y0, nw=NW0, xo=XO0, ldx=2560, W=W0, C=C0, M=8, N=6144, K=2560, cfg=None, ws=None, wsb=0):
+    return lib.sk_rmsnorm_gemm_bf16(x, y, nw, 1e-6, xo, ldx, W, K, C, N, M, N, K, _lib.cfg_ptr(cfg), ws, wsb, None)
+
+
+@pytest.mark.parametrize("name", list(NORMED))
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 40, 64])
+def test_normed_default_config_valid_and_fused_at_decode_m(name, M):
+    """The norm ops use their projection's tuned configuration; at M <= 16
+    (one K split, LDS-fed MFMA or GEMV) the prologue runs inside the
+    projection kernel, so the workspace is the projection's own.  Otherwise the
+    workspace adds the normalised rows [M, K] bf16 after the projection's part."""
+    op, N, K = NORMED[name]
+    cfg = _lib.default_config(op, M, N, K)
+    base = _lib.default_config(BASE[op], M, N, K)
+    assert cfg.as_dict() == base.as_dict()
+    assert _lib.check_config(op, M, N, K, cfg) == SK_OK
+    plain = _lib.workspace_bytes(BASE[op], M, N, K, cfg)
+    normed = _lib.workspace_bytes(op, M, N, K, cfg)
+    unfused = (plain + 255) // 256 * 256 + M * K * 2
+    if M <= 16:
+        assert cfg.split == 1 and cfg.path in (SK_PATH_GEMV, SK_PATH_MFMA_LDS), cfg
+        assert normed == plain            # fused: no buffer for the normalised rows
+    elif cfg.split > 1 or cfg.path == SK_PATH_MFMA:
+        assert normed == unfused          # the register-fragment path and global splits never fuse
+    else:
+        assert normed in (plain, unfused)
+
+
+def test_normed_workspace_layout_for_unfused_configs():
+    split = SkConfig.make(SK_PATH_MFMA_LDS, 5, 8, 16, 2)
+    base = _lib.workspace_bytes(SK_OP_GEMM, 8, 6144, 2560, split)
+    assert base == _tickets(6144 // 16) + 2 * 8 * 6144 * 4
+    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, split) == (base + 255) // 256 * 256 + 8 * 2560 * 2
+    mfma = SkConfig.make(SK_PATH_MFMA, 8, 10, 16)
+    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, mfma) == 8 * 2560 * 2
+    # rows beyond 64: the separate prologue normalises all rows at once
+    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 100, 6144, 2560, mfma) == 100 * 2560 * 2
+
+
+def test_normed_argument_validation():
+    lib = _lib.lib()
+    assert _rms_gemm(lib, y=None) == SK_ERR_NULL
+    assert _rms_gemm(lib, nw=None) == SK_ERR_NULL
+    assert _rms_gemm(lib, xo=None) == SK_ERR_NULL
+    assert _rms_gemm(lib, nw=NW0 + 2) == SK_ERR_ALIGN
+    assert _rms_gemm(lib, y=Y0 + 8) == SK_ERR_ALIGN
+    assert _rms_gemm(lib, ldx=2564) == SK_ERR_ALIGN
+    assert _rms_gemm(lib, xo=X0) == SK_ERR_ALIAS          # xout is x
+    assert _rms_gemm(lib, xo=Y0 + 1024) == SK_ERR_ALIAS   # xout overlaps y
+    assert _rms_gemm(lib, C=Y0) == SK_ERR_ALIAS           # output overlaps y
+    assert _rms_gemm(lib, C=XO0) == SK_ERR_ALIAS          # output overlaps xout
+    assert _rms_gemm(lib, M=0, x=None, y=None, nw=None, xo=None, C=None) == SK_OK
+    split = SkConfig.make(SK_PATH_MFMA_LDS, 5, 8, 16, 2)
+    assert _rms_gemm(lib, cfg=split) == SK_ERR_WORKSPACE
+    need = _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, split)
+    assert _rms_gemm(lib, cfg=split, ws=FAKE, wsb=need - 1) == SK_ERR_WORKSPACE
+    gu = lib.sk_rmsnorm_gateup_swiglu_bf16(X0, Y0, NW0, 1e-6, XO0, 2560, W0, None, 2560, C0, 9728, 8, 9728, 2560,
+                                           None, None, 0, None)
+    assert gu == SK_ERR_NULL                              # missing up half
+    lm = lib.sk_rmsnorm_lm_argmax_bf16(X0, Y0, NW0, 1e-6, XO0, 2560, W0, 2560, C0, C0 + 512, 8, 151936, 2560,
+                                       None, None, 0, None)
+    assert lm == SK_ERR_WORKSPACE

@@ -43,3 +43,26 @@ def test_mfma_lds_shape_configs_valid(case, M):
 @pytest.mark.parametrize("M", [1, 8, 40])
 def test_mfma_lds_gateup_configs_valid(M):
     assert _lib.check_config(SK_OP_GATEUP, M, 9728, 2560, gp.mfmt_config(2560, 16, 16, 1, M)) == SK_OK
+
+
+gn = pytest.importorskip("tests.test_gpu_norm")
+
+
+@pytest.mark.parametrize("name", list(gn.NORM_CONFIGS))
+@pytest.mark.parametrize("M", [1, 3, 8, 16])
+def test_norm_test_configs_valid(name, M):
+    """The norm-prologue test configs: fused ones keep the projection's
+    workspace, unfused ones (global split, register-fragment MFMA) add the
+    normalised rows."""
+    from starter_amd._lib import SK_OP_RMSNORM_GEMM, SK_PATH_GEMV, SK_PATH_MFMA
+
+    cfg = gn.NORM_CONFIGS[name]
+    if cfg.path == SK_PATH_GEMV and M > 8:
+        return
+    assert _lib.check_config(SK_OP_RMSNORM_GEMM, M, 6144, 2560, cfg) == SK_OK
+    plain = _lib.workspace_bytes(SK_OP_GEMM, M, 6144, 2560, cfg)
+    normed = _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, M, 6144, 2560, cfg)
+    if cfg.split > 1 or cfg.path == SK_PATH_MFMA:
+        assert normed == (plain + 255) // 256 * 256 + M * 2560 * 2
+    else:
+        assert normed == plain, f"{name} should run the prologue fused"

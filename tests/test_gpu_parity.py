@@ -22,7 +22,7 @@ import oracle
 from starter_amd import kernels as K
 from starter_amd._lib import (SK_ERR_ALIGN, SK_ERR_CONFIG, SK_ERR_SHAPE, SK_ERR_WORKSPACE, SK_OP_GATEUP, SK_OP_GEMM,
                               SK_PATH_GEMV, SK_PATH_MFMA, SK_PATH_MFMA_LDS, SkConfig, SkError)
-from tests._util import (BF16, assert_gateup_parity, assert_parity, bits, from_bits, randn_bf16,
+from tests._util import (BF16, assert_gateup_parity, assert_parity, bits, check_argmax_rows, from_bits, randn_bf16,
                          reference_tolerance_ok)
 
 pytestmark = pytest.mark.gpu
@@ -213,22 +213,6 @@ def test_gateup_reference_grid_m16():
 # lm_head + fused argmax, standalone argmax
 # ---------------------------------------------------------------------------
 
-def _check_argmax_rows(ids, maxv, logits_bits: np.ndarray, o_ids, o_maxv, what: str):
-    ids = ids.cpu().numpy()
-    maxv = maxv.cpu().numpy()
-    Lf = oracle.bf16_to_f32(logits_bits)
-    for m in range(Lf.shape[0]):
-        row = Lf[m]
-        top = row[o_ids[m]]
-        second = np.max(np.where(np.arange(row.size) == o_ids[m], -np.inf, row))
-        if top - second > 1e-2:
-            assert ids[m] == o_ids[m], f"{what}: row {m} id {ids[m]} != {o_ids[m]} (margin {top - second})"
-            assert maxv[m] == o_maxv[m], f"{what}: row {m} maxv"
-        else:   # exact bf16 tie at the top: lowest tied index, same value
-            assert row[ids[m]] == top and maxv[m] == top, f"{what}: row {m} tie"
-            assert ids[m] == o_ids[m], f"{what}: row {m} tie not broken to the lowest index"
-
-
 LM_CONFIGS = {"default": None, "mfma_lds": SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=16, rows=16),
               "gemv": SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=4)}
 
@@ -246,7 +230,7 @@ def test_lm_argmax_full_vocab(M, cfg):
     ids, maxv = K.lm_argmax(x.to(DEV), _gpu(w), config=LM_CONFIGS[cfg])
     logits = oracle.gemm(bits(x), bits(w))
     o_ids, o_maxv = oracle.argmax(logits)
-    _check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax M={M} {cfg}")
+    check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax M={M} {cfg}")
 
 
 def test_lm_argmax_exact_ties_across_workgroups():
