@@ -193,6 +193,46 @@ int sk_rmsnorm_lm_argmax_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16*
                               int64_t ldx, const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M, int V,
                               int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/*
+ * Attention side of the decode step (head width D = 128 only).
+ *
+ * sk_qk_norm_rope_cache_bf16: per-head RMSNorm + rotary embedding + KV-cache
+ * write of one QKV projection buffer.  Replaces qk_norm_rope_cache
+ * (engine/kernels/rope.py:140-188; cast placement rope.py:17-30):
+ *   qkv     [B*T, ld_qkv] bf16, rows (b, t): HQ query heads | HKV key heads | HKV value heads
+ *   q_norm_w, k_norm_w [D]; cos, sin [rope_rows, D] bf16 (model.py:85-100 tables)
+ *   pos     [B] int32 device array: row (b, t) goes to slot pos[b] + t
+ *   q_out   [B, HQ, T, D]; k_cache, v_cache [B, HKV, cap, D] (one layer)
+ * Slots outside [0, cap) or outside the table are skipped (pos is device data,
+ * so the host cannot check it).  No workspace.
+ */
+int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w, const sk_bf16* k_norm_w,
+                               const sk_bf16* cos, const sk_bf16* sin, int rope_rows, const int32_t* pos,
+                               sk_bf16* q_out, sk_bf16* k_cache, sk_bf16* v_cache, int B, int T, int HQ, int HKV,
+                               int D, int cap, float eps, hipStream_t stream);
+
+/*
+ * sk_decode_attention_bf16: split-K grouped-query flash-decoding with a
+ * device-side length.  Replaces DecodeAttention (engine/kernels/attention.py:
+ * 152-202, kernels 23-149) for chain masks (no draft tree):
+ *   q      [B, HQ, R, D] bf16; k_cache, v_cache [B, HKV, cap, D] bf16
+ *   pos    [B] int32 device array: query row t of sequence b sees keys 0 .. pos[b] + t
+ *   out    [B, R, HQ, D] bf16 (rows (b, t) of [B*R, HQ*D])
+ *   max_len: the longest sequence the caller will attend over (bounds the
+ *            splits; 0 = cap); nsplit: key splits per (b, kv head), 0 = default
+ * (HQ/HKV) * R must be at most 8.  Scores and softmax statistics in fp32,
+ * probabilities rounded to bf16 before the PV product, fp32 accumulation
+ * (attention.py:9-11).  Needs a zero-filled workspace of
+ * sk_decode_attention_workspace_bytes() bytes when it splits the keys; the
+ * last workgroup of each (b, kv head) merges the splits in the same kernel and
+ * leaves the workspace counters at zero.
+ */
+size_t sk_decode_attention_workspace_bytes(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int nsplit);
+
+int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_bf16* v_cache, const int32_t* pos,
+                             sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                             int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Out[M,I] = bf16(bf16(silu(g)) * u) for gu[M, 2I] = [g | u] (row stride ld_gu).
  * Replaces swiglu (engine/kernels/swiglu.py:14-33). */
 int sk_swiglu_bf16(const sk_bf16* gu, int64_t ld_gu, sk_bf16* out, int64_t ld_out,

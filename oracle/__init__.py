@@ -57,6 +57,11 @@ def lib() -> ctypes.CDLL:
         h.oracle_f32_to_bf16.restype = ctypes.c_uint16
         h.oracle_swiglu_scalar.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
         h.oracle_swiglu_scalar.restype = ctypes.c_uint16
+        _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+        h.oracle_qk_norm_rope_cache_bf16.argtypes = [_u16p, _i64, _u16p, _u16p, _u16p, _u16p, _i32p, _u16p, _u16p,
+                                                     _u16p, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float]
+        h.oracle_decode_attention.argtypes = [_u16p, _u16p, _u16p, _i32p, _f32p, _i32, _i32, _i32, _i32, _i32, _i32,
+                                              ctypes.c_float, _i32]
         _lib = h
     return _lib
 
@@ -162,3 +167,35 @@ def swiglu_scalar(g: int, u: int) -> int:
 
 def f32_to_bf16_c(f: float) -> int:
     return int(lib().oracle_f32_to_bf16(f))
+
+
+def qk_norm_rope_cache(qkv: np.ndarray, qw: np.ndarray, kw: np.ndarray, cos: np.ndarray, sin: np.ndarray,
+                       pos: np.ndarray, q_out: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, T: int,
+                       eps: float) -> None:
+    """In place: q_out [B, HQ, T, D], k/v_cache [B, HKV, cap, D] at slots pos[b] + t
+    (engine/kernels/rope.py:140-188).  qkv [B*T, (HQ + 2*HKV)*D] bits."""
+    qkv = _u16(qkv)
+    B, HQ, _, D = q_out.shape
+    HKV, cap = k_cache.shape[1], k_cache.shape[2]
+    for a in (q_out, k_cache, v_cache):
+        if a.dtype != np.uint16 or not a.flags["C_CONTIGUOUS"]:
+            raise TypeError("outputs must be contiguous uint16 arrays")
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    if pos.min() < 0 or pos.max() + T > min(cap, cos.shape[0]):
+        raise ValueError("slots outside the cache or the rotary table")
+    lib().oracle_qk_norm_rope_cache_bf16(qkv, qkv.shape[1], _u16(qw), _u16(kw), _u16(cos), _u16(sin), pos, q_out,
+                                         k_cache, v_cache, B, T, HQ, HKV, D, cap, eps)
+
+
+def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, pos: np.ndarray,
+                     scale: float) -> np.ndarray:
+    """Exact attention of each query row (engine/kernels/attention.py:221-242):
+    q [B, HQ, R, D] bits, caches [B, HKV, cap, D] bits, pos [B] (row t sees keys
+    0 .. pos[b] + t).  Returns fp32 [B, R, HQ, D]."""
+    q, k_cache, v_cache = _u16(q), _u16(k_cache), _u16(v_cache)
+    B, HQ, R, D = q.shape
+    HKV, cap = k_cache.shape[1], k_cache.shape[2]
+    out = np.empty((B, R, HQ, D), dtype=np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    lib().oracle_decode_attention(q, k_cache, v_cache, pos, out, B, HQ, HKV, D, R, cap, scale, threads())
+    return out

@@ -20,6 +20,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 static inline float bf2f(uint16_t h) {
@@ -227,4 +228,93 @@ void oracle_lm_argmax_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, in
     ids[m] = best;
     maxv[m] = bv;
   }
+}
+
+/* Per-head RMSNorm + rotary embedding + KV-cache write (engine/kernels/rope.py:
+ * 17-30 cast placement, 140-188 layouts):
+ *   n = bf16(x * r), r = 1/sqrt(mean(x^2) + eps) (sum of squares formed
+ *   exactly, rounded once to fp32); y = bf16(w * n);
+ *   o[i]      = bf16(bf16(y[i] * cos[i])           + bf16(-y[i+D/2] * sin[i]))
+ *   o[i+D/2]  = bf16(bf16(y[i+D/2] * cos[i+D/2])   + bf16(y[i] * sin[i+D/2]))
+ * qkv [B*T, ld] rows (b, t) hold HQ query heads, HKV key heads, HKV value
+ * heads of width D; query heads go to q_out [B, HQ, T, D]; key heads
+ * (normalised, rotated) and value heads (raw) to the caches [B, HKV, cap, D]
+ * at slot pos[b] + t, which is also the rotary table row. */
+static void norm_rope_head(const uint16_t* x, const uint16_t* w, const uint16_t* c, const uint16_t* s, int D,
+                           float eps, uint16_t* o) {
+  double sq = 0.0;
+  for (int i = 0; i < D; ++i) {
+    const double v = (double)bf2f(x[i]);
+    sq += v * v;
+  }
+  const float r = 1.0f / sqrtf((float)sq / (float)D + eps);
+  const int H = D / 2;
+  for (int i = 0; i < H; ++i) {
+    const float y1 = round_bf(bf2f(w[i]) * round_bf(bf2f(x[i]) * r));
+    const float y2 = round_bf(bf2f(w[i + H]) * round_bf(bf2f(x[i + H]) * r));
+    o[i] = f2bf(round_bf(y1 * bf2f(c[i])) + round_bf(-y2 * bf2f(s[i])));
+    o[i + H] = f2bf(round_bf(y2 * bf2f(c[i + H])) + round_bf(y1 * bf2f(s[i + H])));
+  }
+}
+
+void oracle_qk_norm_rope_cache_bf16(const uint16_t* qkv, int64_t ld, const uint16_t* qw, const uint16_t* kw,
+                                    const uint16_t* cosT, const uint16_t* sinT, const int32_t* pos, uint16_t* q_out,
+                                    uint16_t* k_cache, uint16_t* v_cache, int B, int T, int HQ, int HKV, int D,
+                                    int cap, float eps) {
+  for (int b = 0; b < B; ++b)
+    for (int t = 0; t < T; ++t) {
+      const uint16_t* row = qkv + (int64_t)(b * T + t) * ld;
+      const int slot = pos[b] + t;
+      const uint16_t* c = cosT + (int64_t)slot * D;
+      const uint16_t* s = sinT + (int64_t)slot * D;
+      for (int h = 0; h < HQ; ++h)
+        norm_rope_head(row + (int64_t)h * D, qw, c, s, D, eps, q_out + ((int64_t)(b * HQ + h) * T + t) * D);
+      for (int h = 0; h < HKV; ++h) {
+        const int64_t cs = ((int64_t)(b * HKV + h) * cap + slot) * D;
+        norm_rope_head(row + (int64_t)(HQ + h) * D, kw, c, s, D, eps, k_cache + cs);
+        memcpy(v_cache + cs, row + (int64_t)(HQ + HKV + h) * D, (size_t)D * sizeof(uint16_t));
+      }
+    }
+}
+
+/* Decode attention (engine/kernels/attention.py:221-242, SDPA over the valid
+ * keys): query row t of sequence b (head h, KV head h / (HQ/HKV)) attends to
+ * keys 0 .. pos[b] + t with scores scale * q.k; softmax and the weighted sum
+ * of V are formed in fp64 from the bf16 inputs (exact attention, no bf16
+ * probabilities); out [B, R, HQ, D] fp32.  OpenMP over (b, h). */
+void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* pos,
+                             float* out, int B, int HQ, int HKV, int D, int R, int cap, float scale, int threads) {
+  const int G = HQ / HKV;
+#pragma omp parallel for collapse(2) schedule(dynamic) num_threads(threads > 0 ? threads : 1)
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < HQ; ++h) {
+      const int kh = h / G;
+      const uint16_t* K = k_cache + (int64_t)(b * HKV + kh) * cap * D;
+      const uint16_t* V = v_cache + (int64_t)(b * HKV + kh) * cap * D;
+      double* sc = (double*)malloc(sizeof(double) * (size_t)cap);
+      double* acc = (double*)malloc(sizeof(double) * (size_t)D);
+      for (int t = 0; t < R; ++t) {
+        const uint16_t* qr = q + ((int64_t)(b * HQ + h) * R + t) * D;
+        int L = pos[b] + t + 1;
+        if (L > cap) L = cap;
+        double mx = -INFINITY;
+        for (int n = 0; n < L; ++n) {
+          double d = 0.0;
+          for (int i = 0; i < D; ++i) d += (double)bf2f(qr[i]) * (double)bf2f(K[(int64_t)n * D + i]);
+          sc[n] = d * (double)scale;
+          if (sc[n] > mx) mx = sc[n];
+        }
+        double den = 0.0;
+        for (int i = 0; i < D; ++i) acc[i] = 0.0;
+        for (int n = 0; n < L; ++n) {
+          const double p = exp(sc[n] - mx);
+          den += p;
+          for (int i = 0; i < D; ++i) acc[i] += p * (double)bf2f(V[(int64_t)n * D + i]);
+        }
+        float* o = out + ((int64_t)(b * R + t) * HQ + h) * D;
+        for (int i = 0; i < D; ++i) o[i] = L > 0 ? (float)(acc[i] / den) : 0.0f;
+      }
+      free(sc);
+      free(acc);
+    }
 }

@@ -1,0 +1,461 @@
+// sk_attn.hip - decode attention side of the Qwen3 decode step on gfx950:
+//   * per-head RMSNorm + rotary embedding + KV-cache write of the QKV
+//     projection (engine/kernels/rope.py:94-188), and
+//   * split-K grouped-query flash-decoding over the KV cache with a
+//     device-side sequence length (engine/kernels/attention.py:23-202).
+// Both are memory-bound: the first touches (HQ + 2*HKV) * D values per row,
+// the second streams K and V of every valid position once per KV head.
+#include "starter_amd.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <string.h>
+
+#include "sk_kernels.hpp"
+
+namespace sk {
+
+constexpr int HEAD_D = 128;   // head width of Qwen3 (the only one compiled)
+
+// ---------------------------------------------------------------------------
+// q/k RMSNorm + RoPE + cache write (rope.py:94-188 cast placement):
+//   n = bf16(x * rsqrt(mean(x^2) + eps)); y = bf16(w * n)
+//   o1 = bf16(bf16(y1 * cos1) + bf16(-y2 * sin1)); o2 = bf16(bf16(y2 * cos2) + bf16(y1 * sin2))
+// with (y1, y2) = (y[i], y[i + D/2]).  One wave per head: lane i holds the
+// rotation pair (i, i + 64), so the rotation needs no lane exchange.  Workgroup
+// (row, head group): 4 waves, heads 4*hg .. 4*hg+3 of projection row (b, t);
+// heads < HQ are query heads (to q_out), then HKV key heads (normalised and
+// rotated into k_cache at slot pos[b] + t, their value heads copied raw to
+// v_cache).  A slot outside [0, cap) or outside the rotary table is skipped.
+// ---------------------------------------------------------------------------
+struct RopeArgs {
+  const uint16_t* qkv;
+  int64_t ld_qkv;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int rope_rows;
+  const int32_t* pos;
+  uint16_t* q_out;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int T, HQ, HKV, cap;
+  float eps;
+};
+
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(RopeArgs a) {
+  const int row = blockIdx.x;                       // (b, t)
+  const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (head >= a.HQ + a.HKV) return;                 // wave-uniform
+  const int b = row / a.T, t = row - (row / a.T) * a.T;
+  const int slot = a.pos[b] + t;
+  if (slot < 0 || slot >= a.rope_rows) return;
+  const bool is_q = head < a.HQ;
+  if (!is_q && slot >= a.cap) return;
+  const uint16_t* src = a.qkv + (int64_t)row * a.ld_qkv + (int64_t)head * HEAD_D;
+  const float x1 = bf2f(src[lane]), x2 = bf2f(src[lane + 64]);
+  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  const float r = 1.0f / sqrtf(ss / (float)HEAD_D + a.eps);
+  const uint16_t* w = is_q ? a.qw : a.kw;
+  const float y1 = round_bf(bf2f(w[lane]) * round_bf(x1 * r));
+  const float y2 = round_bf(bf2f(w[lane + 64]) * round_bf(x2 * r));
+  const uint16_t* cs = a.cos + (int64_t)slot * HEAD_D;
+  const uint16_t* sn = a.sin + (int64_t)slot * HEAD_D;
+  const float c1 = bf2f(cs[lane]), c2 = bf2f(cs[lane + 64]);
+  const float s1 = bf2f(sn[lane]), s2 = bf2f(sn[lane + 64]);
+  const uint16_t o1 = f2bf(round_bf(y1 * c1) + round_bf(-y2 * s1));
+  const uint16_t o2 = f2bf(round_bf(y2 * c2) + round_bf(y1 * s2));
+  if (is_q) {
+    uint16_t* dst = a.q_out + ((int64_t)(b * a.HQ + head) * a.T + t) * HEAD_D;
+    dst[lane] = o1;
+    dst[lane + 64] = o2;
+  } else {
+    const int kh = head - a.HQ;
+    const int64_t cslot = ((int64_t)(b * a.HKV + kh) * a.cap + slot) * HEAD_D;
+    a.k_cache[cslot + lane] = o1;
+    a.k_cache[cslot + lane + 64] = o2;
+    const uint16_t* vsrc = a.qkv + (int64_t)row * a.ld_qkv + (int64_t)(a.HQ + a.HKV + kh) * HEAD_D;
+    a.v_cache[cslot + lane] = vsrc[lane];
+    a.v_cache[cslot + lane + 64] = vsrc[lane + 64];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-K GQA flash-decoding (attention.py:23-149 numerics: scores and
+// softmax statistics in fp32, probabilities rounded to bf16 before the PV
+// product, fp32 accumulation, one normalisation at the end).
+//
+// Workgroup (b, kv head, split s): 4 waves stream keys [s*split_len, ...)
+// clipped to the row's valid length pos[b] + t + 1.  Lane layout: lane l holds
+// dims 8*(l%16) .. +7 of key (l/16) of the wave's 4-key step, so one 16-byte
+// load per lane reads 4 consecutive keys (1 KiB) of K and of V.  Every query
+// row of the KV head's group (QR = G*R rows) is processed by the same lanes:
+// q . k partial dot over 8 dims (v_dot2_f32_bf16), summed over the 16 lanes
+// of a DPP row; P.V pairs the bf16 probabilities of two keys with their value
+// rows (v_perm_b32) so each v_dot2 adds two keys' terms in fp32.  Each
+// lane group keeps an online-softmax stream (m, l, acc[8 dims]) over its keys,
+// rescaled once per block of KB keys; the 4 streams of a wave are merged with
+// lane exchanges, the 4 waves in LDS, both in a fixed order.  With several
+// splits, the partial
+// (m, l, acc) goes to the workspace and the last workgroup of the (b, kv head)
+// to arrive merges the splits in split order (no second kernel).
+// ---------------------------------------------------------------------------
+struct AttnArgs {
+  const uint16_t* q;        // [B, HQ, R, D]
+  const uint16_t* k;        // [B, HKV, cap, D]
+  const uint16_t* v;
+  const int32_t* pos;       // [B]: position of query row 0
+  uint16_t* out;            // [B, R, HQ, D]
+  float* part_o;            // [B*HKV, S, QR, D]
+  float* part_ml;           // [B*HKV, S, QR, 2]
+  unsigned* tickets;        // [B*HKV]
+  int HQ, HKV, R, G, cap, S, split_len;
+  float scale;
+};
+
+constexpr int ATTN_WAVES = 4;
+constexpr int ATTN_KB = 4;     // keys per lane stream between rescales
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the total.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = dpp_add(v, 0);
+  v = dpp_add(v, 1);
+  v = dpp_add(v, 2);
+  v = dpp_add(v, 3);
+  return v;
+}
+
+template <int QR>
+__global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a) {
+  __shared__ float s_m[ATTN_WAVES][QR], s_l[ATTN_WAVES][QR];
+  __shared__ __attribute__((aligned(16))) float s_acc[ATTN_WAVES][QR][HEAD_D];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int dg = lane & 15, kr = lane >> 4;
+  const int S = a.S;
+  const int bk = blockIdx.x / S, s = blockIdx.x - (blockIdx.x / S) * S;
+  const int b = bk / a.HKV, kh = bk - (bk / a.HKV) * a.HKV;
+  const int pos = a.pos[b];
+  const int start = s * a.split_len;
+  // keys this workgroup may touch: below the longest row's length and the cache
+  const int end = min(min(start + a.split_len, pos + a.R), a.cap);
+
+  // Query rows (t, g): head kh*G + g, query row t; fp32 copies of this lane's 8 dims.
+  u32x4 qf[QR];   // 8 bf16 of this lane's dims (zero for padding rows)
+  int row_lim[QR];
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    const int t = r / a.G, g = r - (r / a.G) * a.G;
+    const bool real = t < a.R;
+    const int head = kh * a.G + g;
+    const uint16_t* qp = a.q + ((int64_t)(b * a.HQ + min(head, a.HQ - 1)) * a.R + min(t, a.R - 1)) * HEAD_D + 8 * dg;
+    const u32x4 v = ld16(qp);
+    qf[r] = real ? v : u32x4{0u, 0u, 0u, 0u};
+    row_lim[r] = real ? pos + t : -1;   // last visible key of the row
+  }
+
+  float m[QR], l[QR], acc[QR][8];
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[r][d] = 0.f;
+  }
+
+  // Block: KB keys per lane group, 4 lane groups, ATTN_WAVES waves.  The next
+  // block's K/V rows are loaded while the current one is processed (keys past
+  // `end` reload the last valid row and are masked).
+  const int64_t kv_base = (int64_t)bk * a.cap * HEAD_D + 8 * dg;
+  const int step = 4 * ATTN_WAVES * ATTN_KB;
+  auto load_block = [&](int n0, u32x4* kv, u32x4* vv) {
+#pragma unroll
+    for (int j = 0; j < ATTN_KB; ++j) {
+      const int nc = max(min(n0 + 4 * ATTN_WAVES * j + 4 * wave + kr, end - 1), 0);
+      kv[j] = ld16(a.k + kv_base + (int64_t)nc * HEAD_D);
+      vv[j] = ld16(a.v + kv_base + (int64_t)nc * HEAD_D);
+    }
+  };
+  u32x4 kv[ATTN_KB], vv[ATTN_KB];
+  if (start < end) load_block(start, kv, vv);
+  for (int n0 = start; n0 < end; n0 += step) {
+    u32x4 kn[ATTN_KB], vn[ATTN_KB];
+    load_block(n0 + step, kn, vn);
+    int key[ATTN_KB];
+#pragma unroll
+    for (int j = 0; j < ATTN_KB; ++j) key[j] = n0 + 4 * ATTN_WAVES * j + 4 * wave + kr;
+    // V of key pairs (j, j+1) per dim, packed as bf16 pairs for v_dot2:
+    // vp[jp][c][0] = (V_j[2c], V_j+1[2c]), vp[jp][c][1] = (V_j[2c+1], V_j+1[2c+1]).
+    uint32_t vp[ATTN_KB / 2][4][2];
+#pragma unroll
+    for (int jp = 0; jp < ATTN_KB / 2; ++jp)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        vp[jp][c][0] = __builtin_amdgcn_perm(vv[2 * jp + 1][c], vv[2 * jp][c], 0x05040100u);
+        vp[jp][c][1] = __builtin_amdgcn_perm(vv[2 * jp + 1][c], vv[2 * jp][c], 0x07060302u);
+      }
+#pragma unroll
+    for (int r = 0; r < QR; ++r) {
+      float sc[ATTN_KB];
+      float mx = m[r];
+#pragma unroll
+      for (int j = 0; j < ATTN_KB; ++j) {
+        const float dot = row16_sum(dot8(kv[j], qf[r], 0.f)) * a.scale;
+        sc[j] = (key[j] < end && key[j] <= row_lim[r]) ? dot : -INFINITY;
+        mx = fmaxf(mx, sc[j]);
+      }
+      const float msafe = mx == -INFINITY ? 0.f : mx;
+      const float alpha = __expf(m[r] - msafe);
+      float lsum = l[r] * alpha;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[r][d] *= alpha;
+#pragma unroll
+      for (int jp = 0; jp < ATTN_KB / 2; ++jp) {
+        const float p0 = __expf(sc[2 * jp] - msafe), p1 = __expf(sc[2 * jp + 1] - msafe);
+        lsum += p0;
+        lsum += p1;
+        const bf16x2 pp = {(__bf16)p0, (__bf16)p1};   // probabilities rounded to bf16 (RNE)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[r][2 * c] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vp[jp][c][0]),
+                                                          acc[r][2 * c], false);
+          acc[r][2 * c + 1] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vp[jp][c][1]),
+                                                              acc[r][2 * c + 1], false);
+        }
+      }
+      l[r] = lsum;
+      m[r] = mx;
+    }
+#pragma unroll
+    for (int j = 0; j < ATTN_KB; ++j) {
+      kv[j] = kn[j];
+      vv[j] = vn[j];
+    }
+  }
+
+  // Merge the 4 lane-group streams of each wave (lanes l, l^16, l^32, l^48
+  // hold the same dims), then the waves' results in LDS in wave order.
+#pragma unroll
+  for (int r = 0; r < QR; ++r) {
+    float M = fmaxf(m[r], __shfl_xor(m[r], 16));
+    M = fmaxf(M, __shfl_xor(M, 32));
+    const float w = m[r] == -INFINITY ? 0.f : __expf(m[r] - M);
+    float lw = l[r] * w;
+    lw += __shfl_xor(lw, 16);
+    lw += __shfl_xor(lw, 32);
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      float o = acc[r][d] * w;
+      o += __shfl_xor(o, 16);
+      o += __shfl_xor(o, 32);
+      acc[r][d] = o;
+    }
+    if (lane == 0) {
+      s_m[wave][r] = M;
+      s_l[wave][r] = lw;
+    }
+    if (kr == 0) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) s_acc[wave][r][8 * dg + d] = acc[r][d];
+    }
+  }
+  __syncthreads();
+  const bool single = (S == 1);
+  for (int idx = threadIdx.x; idx < QR * HEAD_D; idx += 64 * ATTN_WAVES) {
+    const int r = idx / HEAD_D, d = idx - (idx / HEAD_D) * HEAD_D;
+    float M = -INFINITY;
+    for (int wv = 0; wv < ATTN_WAVES; ++wv) M = fmaxf(M, s_m[wv][r]);
+    float L = 0.f, O = 0.f;
+    for (int wv = 0; wv < ATTN_WAVES; ++wv) {
+      const float w = s_m[wv][r] == -INFINITY ? 0.f : __expf(s_m[wv][r] - M);
+      L += w * s_l[wv][r];
+      O += w * s_acc[wv][r][d];
+    }
+    const int t = r / a.G, g = r - (r / a.G) * a.G;
+    if (single) {
+      if (t < a.R)
+        a.out[((int64_t)(b * a.R + t) * a.HQ + kh * a.G + g) * HEAD_D + d] = f2bf(L > 0.f ? O / L : 0.f);
+    } else {
+      const int64_t pr = ((int64_t)bk * S + s) * QR + r;
+      store_agent(&a.part_o[pr * HEAD_D + d], O);
+      if (d == 0) {
+        store_agent(&a.part_ml[2 * pr], M);
+        store_agent(&a.part_ml[2 * pr + 1], L);
+      }
+    }
+  }
+  if (single) return;
+
+  // Last workgroup of this (b, kv head) merges the splits in split order.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = take_ticket(&a.tickets[bk], (unsigned)S) ? 1 : 0;
+  __syncthreads();
+  if (!s_last) return;
+  for (int idx = threadIdx.x; idx < QR * HEAD_D; idx += 64 * ATTN_WAVES) {
+    const int r = idx / HEAD_D, d = idx - (idx / HEAD_D) * HEAD_D;
+    const int t = r / a.G, g = r - (r / a.G) * a.G;
+    if (t >= a.R) continue;
+    float M = -INFINITY;
+    for (int sp = 0; sp < S; ++sp) M = fmaxf(M, load_agent(&a.part_ml[2 * (((int64_t)bk * S + sp) * QR + r)]));
+    float L = 0.f, O = 0.f;
+    for (int sp = 0; sp < S; ++sp) {
+      const int64_t pr = ((int64_t)bk * S + sp) * QR + r;
+      const float ms = load_agent(&a.part_ml[2 * pr]);
+      const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+      L += w * load_agent(&a.part_ml[2 * pr + 1]);
+      O += w * load_agent(&a.part_o[pr * HEAD_D + d]);
+    }
+    a.out[((int64_t)(b * a.R + t) * a.HQ + kh * a.G + g) * HEAD_D + d] = f2bf(L > 0.f ? O / L : 0.f);
+  }
+}
+
+}  // namespace sk
+
+namespace {
+
+constexpr int kAttnMaxQR = 8;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+int cdiv(int a, int b) { return (a + b - 1) / b; }
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+struct AttnPlan {
+  int QR = 0, S = 0, split_len = 0;
+  size_t tickets = 0, part_o = 0, part_ml = 0, need = 0;
+};
+
+// Splits: enough workgroups to give every compute unit several (the keys of
+// one (b, kv head) pair are split when B*HKV alone cannot fill the chip), each
+// split a whole number of 64-key workgroup blocks of the longest sequence the
+// plan will see.
+int attn_plan(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int nsplit, AttnPlan* p) {
+  if (B < 1 || HKV < 1 || HQ < HKV || HQ % HKV != 0 || R < 1 || cap < 1 || D != sk::HEAD_D) return SK_ERR_SHAPE;
+  const int G = HQ / HKV;
+  const int QR = G * R;
+  if (QR > kAttnMaxQR) return SK_ERR_SHAPE;
+  p->QR = QR <= 4 ? 4 : 8;
+  const int work = max_len > 0 && max_len < cap ? max_len : cap;
+  const int block = 4 * sk::ATTN_WAVES * sk::ATTN_KB;
+  const int blocks = cdiv(work, block);
+  int S = nsplit;
+  if (S <= 0) {
+    const long pairs = (long)B * HKV;
+    S = (int)((1024 + pairs - 1) / pairs);   // about 4 workgroups per CU of an MI355X
+    if (S > 32) S = 32;
+  }
+  if (S > blocks) S = blocks;
+  if (S < 1) S = 1;
+  p->split_len = cdiv(blocks, S) * block;
+  p->S = cdiv(work, p->split_len);
+  if (p->S == 1) {
+    p->need = 0;
+    return SK_OK;
+  }
+  const size_t pairs = (size_t)B * HKV;
+  p->tickets = align256(pairs * sizeof(unsigned));
+  p->part_o = pairs * p->S * p->QR * sk::HEAD_D * sizeof(float);
+  p->part_ml = pairs * p->S * p->QR * 2 * sizeof(float);
+  p->need = p->tickets + align256(p->part_o) + p->part_ml;
+  return SK_OK;
+}
+
+int attn_launch_status() { return hipGetLastError() == hipSuccess ? SK_OK : SK_ERR_LAUNCH; }
+
+int attn_device_ok() {
+  int dev = 0;
+  hipDeviceProp_t prop;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return SK_ERR_DEVICE;
+  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? SK_OK : SK_ERR_DEVICE;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w, const sk_bf16* k_norm_w,
+                               const sk_bf16* cos, const sk_bf16* sin, int rope_rows, const int32_t* pos,
+                               sk_bf16* q_out, sk_bf16* k_cache, sk_bf16* v_cache, int B, int T, int HQ, int HKV,
+                               int D, int cap, float eps, hipStream_t stream) {
+  if (B < 0 || T < 0 || HQ < 1 || HKV < 1 || cap < 1 || rope_rows < 1 || D != sk::HEAD_D) return SK_ERR_SHAPE;
+  if (ld_qkv < (int64_t)(HQ + 2 * HKV) * D) return SK_ERR_SHAPE;
+  if ((long)B * T > 0x7FFFFFFFL) return SK_ERR_SHAPE;
+  if (B == 0 || T == 0) return SK_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !pos || !q_out || !k_cache || !v_cache) return SK_ERR_NULL;
+  int st = attn_device_ok();
+  if (st) return st;
+  sk::RopeArgs a;
+  a.qkv = qkv;
+  a.ld_qkv = ld_qkv;
+  a.qw = q_norm_w;
+  a.kw = k_norm_w;
+  a.cos = cos;
+  a.sin = sin;
+  a.rope_rows = rope_rows;
+  a.pos = pos;
+  a.q_out = q_out;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.T = T;
+  a.HQ = HQ;
+  a.HKV = HKV;
+  a.cap = cap;
+  a.eps = eps;
+  const unsigned groups = (unsigned)cdiv(HQ + HKV, 4);
+  sk::qk_norm_rope_kernel<<<dim3((unsigned)(B * T), groups), dim3(256), 0, stream>>>(a);
+  return attn_launch_status();
+}
+
+size_t sk_decode_attention_workspace_bytes(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int nsplit) {
+  AttnPlan p;
+  if (attn_plan(B, HQ, HKV, D, R, cap, max_len, nsplit, &p)) return 0;
+  return p.need;
+}
+
+int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_bf16* v_cache, const int32_t* pos,
+                             sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                             int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (B < 0) return SK_ERR_SHAPE;
+  if (B == 0) return SK_OK;
+  AttnPlan p;
+  int st = attn_plan(B, HQ, HKV, D, R, cap, max_len, nsplit, &p);
+  if (st) return st;
+  if (!q || !k_cache || !v_cache || !pos || !out) return SK_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return SK_ERR_ALIGN;
+  if (p.need > 0 && (!ws || ws_bytes < p.need)) return SK_ERR_WORKSPACE;
+  st = attn_device_ok();
+  if (st) return st;
+  sk::AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.pos = pos;
+  a.out = out;
+  if (p.need > 0) {
+    char* w = static_cast<char*>(ws);
+    a.tickets = reinterpret_cast<unsigned*>(w);
+    a.part_o = reinterpret_cast<float*>(w + p.tickets);
+    a.part_ml = reinterpret_cast<float*>(w + p.tickets + align256(p.part_o));
+  }
+  a.HQ = HQ;
+  a.HKV = HKV;
+  a.R = R;
+  a.G = HQ / HKV;
+  a.cap = cap;
+  a.S = p.S;
+  a.split_len = p.split_len;
+  a.scale = scale;
+  const dim3 grid((unsigned)(B * HKV * p.S));
+  if (p.QR == 4)
+    sk::decode_attn_kernel<4><<<grid, dim3(64 * sk::ATTN_WAVES), 0, stream>>>(a);
+  else
+    sk::decode_attn_kernel<8><<<grid, dim3(64 * sk::ATTN_WAVES), 0, stream>>>(a);
+  return attn_launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,247 @@
+"""Synthetic Qwen3 greedy decode on the HIP hot path.
+
+Mirrors the reference's decode forward (engine/model.py:182-210 ``run_layers``,
+215-330 ``Plan``; engine/engine.py:198-230 graph capture and replay) with this
+package's kernels in every decode-step op:
+
+* ``mm["qkv"]`` / ``mm["gu"]`` / ``mm["lm"]``: residual add + RMSNorm fused into
+  the projection (``SkinnyMatmul`` / ``SkinnyGateUp`` / ``LmArgmax`` with the
+  norm prologue); ``mm["o"]`` / ``mm["d"]``: ``SkinnyMatmul``;
+* q/k RMSNorm + RoPE + KV write: ``qk_norm_rope_cache``;
+* attention: ``DecodeAttention`` (split-K GQA flash-decoding);
+* the greedy token: argmax fused into the lm_head kernel.
+
+The token embedding gather, the per-step position increment and the prefill
+pass (bf16 GEMMs through torch, SDPA over the prompt, as the reference's own
+prefill does, model.py:264-289) are torch plumbing around them.  Weights are
+random (``N(0, 0.02)`` projections, unit norm gains), so the generated text is
+meaningless; the work per step is that of the real model.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+
+BF16 = torch.bfloat16
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    """Qwen3-4B by default (RoPE theta 1e6)."""
+
+    hidden: int = 2560
+    intermediate: int = 9728
+    layers: int = 36
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+
+
+def rope_tables(cfg: Qwen3Config, max_pos: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16 cos/sin tables [max_pos, D] built like the reference (engine/model.py:85-100):
+    fp32 inverse frequencies, fp32 outer product, ``cat(freqs, freqs)``, then
+    cos/sin, then bf16.  Computed on the CPU (no TF32 question) and copied."""
+    D = cfg.head_dim
+    inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
+    positions = torch.arange(max_pos, dtype=torch.float32)
+    freqs = (inv_freq[:, None].float() @ positions[None, :].float()).transpose(0, 1)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(BF16).contiguous().to(device), emb.sin().to(BF16).contiguous().to(device)
+
+
+@dataclass
+class Layer:
+    in_norm: torch.Tensor
+    wqkv: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    wo: torch.Tensor
+    post_norm: torch.Tensor
+    wgu: torch.Tensor
+    wd: torch.Tensor
+
+
+class SyntheticModel:
+    """Random-init weights of the reference layout (engine/model.py:102-130):
+    fused q|k|v and gate|up rows, tied embeddings / lm_head."""
+
+    def __init__(self, cfg: Qwen3Config = Qwen3Config(), device="cuda:0", seed: int = 0, norm_noise: float = 0.0):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        H, I, D = cfg.hidden, cfg.intermediate, cfg.head_dim
+        HQ, HKV = cfg.heads, cfg.kv_heads
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=self.device) * 0.02).to(BF16)
+
+        def gain(n):
+            if norm_noise == 0.0:
+                return torch.ones(n, dtype=BF16, device=self.device)
+            return (1 + norm_noise * torch.randn(n, generator=g, device=self.device)).to(BF16)
+
+        self.embed = w(cfg.vocab, H)
+        self.lm_head = self.embed
+        self.final_norm = gain(H)
+        self.layers = [Layer(in_norm=gain(H), wqkv=w((HQ + 2 * HKV) * D, H), q_norm=gain(D), k_norm=gain(D),
+                             wo=w(H, HQ * D), post_norm=gain(H), wgu=w(2 * I, H), wd=w(H, I))
+                       for _ in range(cfg.layers)]
+        self.scale = 1.0 / math.sqrt(D)
+
+
+class DecodePlan:
+    """Static buffers, KV cache and step functions for one (B, T, max_new) shape
+    (engine/model.py:215-262).  ``decode()`` touches only preallocated tensors
+    and library workspaces, so it can be captured into a HIP graph."""
+
+    def __init__(self, model: SyntheticModel, B: int, T: int, max_new: int):
+        self.model = model
+        cfg = model.cfg
+        self.B, self.T, self.max_new = B, T, max_new
+        self.cap = ((T + max(max_new, 256) + 2 * 64 + 63) // 64) * 64     # engine/model.py:224
+        dev = model.device
+        H, I, D, HQ, HKV = cfg.hidden, cfg.intermediate, cfg.head_dim, cfg.heads, cfg.kv_heads
+        self.cos, self.sin = rope_tables(cfg, self.cap, dev)
+        self.ids = torch.zeros((B, T), dtype=torch.int64, device=dev)
+        self.tok = torch.zeros((B,), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros((B,), dtype=torch.int32, device=dev)
+        self.k_cache = torch.zeros((cfg.layers, B, HKV, self.cap, D), dtype=BF16, device=dev)
+        self.v_cache = torch.zeros((cfg.layers, B, HKV, self.cap, D), dtype=BF16, device=dev)
+        self.zero = torch.zeros((B, H), dtype=BF16, device=dev)
+        self.xa = torch.empty((B, H), dtype=BF16, device=dev)
+        self.xb = torch.empty((B, H), dtype=BF16, device=dev)
+        self.q = torch.empty((B, HQ, 1, D), dtype=BF16, device=dev)
+        self.attn_out = torch.empty((B, 1, HQ, D), dtype=BF16, device=dev)
+        self.attention = K.DecodeAttention(B, HQ, HKV, D, self.cap, dev, maxlen=min(self.cap, T + max_new))
+        # the decode-step projections (decode_matmuls, engine/model.py:137-179)
+        self.mm_qkv = K.SkinnyMatmul(B, (HQ + 2 * HKV) * D, H, dev, normed=True)
+        self.mm_o = K.SkinnyMatmul(B, H, HQ * D, dev)
+        self.mm_gu = K.SkinnyGateUp(B, I, H, dev, normed=True)
+        self.mm_d = K.SkinnyMatmul(B, H, I, dev)
+        self.mm_lm = K.LmArgmax(B, cfg.vocab, H, dev, normed=True)
+        self.g_decode = None
+
+    # -- prefill (torch GEMMs + SDPA, this package's norm/rope/swiglu/argmax) --
+    @torch.inference_mode()
+    def prefill(self) -> None:
+        """Consume ``ids`` from position 0; leaves the first generated token in
+        ``tok`` and ``pos = T`` (engine/model.py:264-289)."""
+        m, cfg = self.model, self.model.cfg
+        B, T = self.B, self.T
+        HQ, D = cfg.heads, cfg.head_dim
+        self.pos.zero_()
+        x = F.embedding(self.ids.view(-1), m.embed)
+        zero = torch.zeros_like(x)
+        h = K.add_rms_norm(x, zero, m.layers[0].in_norm, cfg.eps, xout=torch.empty_like(x))
+        q = torch.empty((B, HQ, T, D), dtype=BF16, device=x.device)
+        for i, layer in enumerate(m.layers):
+            k_i, v_i = self.k_cache[i], self.v_cache[i]
+            qkv = h @ layer.wqkv.t()
+            K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.pos, q, k_i, v_i, T,
+                                 cfg.eps)
+            a = F.scaled_dot_product_attention(q, k_i[:, :, :T].contiguous(), v_i[:, :, :T].contiguous(),
+                                               is_causal=True, scale=m.scale, enable_gqa=True)
+            o = a.transpose(1, 2).reshape(B * T, HQ * D) @ layer.wo.t()
+            h2 = K.add_rms_norm(x, o, layer.post_norm, cfg.eps)
+            d = K.swiglu(h2 @ layer.wgu.t()) @ layer.wd.t()
+            nxt = m.layers[i + 1].in_norm if i + 1 < len(m.layers) else m.final_norm
+            h = K.add_rms_norm(x, d, nxt, cfg.eps)
+        logits = h.view(B, T, cfg.hidden)[:, -1].contiguous() @ m.lm_head.t()
+        ids, _ = K.argmax(logits)
+        self.tok.copy_(ids)
+        self.pos.fill_(T)
+
+    # -- one decode step: run_layers (engine/model.py:182-210) + greedy token --
+    def decode(self) -> None:
+        """Consume ``tok`` at ``pos``; writes the next greedy token to ``tok``
+        and advances ``pos``."""
+        m, cfg = self.model, self.model.cfg
+        B = self.B
+        x = F.embedding(self.tok, m.embed)
+        cur, y = x, self.zero
+        for i, layer in enumerate(m.layers):
+            qkv = self.mm_qkv(cur, layer.wqkv, norm=(y, layer.in_norm, self.xa, cfg.eps))
+            K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.pos, self.q,
+                                 self.k_cache[i], self.v_cache[i], 1, cfg.eps)
+            self.attention(self.q, self.k_cache[i], self.v_cache[i], self.pos, self.attn_out)
+            o = self.mm_o(self.attn_out.view(B, cfg.heads * cfg.head_dim), layer.wo)
+            I = cfg.intermediate
+            act = self.mm_gu(self.xa, layer.wgu[:I], layer.wgu[I:], norm=(o, layer.post_norm, self.xb, cfg.eps))
+            y = self.mm_d(act, layer.wd)
+            cur = self.xb
+        ids, _ = self.mm_lm(cur, m.lm_head, norm=(y, m.final_norm, self.xa, cfg.eps))
+        self.tok.copy_(ids)
+        self.pos.add_(1)
+
+    def capture(self) -> None:
+        """Capture one decode step into a HIP graph (engine/engine.py:198-215).
+        Call after prefill; the captured step is replayed as the sequence grows
+        (the attention length and cache slots come from ``pos`` on the device)."""
+        tok0, pos0 = self.tok.clone(), self.pos.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.decode()                       # warm (writes slot pos; restored below)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.tok.copy_(tok0)
+        self.pos.copy_(pos0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.decode()
+        torch.cuda.synchronize()
+        self.tok.copy_(tok0)
+        self.pos.copy_(pos0)
+        self.g_decode = g
+
+    def step(self) -> None:
+        if self.g_decode is None:
+            self.decode()
+        else:
+            self.g_decode.replay()
+
+    @torch.inference_mode()
+    def generate(self, ids: torch.Tensor, max_new: int | None = None) -> torch.Tensor:
+        """Greedy tokens [B, max_new]: the prefill's token, then one per decode step."""
+        max_new = self.max_new if max_new is None else max_new
+        self.ids.copy_(ids)
+        self.prefill()
+        out = torch.empty((self.B, max_new), dtype=torch.int64, device=self.ids.device)
+        out[:, 0] = self.tok
+        for t in range(1, max_new):
+            self.step()
+            out[:, t] = self.tok
+        return out
+
+
+def time_decode(plan: DecodePlan, steps: int) -> dict:
+    """Decode throughput the way the reference defines it (B tokens per step,
+    QWEN_ENGINE_CONTRACT.md:93-102): ``steps`` graph replays after a prefill,
+    bracketed by HIP events on the replay stream.  Returns tok/s, ms per step
+    and the prefill time."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan.prefill()
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    if plan.g_decode is None:
+        plan.capture()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        plan.g_decode.replay()
+    b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b)
+    return {"tok_s": plan.B * steps / (ms * 1e-3), "ms_per_step": ms / steps, "steps": steps,
+            "prefill_s": prefill_s, "e2e_tok_s": plan.B * (steps + 1) / (prefill_s + ms * 1e-3)}

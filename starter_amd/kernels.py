@@ -18,6 +18,8 @@ _norm_stats + _normed_tile   rmsnorm_gemm / rmsnorm_gateup_swiglu / rmsnorm_lm_a
 add_rms_norm  add_rmsnorm.py add_rms_norm (sk_add_rmsnorm_bf16)
 swiglu        swiglu.py      swiglu (sk_swiglu_bf16)
 fast_topk[0]  topk.py:40     argmax (sk_argmax_bf16)
+qk_norm_rope_cache rope.py   qk_norm_rope_cache (sk_qk_norm_rope_cache_bf16)
+DecodeAttention attention.py DecodeAttention (sk_decode_attention_bf16, chain masks)
 logits.argmax engine.py:207  LmArgmax (sk_lm_argmax_bf16, fused into lm_head)
 ===========================  ==================================================
 
@@ -27,6 +29,8 @@ pool, as in the reference), workspaces once per instance.
 """
 
 from __future__ import annotations
+
+import math
 
 import torch
 
@@ -43,6 +47,7 @@ __all__ = [
     "add_rms_norm", "swiglu", "pick_matmul", "pick_gateup", "pick_normed", "pick_lm_argmax", "SkConfig",
     "SK_PATH_MFMA", "SK_PATH_GEMV", "SK_OP_GEMM", "SK_OP_GATEUP", "SK_OP_LM_ARGMAX", "SK_OP_ARGMAX",
     "SK_OP_RMSNORM_GEMM", "SK_OP_RMSNORM_GATEUP", "SK_OP_RMSNORM_LM_ARGMAX",
+    "qk_norm_rope_cache", "DecodeAttention",
 ]
 
 
@@ -282,6 +287,82 @@ def swiglu(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     check(lib().sk_swiglu_bf16(gu.data_ptr(), gu.stride(0), out.data_ptr(), out.stride(0), M, I, _stream(gu)),
           "sk_swiglu_bf16")
     return out
+
+
+# ---------------------------------------------------------------------------
+# Attention side of the decode step
+# ---------------------------------------------------------------------------
+
+def _i32_dev(t: torch.Tensor, name: str) -> None:
+    _need(t.is_cuda and t.dtype == torch.int32 and t.is_contiguous(), f"{name} must be a contiguous int32 device tensor")
+
+
+def qk_norm_rope_cache(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
+                       sin: torch.Tensor, pos: torch.Tensor, q_out: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, T: int, eps: float, fused: bool = True,
+                       depth: torch.Tensor | None = None) -> None:
+    """Normalise, rotate and scatter one projection buffer (engine/kernels/rope.py:140-188).
+
+    qkv [B*T, (HQ + 2*HKV)*D] rows (b, t); pos [B] int32 (row (b, t) -> slot
+    pos[b] + t); q_out [B, HQ, T, D]; k_cache / v_cache [B, HKV, cap, D] (one
+    layer).  ``fused`` is accepted for signature compatibility (there is one
+    launch either way); draft-tree depths are not supported."""
+    if depth is not None:
+        raise NotImplementedError("draft-tree rotary positions (depth=) are not supported")
+    _mat(qkv, "qkv")
+    B, HQ, T_, D = q_out.shape
+    _need(T_ == T, "q_out must be [B, HQ, T, D]")
+    HKV, cap = k_cache.shape[1], k_cache.shape[2]
+    _need(q_out.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous outputs")
+    _need(k_cache.shape == v_cache.shape and k_cache.shape[0] == B and k_cache.shape[3] == D, "cache shapes")
+    _need(qkv.shape[0] == B * T and qkv.shape[1] >= (HQ + 2 * HKV) * D, "qkv shape")
+    _need(cos.shape == sin.shape and cos.shape[1] == D and cos.is_contiguous() and sin.is_contiguous(), "rope tables")
+    _i32_dev(pos, "pos")
+    _device_guard(qkv)
+    check(lib().sk_qk_norm_rope_cache_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+                                           cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(),
+                                           q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), B, T, HQ, HKV,
+                                           D, cap, float(eps), _stream(qkv)), "sk_qk_norm_rope_cache_bf16")
+
+
+class DecodeAttention:
+    """Workspace-owning wrapper; one instance per (B, HQ, cap) plan
+    (engine/kernels/attention.py:152-202).  Split count and key ranges are
+    fixed at construction from ``maxlen`` (default cap); the valid length of
+    each sequence is read from ``pos`` on the device at every call, so one
+    instance replays inside a graph while the sequences grow.  Draft trees are
+    not supported; ``block_n``/``num_warps``/``num_stages`` are accepted for
+    signature compatibility."""
+
+    def __init__(self, B: int, HQ: int, HKV: int, D: int, cap: int, device, nsplit: int | None = None,
+                 block_n: int = 64, num_warps: int = 4, num_stages: int = 2, R: int = 1, tree: bool = False,
+                 maxlen: int | None = None):
+        if tree:
+            raise NotImplementedError("draft-tree masks are not supported")
+        self.B, self.HQ, self.HKV, self.D, self.cap, self.R = B, HQ, HKV, D, cap, R
+        self.maxlen = maxlen or 0
+        self.nsplit = nsplit or 0
+        self.scale = 1.0 / math.sqrt(D)
+        n = int(lib().sk_decode_attention_workspace_bytes(B, HQ, HKV, D, R, cap, self.maxlen, self.nsplit))
+        self.ws = torch.zeros(n, dtype=torch.uint8, device=device) if n else None
+
+    def __call__(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                 out: torch.Tensor, tree: torch.Tensor | None = None) -> None:
+        """q [B, HQ, R, D] bf16; k/v_cache [B, HKV, cap, D]; pos [B] int32 (position of
+        query row 0); out [B, R, HQ, D] bf16."""
+        if tree is not None:
+            raise NotImplementedError("draft-tree masks are not supported")
+        B, HQ, HKV, D, R, cap = self.B, self.HQ, self.HKV, self.D, self.R, self.cap
+        _need(q.shape == (B, HQ, R, D) and q.is_contiguous() and q.dtype == BF16, "q must be [B, HQ, R, D] bf16")
+        _need(k_cache.shape == (B, HKV, cap, D) and v_cache.shape == k_cache.shape, "cache shapes")
+        _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous caches")
+        _need(out.shape == (B, R, HQ, D) and out.is_contiguous(), "out must be [B, R, HQ, D]")
+        _i32_dev(pos, "pos")
+        _device_guard(q)
+        wp, wn = _ws_args(self.ws)
+        check(lib().sk_decode_attention_bf16(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(),
+                                             out.data_ptr(), B, HQ, HKV, D, R, cap, self.maxlen, float(self.scale),
+                                             self.nsplit, wp, wn, _stream(q)), "sk_decode_attention_bf16")
 
 
 # ---------------------------------------------------------------------------

@@ -308,3 +308,131 @@ def test_gateup_parity_rule_accepts_reference_pipeline_and_rejects_wrong_epilogu
     wrong = (F.silu(F.linear(x, w[:9728]).float()) * F.linear(x, w[9728:]).float()).to(BF16)
     _, _, exact = gateup_violations(wrong, xb, wg, wu)
     assert exact < 0.9
+
+
+# --------------------------------------------------------------------------
+# q/k RMSNorm + RoPE + KV-cache write (engine/kernels/rope.py)
+# --------------------------------------------------------------------------
+
+def rope_tables_cpu(D: int, theta: float, max_pos: int):
+    """cos/sin bf16 tables built the way the reference builds them
+    (engine/model.py:85-100): fp32 inv_freq, fp32 outer product, cat, cos/sin, bf16."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.int64).float() / D))
+    positions = torch.arange(max_pos, dtype=torch.float32)
+    freqs = (inv_freq[:, None].float() @ positions[None, :].float()).transpose(0, 1)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(BF16).contiguous(), emb.sin().to(BF16).contiguous()
+
+
+def _torch_rope_reference(qkv, qw, kw, cos, sin, start, B, T, HQ, HKV, D, eps):
+    """The reference test's composition (tests/test_kernels.py:11-19, 45-53) on the CPU."""
+    def ref_rmsnorm(x, w):
+        h = x.float()
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+        return w * h.to(x.dtype)
+
+    def rotate_half(x):
+        x1, x2 = x[..., : x.shape[-1] // 2], x[..., x.shape[-1] // 2:]
+        return torch.cat((-x2, x1), dim=-1)
+
+    q = qkv[:, : HQ * D].view(B, T, HQ, D)
+    k = qkv[:, HQ * D:(HQ + HKV) * D].view(B, T, HKV, D)
+    v = qkv[:, (HQ + HKV) * D:].view(B, T, HKV, D)
+    c = cos[start:start + T][None, :, None, :]
+    s = sin[start:start + T][None, :, None, :]
+    qn, kn = ref_rmsnorm(q, qw), ref_rmsnorm(k, kw)
+    q_ref = ((qn * c) + (rotate_half(qn) * s)).transpose(1, 2)
+    k_ref = ((kn * c) + (rotate_half(kn) * s)).transpose(1, 2)
+    return q_ref, k_ref, v.transpose(1, 2)
+
+
+@pytest.mark.parametrize("B,T,HQ,HKV,start", [(2, 5, 8, 2, 3), (3, 1, 32, 8, 700), (1, 16, 4, 4, 0)])
+def test_oracle_rope_matches_reference_composition(B, T, HQ, HKV, start):
+    D, CAP, eps = 128, start + T + 4, 1e-6
+    g = torch.Generator().manual_seed(B * 100 + T)
+    cos, sin = rope_tables_cpu(D, 5e6, CAP)
+    qkv = randn_bf16((B * T, (HQ + 2 * HKV) * D), 1.0, g)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    q_out = np.zeros((B, HQ, T, D), np.uint16)
+    kc = np.zeros((B, HKV, CAP, D), np.uint16)
+    vc = np.zeros((B, HKV, CAP, D), np.uint16)
+    pos = np.full(B, start, np.int32)
+    oracle.qk_norm_rope_cache(bits(qkv), bits(qw), bits(kw), bits(cos), bits(sin), pos, q_out, kc, vc, T, eps)
+    q_ref, k_ref, v_ref = _torch_rope_reference(qkv, qw, kw, cos, sin, start, B, T, HQ, HKV, D, eps)
+    # torch's CPU rsqrt and the oracle's 1/sqrt may differ in the last fp32
+    # bit, which moves a normalised value by one bf16 ulp on rare elements
+    qd = np.abs(q_out.astype(np.int32) - bits(q_ref).astype(np.int32))
+    kd = np.abs(kc[:, :, start:start + T].astype(np.int32) - bits(k_ref).astype(np.int32))
+    assert qd.max() <= 2 and (qd != 0).mean() < 2e-3, (qd.max(), (qd != 0).mean())
+    assert kd.max() <= 2 and (kd != 0).mean() < 2e-3
+    assert np.array_equal(vc[:, :, start:start + T], bits(v_ref))
+    untouched = np.ones(CAP, bool)
+    untouched[start:start + T] = False
+    assert not kc[:, :, untouched].any() and not vc[:, :, untouched].any()
+
+
+def test_oracle_rope_position_zero_is_norm_only():
+    """At position 0, cos = 1 and sin = 0: the rotation is the identity, so the
+    output is the per-head RMSNorm of the row, y = bf16(w * bf16(x * r))."""
+    D, eps = 128, 1e-6
+    g = torch.Generator().manual_seed(3)
+    cos, sin = rope_tables_cpu(D, 1e6, 4)
+    assert torch.all(cos[0] == 1) and torch.all(sin[0] == 0)
+    qkv = randn_bf16((1, 3 * D), 2.0, g)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    q_out = np.zeros((1, 1, 1, D), np.uint16)
+    kc = np.zeros((1, 1, 2, D), np.uint16)
+    vc = np.zeros_like(kc)
+    oracle.qk_norm_rope_cache(bits(qkv), bits(qw), bits(qw), bits(cos), bits(sin), np.zeros(1, np.int32), q_out, kc,
+                              vc, 1, eps)
+    x = qkv[0, :D].double()
+    r = 1.0 / torch.sqrt((x * x).mean() + eps)
+    y = (qw.float() * (x * r).float().to(BF16).float()).to(BF16)
+    assert np.array_equal(q_out[0, 0, 0], bits(y))
+
+
+# --------------------------------------------------------------------------
+# decode attention (engine/kernels/attention.py:221-242)
+# --------------------------------------------------------------------------
+
+def _attn_inputs(B, HQ, HKV, R, CAP, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = randn_bf16((B, HQ, R, 128), 1.0, g)
+    kc = randn_bf16((B, HKV, CAP, 128), 1.0, g)
+    vc = randn_bf16((B, HKV, CAP, 128), 1.0, g)
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("R", [1, 2])
+def test_oracle_attention_matches_sdpa(R):
+    B, HQ, HKV, CAP = 3, 8, 2, 200
+    q, kc, vc = _attn_inputs(B, HQ, HKV, R, CAP, seed=R)
+    pos = np.array([200 - R, 0, 76], np.int32)
+    scale = 128 ** -0.5
+    out = oracle.decode_attention(bits(q), bits(kc), bits(vc), pos, scale)
+    for b in range(B):
+        L = int(pos[b]) + R
+        k = kc[b, :, :L].double().repeat_interleave(HQ // HKV, dim=0)
+        v = vc[b, :, :L].double().repeat_interleave(HQ // HKV, dim=0)
+        mask = torch.arange(L)[None, :] <= (int(pos[b]) + torch.arange(R))[:, None]
+        ref = F.scaled_dot_product_attention(q[b].double(), k, v, attn_mask=mask[None], scale=scale)
+        got = torch.from_numpy(out[b]).transpose(0, 1).double()     # [HQ, R, D]
+        assert (got - ref).abs().max().item() < 1e-5
+
+
+def test_oracle_attention_special_cases():
+    """One visible key: the output is that key's value row.  Zero query: every
+    visible key has the same score, so the output is the mean of their values."""
+    B, HQ, HKV, CAP = 2, 4, 1, 50
+    q, kc, vc = _attn_inputs(B, HQ, HKV, 1, CAP, seed=9)
+    out = oracle.decode_attention(bits(q), bits(kc), bits(vc), np.array([0, 0], np.int32), 0.1)
+    for b in range(B):
+        for h in range(HQ):
+            assert np.array_equal(out[b, 0, h], vc[b, 0, 0].float().numpy())
+    zq = torch.zeros_like(q)
+    pos = np.array([9, 30], np.int32)
+    out = oracle.decode_attention(bits(zq), bits(kc), bits(vc), pos, 0.1)
+    for b in range(B):
+        mean = vc[b, 0, : int(pos[b]) + 1].double().mean(0).numpy()
+        assert np.abs(out[b, 0, 0] - mean).max() < 1e-6
