@@ -21,7 +21,14 @@ rotating weights, also timed with events on the launch stream; they include
 the inter-kernel gap, so they slightly understate kernel-only bandwidth
 (rocprofv3 --kernel-trace --stats gives kernel-only durations; see profiles/).
 
+The ``decode`` object of the JSON line is BASELINE configuration 5: a
+synthetic Qwen3-4B (36 layers, random bf16 weights) decoding greedily at
+batch 16 after a 1024-token prompt, one HIP graph per decode step, reported as
+decode tok/s = 16 * steps / decode time (and end-to-end tok/s including the
+prefill).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+                       [--decode-steps S] [--decode-only]
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 
@@ -335,6 +342,32 @@ def traffic_summary(fetch_dir: str, write_dir: str, M: int) -> int:
     return 0
 
 
+def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int = 128) -> dict:
+    """synthetic Qwen3-4B (36 layers, random bf16
+    weights ~N(0, 0.02)), B prompts of T uniform-random token ids, prefill, then
+    ``steps`` greedy decode steps replayed from one captured HIP graph.
+    decode tok/s = B * steps / decode time (HIP events on the replay stream);
+    end-to-end tok/s = B * (steps + 1) / (prefill + decode)."""
+    import torch
+
+    from starter_amd.decode import DecodePlan, Qwen3Config, SyntheticModel, time_decode
+
+    log(f"decode: building the synthetic Qwen3-4B (B={B}, prompt {T}, {steps} steps)")
+    model = SyntheticModel(Qwen3Config(), "cuda:0", seed=7)
+    plan = DecodePlan(model, B, T, max_new)
+    g = torch.Generator(device="cuda:0").manual_seed(11)
+    plan.ids.copy_(torch.randint(0, model.cfg.vocab, (B, T), device="cuda:0", generator=g))
+    r = time_decode(plan, steps)
+    log(f"decode: {r['tok_s']:.0f} tok/s ({r['ms_per_step']:.3f} ms/step), prefill {r['prefill_s']:.3f} s, "
+        f"end-to-end {r['e2e_tok_s']:.0f} tok/s")
+    out = {"tok_s": round(r["tok_s"], 1), "ms_per_step": round(r["ms_per_step"], 4), "steps": steps, "B": B,
+           "prompt": T, "prefill_s": round(r["prefill_s"], 4), "e2e_tok_s": round(r["e2e_tok_s"], 1),
+           "workload": "synthetic qwen3-4b greedy decode, 36 layers, GQA 32/8, cap %d, HIP graph per step" % plan.cap}
+    del plan, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -345,6 +378,10 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time all five shapes at M in 1..64 (BASELINE config 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-samples", type=int, default=20)
+    ap.add_argument("--decode-steps", type=int, default=127,
+                    help="C5: greedy decode steps timed after a B=16, T=1024 prefill (0 skips it)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="run only the C5 decode measurement and print its JSON object")
     ap.add_argument("--probe", action="store_true",
                     help="launch gate_up at --M (untimed) and a 512 MiB copy, for rocprofv3 --pmc passes")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -375,6 +412,9 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.probe:
         return probe(args.M)
+    if args.decode_only:
+        print(json.dumps({"decode": decode_benchmark(max(1, args.decode_steps))}), flush=True)
+        return 0
     log(f"device {torch.cuda.get_device_name(0)}; building workload (36 layers of weights)")
     wl = Workload(args.layers, args.M)
 
@@ -440,6 +480,12 @@ def main() -> int:
                 "kernel": f"gate_up+swiglu M={args.M} ({alg_bytes('gate_up', args.M)} algorithmic bytes/launch, "
                           f"{dom['us']} us/launch)"}
 
+    decode = None
+    if args.decode_steps > 0:
+        del wl
+        torch.cuda.empty_cache()
+        decode = decode_benchmark(args.decode_steps)
+
     cpu = port = None
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -466,6 +512,7 @@ def main() -> int:
                    "step_tflops": round(step_flops / (ms_per_step * 1e-3) / 1e12, 3),
                    "frac_peak_hbm": round(value / PEAK_HBM_GBS, 4)},
         "roofline": roofline,
+        "decode": decode,
         "cpu_baseline": cpu,
         "cpu_port": port,
         "per_gemm": per_gemm,

@@ -174,11 +174,12 @@ int sk_add_rmsnorm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w, fl
  * then the projection of A exactly as sk_gemm_bf16 / sk_gateup_swiglu_bf16 /
  * sk_lm_argmax_bf16.  x, y and xout are [M, K] with row stride ldx; w_norm is
  * [K].  xout must not overlap x or y, and the outputs must not overlap x, y
- * or xout.  With a one-split configuration of the LDS-fed MFMA or GEMV path
- * the prologue runs inside the projection kernel (each workgroup normalises
- * the activation columns it loads; workgroup 0 writes xout); otherwise a
- * separate add+norm kernel writes A into the workspace first.  Query the
- * workspace with SK_OP_RMSNORM_* ops.
+ * or xout.  With a one-split GEMV configuration (the M <= 4 default) the
+ * prologue runs inside the projection kernel (each workgroup normalises the
+ * activation columns it loads; workgroup 0 writes xout); otherwise a separate
+ * add+norm kernel writes A into the workspace first (on the MFMA paths every
+ * workgroup would redo the whole block's normalisation, which measured slower
+ * than the extra launch).  Query the workspace with SK_OP_RMSNORM_* ops.
  */
 int sk_rmsnorm_gemm_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps, sk_bf16* xout,
                          int64_t ldx, const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N, int K,

@@ -281,9 +281,12 @@ void oracle_qk_norm_rope_cache_bf16(const uint16_t* qkv, int64_t ld, const uint1
  * keys): query row t of sequence b (head h, KV head h / (HQ/HKV)) attends to
  * keys 0 .. pos[b] + t with scores scale * q.k; softmax and the weighted sum
  * of V are formed in fp64 from the bf16 inputs (exact attention, no bf16
- * probabilities); out [B, R, HQ, D] fp32.  OpenMP over (b, h). */
+ * probabilities); out [B, R, HQ, D] fp32.  wabs (optional, same shape) gets
+ * sum_n p_n |v_n| / sum_n p_n, the scale of the error that rounding the
+ * probabilities to bf16 can cause.  OpenMP over (b, h). */
 void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* pos,
-                             float* out, int B, int HQ, int HKV, int D, int R, int cap, float scale, int threads) {
+                             float* out, float* wabs, int B, int HQ, int HKV, int D, int R, int cap, float scale,
+                             int threads) {
   const int G = HQ / HKV;
 #pragma omp parallel for collapse(2) schedule(dynamic) num_threads(threads > 0 ? threads : 1)
   for (int b = 0; b < B; ++b)
@@ -292,7 +295,7 @@ void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const u
       const uint16_t* K = k_cache + (int64_t)(b * HKV + kh) * cap * D;
       const uint16_t* V = v_cache + (int64_t)(b * HKV + kh) * cap * D;
       double* sc = (double*)malloc(sizeof(double) * (size_t)cap);
-      double* acc = (double*)malloc(sizeof(double) * (size_t)D);
+      double* acc = (double*)malloc(sizeof(double) * (size_t)D * 2);   /* [sum p v | sum p |v|] */
       for (int t = 0; t < R; ++t) {
         const uint16_t* qr = q + ((int64_t)(b * HQ + h) * R + t) * D;
         int L = pos[b] + t + 1;
@@ -305,14 +308,21 @@ void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const u
           if (sc[n] > mx) mx = sc[n];
         }
         double den = 0.0;
-        for (int i = 0; i < D; ++i) acc[i] = 0.0;
+        for (int i = 0; i < 2 * D; ++i) acc[i] = 0.0;
         for (int n = 0; n < L; ++n) {
           const double p = exp(sc[n] - mx);
           den += p;
-          for (int i = 0; i < D; ++i) acc[i] += p * (double)bf2f(V[(int64_t)n * D + i]);
+          for (int i = 0; i < D; ++i) {
+            const double v = (double)bf2f(V[(int64_t)n * D + i]);
+            acc[i] += p * v;
+            acc[D + i] += p * fabs(v);
+          }
         }
-        float* o = out + ((int64_t)(b * R + t) * HQ + h) * D;
-        for (int i = 0; i < D; ++i) o[i] = L > 0 ? (float)(acc[i] / den) : 0.0f;
+        const int64_t o0 = ((int64_t)(b * R + t) * HQ + h) * D;
+        for (int i = 0; i < D; ++i) {
+          out[o0 + i] = L > 0 ? (float)(acc[i] / den) : 0.0f;
+          if (wabs) wabs[o0 + i] = L > 0 ? (float)(acc[D + i] / den) : 0.0f;
+        }
       }
       free(sc);
       free(acc);

@@ -35,7 +35,7 @@ COMMON = [
 ]
 
 N_EPI = 5       # EPI_STORE, EPI_SWIGLU, EPI_ARGMAX, EPI_PART, EPI_PART_GU
-NORM_EPIS = (5, 6, 7)   # the first three with the norm prologue (LDS-fed MFMA and GEMV only)
+NORM_EPIS = (5, 6, 7)   # the first three with the norm prologue (GEMV path only)
 
 
 def _units() -> list[tuple[Path, list[str], Path]]:
@@ -46,7 +46,6 @@ def _units() -> list[tuple[Path, list[str], Path]]:
         units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
     for epi in NORM_EPIS:
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
-        units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
     return units
 
 

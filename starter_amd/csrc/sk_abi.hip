@@ -164,7 +164,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0) return SK_ERR_CONFIG;
   if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
   const bool gateup = (op == SK_OP_GATEUP);
-  if (fused && (c.split != 1 || (c.path != SK_PATH_GEMV && c.path != SK_PATH_MFMA_LDS))) return SK_ERR_CONFIG;
+  if (fused && (c.split != 1 || c.path != SK_PATH_GEMV)) return SK_ERR_CONFIG;
   pl->cfg = c;
   pl->epi = epi_for(op, c.split) + (fused ? sk::EPI_STORE_NORM : 0);
   pl->fused = fused;
@@ -188,10 +188,8 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tn = gateup ? 2 : c.rows / 16;
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
-    if (c.waves > sk::max_waves_for_regs(sk::mfmt_regs(pl->tm, pl->tn, KW, fused), fused)) return SK_ERR_CONFIG;
+    if (c.waves > sk::max_waves_for_regs(sk::mfmt_regs(pl->tm, pl->tn, KW))) return SK_ERR_CONFIG;
     pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
-    // Norm instances keep the norm weights (K bf16, 16-byte padded) in front.
-    if (fused) pl->pre_lds += ((size_t)2 * K + 15) & ~(size_t)15;
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
     if (M > 8) return SK_ERR_CONFIG;
@@ -228,14 +226,16 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
 }
 
 // Plan of any GEMM-family op.  A norm op runs its prologue inside the
-// projection kernel when the configuration allows (one K split, LDS-fed MFMA
-// or GEMV path, a compiled norm instance within the wave limit), else as a
-// separate add+norm launch in front of the plain projection.
+// projection kernel on the GEMV path with one K split (a compiled norm
+// instance within the wave limit), else as a separate add+norm launch in
+// front of the plain projection.  The MFMA paths take the separate launch:
+// there every workgroup would normalise the whole activation block again,
+// and on an MI355X that VALU work cost more than the extra launch (qkv at
+// M = 16: 16.5 us fused in the LDS-fed MFMA kernel, 12.6 us as two launches).
 int plan_shape(int op, int M, int N, int K, const sk_config& c, Plan* pl) {
   const bool norm = is_norm_op(op);
   const int bop = base_op(op);
-  if (norm && c.split == 1 && (c.path == SK_PATH_GEMV || c.path == SK_PATH_MFMA_LDS) &&
-      plan_shape_impl(bop, M, N, K, c, true, pl) == SK_OK) {
+  if (norm && c.split == 1 && c.path == SK_PATH_GEMV && plan_shape_impl(bop, M, N, K, c, true, pl) == SK_OK) {
     pl->norm = true;
     return SK_OK;
   }

@@ -1,4 +1,4 @@
-// LDS-transposed MFMA kernel instances for one epilogue (-DSK_EPI=<0..7>).
+// LDS-transposed MFMA kernel instances for one epilogue (-DSK_EPI=<0..4>).
 #include "sk_registry.hpp"
 
 #ifndef SK_EPI
@@ -11,7 +11,7 @@
 namespace sk {
 
 template <int MT, int NT, int KW, int EPI>
-__global__ void __launch_bounds__(64 * max_waves_for_regs(mfmt_regs(MT, NT, KW, EpiTraits<EPI>::norm), EpiTraits<EPI>::norm))
+__global__ void __launch_bounds__(64 * max_waves_for_regs(mfmt_regs(MT, NT, KW)))
 mfmt_entry(Args p) {
   mfmt_body<MT, NT, KW, EPI>(p);
 }
@@ -23,7 +23,7 @@ mfmt_entry(Args p) {
 
 KernelFn SK_CAT(mfmt_for_epi, SK_EPI)(int MT, int NT, int KW) {
   switch (MT * 100000 + NT * 1000 + KW) {
-#if SK_EPI == 1 || SK_EPI == 4 || SK_EPI == 6   // gate/up: 16 gate rows + 16 up rows
+#if SK_EPI == 1 || SK_EPI == 4   // gate/up: 16 gate rows + 16 up rows
     SK_LIST(2)
 #else
     SK_LIST(1)

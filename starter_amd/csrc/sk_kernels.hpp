@@ -451,21 +451,6 @@ __device__ __forceinline__ void mfma_body(Args p) {
     kcol[u] = uu * 32 + 8 * g4;
   }
 
-  // Activation fragments: lane holds A[16*mt + r16][kcol[u] .. +8], zero for
-  // rows >= M and padding units.
-  bf16x8 af[MT][KU];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = 16 * mt + r16;
-    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda;
-#pragma unroll
-    for (int u = 0; u < KU; ++u) {
-      u32x4 v = ld16(ap + kcol[u]);
-      if (m >= M || u >= nu) v = u32x4{0u, 0u, 0u, 0u};
-      af[mt][u] = __builtin_bit_cast(bf16x8, v);
-    }
-  }
-
   // Weight row base of tile rb (rows past N clamp to N-1: in bounds, unused).
   auto wrow = [&](int rb, int nt) -> const uint16_t* {
     if constexpr (GATEUP) {
@@ -477,6 +462,7 @@ __device__ __forceinline__ void mfma_body(Args p) {
     }
   };
 
+  // First tile's weights, issued before the activations so both latencies overlap.
   u32x4 wf[NT][KU];
   if (ntiles > 0) {
 #pragma unroll
@@ -486,6 +472,28 @@ __device__ __forceinline__ void mfma_body(Args p) {
       for (int u = 0; u < KU; ++u) wf[nt][u] = ld16_stream(wp + kcol[u]);
     }
   }
+
+  // Activation fragments: lane holds A[16*mt + r16][kcol[u] .. +8].  Rows
+  // m >= M repeat row M-1: MFMA output column m depends only on activation
+  // row m, and those columns are never read, so they need no zeroing (and the
+  // loads need no wait before the weight stream).  Padding units (u >= nu,
+  // wave-uniform) are zeroed, on the one path that has them.
+  bf16x8 af[MT][KU];
+  auto load_acts = [&](auto padded) {
+    constexpr bool PAD = decltype(padded)::value;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint16_t* ap = p.A + (int64_t)min(16 * mt + r16, M - 1) * p.lda;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        u32x4 v = ld16(ap + kcol[u]);
+        if (PAD && u >= nu) v = u32x4{0u, 0u, 0u, 0u};
+        af[mt][u] = __builtin_bit_cast(bf16x8, v);
+      }
+    }
+  };
+  if (nu == KU) load_acts(std::false_type{});
+  else load_acts(std::true_type{});
 
   auto tile = [&](int j, auto prefetch) {
     constexpr bool PF = decltype(prefetch)::value;
@@ -554,7 +562,7 @@ template <int MT, int NT, int KW, int EPI>
 __device__ __forceinline__ void mfmt_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int BASE = EpiTraits<EPI>::base;   // epilogue without the norm prologue
-  constexpr bool NORM = EpiTraits<EPI>::norm;
+  static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
   constexpr int ROWS = 16 * NT;                  // weight rows per tile
   constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
   constexpr int UNITS = KW / 32;                 // MFMA K steps per wave
@@ -586,52 +594,17 @@ __device__ __forceinline__ void mfmt_body(Args p) {
   const bool has_chunk = chunk < c_hi;                  // wave-uniform
   const int k0 = min(chunk, chunks - 1) * KW;
 
-  // LDS: [norm weights, K bf16 (norm instances)][wave-private staging of 16
-  // rows x 256 columns per wave: the NT row tiles (and the two halves of a
-  // 512-column chunk) pass through it in turn][partials][staged outputs].
-  const int nwl_bytes = NORM ? ((2 * p.K + 15) & ~15) : 0;
-  const uint16_t* nwl = reinterpret_cast<const uint16_t*>(lds);
-  char* tr = reinterpret_cast<char*>(lds) + nwl_bytes + wave * (16 * PITCH);
-  float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nwl_bytes + nw * (16 * PITCH));
+  // LDS: [wave-private staging of 16 rows x 256 columns per wave: the NT row
+  // tiles (and the two halves of a 512-column chunk) pass through it in
+  // turn][partials][staged outputs].
+  char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
+  float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
   const int part_floats = nw * M * ROWS;
   void* stage = parts + 2 * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
   if constexpr (BASE == EPI_ARGMAX) {
     if (tid < M) lds_best[tid] = 0ull;
   }
-
-  // Activation fragments of this chunk: lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8];
-  // zero for rows >= M, columns >= K and waves without a chunk.  When the
-  // chunk lies inside K (wave-uniform) the loads share one base address with
-  // immediate offsets; otherwise each column is clamped in bounds.  Norm
-  // instances also load the residual rows y at the same positions.
-  const bool full_chunk = has_chunk && k0 + KW <= p.K;
-  bf16x8 af[MT][UNITS];
-  u32x4 yf[NORM ? MT : 1][NORM ? UNITS : 1];
-  auto load_acts = [&](auto full) {
-    constexpr bool FULL = decltype(full)::value;
-    auto col = [&](int u) { return FULL ? k0 + 8 * g4 + 32 * u : min(k0 + 32 * u + 8 * g4, p.K - 8); };
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = 16 * mt + r16;
-      const int64_t roff = (int64_t)min(m, M - 1) * p.lda;
-#pragma unroll
-      for (int u = 0; u < UNITS; ++u) {
-        const int k = k0 + 32 * u + 8 * g4;
-        const bool ok = m < M && (FULL || (k < p.K && has_chunk));
-        u32x4 v = ld16(p.A + roff + col(u));
-        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
-        af[mt][u] = __builtin_bit_cast(bf16x8, v);
-        if constexpr (NORM) {
-          u32x4 yv = ld16(p.Y + roff + col(u));
-          if (!ok) yv = u32x4{0u, 0u, 0u, 0u};
-          yf[mt][u] = yv;
-        }
-      }
-    }
-  };
-  if (full_chunk) load_acts(std::true_type{});
-  else load_acts(std::false_type{});
 
   // Load instruction i covers tile rows i*RPI + lane/LPR, columns k0 + 8*(lane%LPR).
   const int lrow = lane / LPR;
@@ -655,69 +628,42 @@ __device__ __forceinline__ void mfmt_body(Args p) {
   char* const wdst = tr + (lane >> 5) * PITCH + 16 * (lane & 31);
   constexpr int NLD16 = 16 / RPI;                 // load instructions per 16-row tile
 
-  // First tile's weight rows.  Norm instances issue them before the prologue
-  // only when the residual fragments and the rows fit the registers together
-  // (then the weight stream's first latency overlaps the prologue's loads).
-  constexpr bool EARLY_W = !NORM || 4 * UNITS * MT * 2 + 4 * NLD <= 160;
+  // First tile's weight rows, issued before the activations so that both
+  // latencies overlap.
   u32x4 wf[NLD];
-  auto load_first_tile = [&]() {
-    if (ntiles > 0) {
+  if (ntiles > 0) {
 #pragma unroll
-      for (int i = 0; i < NLD; ++i) wf[i] = ld16_stream(wsrc(rb0, i));
-    }
-  };
-  if constexpr (EARLY_W) load_first_tile();
+    for (int i = 0; i < NLD; ++i) wf[i] = ld16_stream(wsrc(rb0, i));
+  }
 
-  if constexpr (NORM) {
-    // The norm weights go to LDS, once per workgroup (16 bytes per thread and step).
-    for (int c = tid; c < (p.K >> 3); c += 64 * nw)
-      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(nwl) + 8 * c) = ld16(p.NW + 8 * c);
-    // s = bf16(x + y) replaces x in the fragments; each row's sum of squares
-    // is reduced over the four lanes holding that row (lanes l, l^16, l^32,
-    // l^48), then over the waves in LDS in wave order.  The workgroup covers
-    // all of K (one global split), so every row sum is complete.
-    float sq[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      sq[mt] = 0.f;
-#pragma unroll
-      for (int u = 0; u < UNITS; ++u)
-        af[mt][u] = __builtin_bit_cast(bf16x8, add_bf16x8(__builtin_bit_cast(u32x4, af[mt][u]), yf[mt][u], sq[mt]));
-      sq[mt] += __shfl_xor(sq[mt], 16);
-      sq[mt] += __shfl_xor(sq[mt], 32);
-    }
-    // The second partial buffer is first written by tile 1, after tile 0's barrier.
-    float* red = parts + part_floats;
-    if (g4 == 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        if (16 * mt + r16 < M) red[wave * M + 16 * mt + r16] = sq[mt];
-    }
-    lds_barrier();
+  // Activation fragments of this chunk: lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8].
+  // Rows m >= M repeat row M-1 (they only feed MFMA output columns that are
+  // never read, so they need no zeroing and no wait); columns >= K and waves
+  // without a chunk are zeroed.  When the chunk lies inside K (wave-uniform)
+  // the loads share one base address with immediate offsets and need no
+  // masking; otherwise each column is clamped in bounds.
+  const bool full_chunk = has_chunk && k0 + KW <= p.K;
+  bf16x8 af[MT][UNITS];
+  auto load_acts = [&](auto full) {
+    constexpr bool FULL = decltype(full)::value;
+    auto col = [&](int u) { return FULL ? k0 + 8 * g4 + 32 * u : min(k0 + 32 * u + 8 * g4, p.K - 8); };
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = 16 * mt + r16;
-      float t = 0.f;
-      for (int w = 0; w < nw; ++w) t += red[w * M + min(m, M - 1)];
-      const float rstd = rms_rstd(t, p.K, p.eps);
+      const int64_t roff = (int64_t)min(m, M - 1) * p.lda;
 #pragma unroll
       for (int u = 0; u < UNITS; ++u) {
         const int k = k0 + 32 * u + 8 * g4;
-        const bool ok = m < M && k < p.K && has_chunk;
-        const u32x4 sv = __builtin_bit_cast(u32x4, af[mt][u]);
-        if (blockIdx.x == 0 && ok) *reinterpret_cast<u32x4*>(p.XO + (int64_t)m * p.lda + k) = sv;
-        const u32x4 wn = *reinterpret_cast<const u32x4*>(nwl + min(k, p.K - 8));
-        u32x4 a = norm_bf16x8(sv, wn, rstd);
-        if (!ok) a = u32x4{0u, 0u, 0u, 0u};
-        af[mt][u] = __builtin_bit_cast(bf16x8, a);
+        const bool ok = FULL || (k < p.K && has_chunk);
+        u32x4 v = ld16(p.A + roff + col(u));
+        if (!ok) v = u32x4{0u, 0u, 0u, 0u};
+        af[mt][u] = __builtin_bit_cast(bf16x8, v);
       }
     }
-  }
-  if constexpr (!EARLY_W) {
-    // Not hoisted above the prologue by the scheduler.
-    __builtin_amdgcn_sched_barrier(0);
-    load_first_tile();
-  }
+  };
+  if (full_chunk) load_acts(std::true_type{});
+  else load_acts(std::false_type{});
+
 
   auto tile = [&](int j, auto prefetch) {
     constexpr bool PF = decltype(prefetch)::value;
@@ -844,35 +790,6 @@ __device__ __forceinline__ void gemv_body(Args p) {
     kcol[u] = min(max(k, 0), p.K - 8);
   }
 
-  u32x4 af[MR][KU];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    const uint16_t* ap = p.A + (int64_t)min(m, M - 1) * p.lda;
-#pragma unroll
-    for (int u = 0; u < KU; ++u) {
-      u32x4 v = ld16(ap + kcol[u]);
-      if (m >= M || !kok[u]) v = u32x4{0u, 0u, 0u, 0u};
-      af[m][u] = v;
-    }
-  }
-  // Norm prologue, loads.
-  u32x4 yf[NORM ? MR : 1][NORM ? KU : 1];
-  u32x4 nf[NORM ? KU : 1];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const uint16_t* yp = p.Y + (int64_t)min(m, M - 1) * p.lda;
-#pragma unroll
-      for (int u = 0; u < KU; ++u) {
-        u32x4 v = ld16(yp + kcol[u]);
-        if (m >= M || !kok[u]) v = u32x4{0u, 0u, 0u, 0u};
-        yf[m][u] = v;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < KU; ++u) nf[u] = ld16(p.NW + kcol[u]);
-  }
-
   auto wrow = [&](int rb, int rr) -> const uint16_t* {
     if constexpr (GATEUP) {
       const int row = min(rb * R + (rr % R), p.N - 1);
@@ -882,6 +799,54 @@ __device__ __forceinline__ void gemv_body(Args p) {
       return p.W0 + (int64_t)row * p.ldw;
     }
   };
+
+  // First tile's weight rows, issued before the activations so both
+  // latencies overlap (norm instances: after the prologue, see below).
+  u32x4 wf[RR][KU];
+  auto load_first_tile = [&]() {
+    if (ntiles > 0) {
+#pragma unroll
+      for (int rr = 0; rr < RR; ++rr) {
+        const uint16_t* wp = wrow(rb0, rr);
+#pragma unroll
+        for (int u = 0; u < KU; ++u) wf[rr][u] = ld16_stream(wp + kcol[u]);
+      }
+    }
+  };
+  if constexpr (!NORM) load_first_tile();
+
+  // Activations (and, for norm instances, the residual rows and the norm
+  // weights).  Rows m >= M repeat row M-1: their dot products go to partial
+  // slots that are never stored.  Padding columns (kok false) are zeroed on
+  // the one path that has them (wave-uniform: all of the wave's units real).
+  const bool full = (nu == KU) && ((u_lo + KU) * 512 <= kend);
+  u32x4 af[MR][KU];
+  u32x4 yf[NORM ? MR : 1][NORM ? KU : 1];
+  u32x4 nf[NORM ? KU : 1];
+  auto load_acts = [&](auto fullc) {
+    constexpr bool FULL = decltype(fullc)::value;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const int64_t roff = (int64_t)min(m, M - 1) * p.lda;
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        u32x4 v = ld16(p.A + roff + kcol[u]);
+        if (!FULL && !kok[u]) v = u32x4{0u, 0u, 0u, 0u};
+        af[m][u] = v;
+        if constexpr (NORM) {
+          u32x4 yv = ld16(p.Y + roff + kcol[u]);
+          if (!FULL && !kok[u]) yv = u32x4{0u, 0u, 0u, 0u};
+          yf[m][u] = yv;
+        }
+      }
+    }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int u = 0; u < KU; ++u) nf[u] = ld16(p.NW + kcol[u]);
+    }
+  };
+  if (full) load_acts(std::true_type{});
+  else load_acts(std::false_type{});
 
   if constexpr (NORM) {
     // s = bf16(x + y) replaces x; row sums of squares over the wave (DPP),
@@ -917,16 +882,11 @@ __device__ __forceinline__ void gemv_body(Args p) {
     }
   }
 
-  // First tile's weight rows, after the norm prologue (not hoisted above it).
-  if constexpr (NORM) __builtin_amdgcn_sched_barrier(0);
-  u32x4 wf[RR][KU];
-  if (ntiles > 0) {
-#pragma unroll
-    for (int rr = 0; rr < RR; ++rr) {
-      const uint16_t* wp = wrow(rb0, rr);
-#pragma unroll
-      for (int u = 0; u < KU; ++u) wf[rr][u] = ld16_stream(wp + kcol[u]);
-    }
+  if constexpr (NORM) {
+    // Norm instances: the first tile's weight rows after the prologue (not
+    // hoisted above it, where they would sit next to its registers).
+    __builtin_amdgcn_sched_barrier(0);
+    load_first_tile();
   }
 
   auto tile = [&](int j, auto prefetch) {

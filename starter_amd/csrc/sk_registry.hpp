@@ -3,8 +3,7 @@
 // The kernel templates are instantiated for a fixed set of (row tiles, K-unit
 // bound) pairs per epilogue, one translation unit per epilogue
 // (sk_inst_mfma.hip / sk_inst_mfmt.hip / sk_inst_gemv.hip built with
-// -DSK_EPI=<n>; the norm-prologue epilogues 5..7 exist for the LDS-fed MFMA
-// and GEMV paths only).
+// -DSK_EPI=<n>; the norm-prologue epilogues 5..7 exist for the GEMV path only).
 // The host planner asks for the smallest instantiated K-unit bound that covers
 // a wave's K range; a nullptr answer means "no such instance" and the config
 // is rejected with SK_ERR_CONFIG.
@@ -33,14 +32,12 @@ constexpr int gemv_regs(int MR, int RR, int KU, bool norm = false) {
 }
 // LDS-transposed MFMA: KW/32 activation units per tile row block plus the
 // staged weight rows (KW/512 rows per load instruction).
-constexpr int mfmt_regs(int MT, int NT, int KW, bool norm = false) {
-  return 4 * (KW / 32) * MT + 4 * (16 * NT * KW / 512) + 4 * NT * MT + 32 +
-         (norm ? norm_extra(4 * (KW / 32) * MT, 4 * (16 * NT * KW / 512), 4 * (KW / 32)) : 0);
+constexpr int mfmt_regs(int MT, int NT, int KW) {
+  return 4 * (KW / 32) * MT + 4 * (16 * NT * KW / 512) + 4 * NT * MT + 32;
 }
 // Waves per workgroup an instance is compiled for (its __launch_bounds__):
-// 16 waves leave 128 VGPRs per lane, 8 waves 256.  The norm-prologue
-// instances also have a 12-wave tier (168 VGPRs), which the 10-wave
-// 256-column chunk configurations of K = 2560 need.
+// 16 waves leave 128 VGPRs per lane, 8 waves 256; norm-prologue instances
+// also have a 12-wave tier (168 VGPRs).
 constexpr int max_waves_for_regs(int regs, bool norm = false) {
   return regs <= 128 ? 16 : (norm && regs <= 168 ? 12 : (regs <= 256 ? 8 : 4));
 }
@@ -55,9 +52,6 @@ KernelFn mfmt_for_epi1(int MT, int NT, int KW);
 KernelFn mfmt_for_epi2(int MT, int NT, int KW);
 KernelFn mfmt_for_epi3(int MT, int NT, int KW);
 KernelFn mfmt_for_epi4(int MT, int NT, int KW);
-KernelFn mfmt_for_epi5(int MT, int NT, int KW);
-KernelFn mfmt_for_epi6(int MT, int NT, int KW);
-KernelFn mfmt_for_epi7(int MT, int NT, int KW);
 KernelFn gemv_for_epi0(int MR, int R, int KU);
 KernelFn gemv_for_epi1(int MR, int R, int KU);
 KernelFn gemv_for_epi2(int MR, int R, int KU);
@@ -85,9 +79,6 @@ inline KernelFn mfmt_kernel_for(int epi, int MT, int NT, int KW) {
     case EPI_ARGMAX: return mfmt_for_epi2(MT, NT, KW);
     case EPI_PART: return mfmt_for_epi3(MT, NT, KW);
     case EPI_PART_GU: return mfmt_for_epi4(MT, NT, KW);
-    case EPI_STORE_NORM: return mfmt_for_epi5(MT, NT, KW);
-    case EPI_SWIGLU_NORM: return mfmt_for_epi6(MT, NT, KW);
-    case EPI_ARGMAX_NORM: return mfmt_for_epi7(MT, NT, KW);
   }
   return nullptr;
 }

@@ -179,7 +179,7 @@ def test_valid_call_without_gpu_fails_loudly():
     if torch.cuda.is_available():
         pytest.skip("a GPU is present; the GPU tests exercise this path")
     assert _gemm(_lib.lib()) == SK_ERR_DEVICE
-    assert _rms_gemm(_lib.lib()) == SK_ERR_DEVICE
+    assert _rms_gemm(_lib.lib(), M=1) == SK_ERR_DEVICE   # fused GEMV default: no workspace
 
 
 # ---------------------------------------------------------------------------
@@ -199,8 +199,8 @@ def _rms_gemm(lib, x=X0, y=Y0, nw=NW0, xo=XO0, ldx=2560, W=W0, C=C0, M=8, N=6144
 @pytest.mark.parametrize("name", list(NORMED))
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 40, 64])
 def test_normed_default_config_valid_and_fused_at_decode_m(name, M):
-    """The norm ops use their projection's tuned configuration; at M <= 16
-    (one K split, LDS-fed MFMA or GEMV) the prologue runs inside the
+    """The norm ops use their projection's tuned configuration; on the GEMV
+    path with one K split (the M <= 4 defaults) the prologue runs inside the
     projection kernel, so the workspace is the projection's own.  Otherwise the
     workspace adds the normalised rows [M, K] bf16 after the projection's part."""
     op, N, K = NORMED[name]
@@ -211,13 +211,12 @@ def test_normed_default_config_valid_and_fused_at_decode_m(name, M):
     plain = _lib.workspace_bytes(BASE[op], M, N, K, cfg)
     normed = _lib.workspace_bytes(op, M, N, K, cfg)
     unfused = (plain + 255) // 256 * 256 + M * K * 2
-    if M <= 16:
-        assert cfg.split == 1 and cfg.path in (SK_PATH_GEMV, SK_PATH_MFMA_LDS), cfg
+    if cfg.path == SK_PATH_GEMV and cfg.split == 1:
         assert normed == plain            # fused: no buffer for the normalised rows
-    elif cfg.split > 1 or cfg.path == SK_PATH_MFMA:
-        assert normed == unfused          # the register-fragment path and global splits never fuse
     else:
-        assert normed in (plain, unfused)
+        assert normed == unfused          # MFMA paths and global splits never fuse
+    if M == 1 and name in ("qkv", "gu"):
+        assert cfg.path == SK_PATH_GEMV
 
 
 def test_normed_workspace_layout_for_unfused_configs():
@@ -225,6 +224,10 @@ def test_normed_workspace_layout_for_unfused_configs():
     base = _lib.workspace_bytes(SK_OP_GEMM, 8, 6144, 2560, split)
     assert base == _tickets(6144 // 16) + 2 * 8 * 6144 * 4
     assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, split) == (base + 255) // 256 * 256 + 8 * 2560 * 2
+    lds = SkConfig.make(SK_PATH_MFMA_LDS, 10, 8, 16)
+    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, lds) == 8 * 2560 * 2
+    gemv = SkConfig.make(SK_PATH_GEMV, 1, 5, 2)
+    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 4, 6144, 2560, gemv) == 0   # fused
     mfma = SkConfig.make(SK_PATH_MFMA, 8, 10, 16)
     assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, mfma) == 8 * 2560 * 2
     # rows beyond 64: the separate prologue normalises all rows at once

@@ -51,8 +51,8 @@ gn = pytest.importorskip("tests.test_gpu_norm")
 @pytest.mark.parametrize("name", list(gn.NORM_CONFIGS))
 @pytest.mark.parametrize("M", [1, 3, 8, 16])
 def test_norm_test_configs_valid(name, M):
-    """The norm-prologue test configs: fused ones keep the projection's
-    workspace, unfused ones (global split, register-fragment MFMA) add the
+    """The norm-prologue test configs: fused ones (GEMV, one split) keep the
+    projection's workspace, unfused ones (MFMA paths, global splits) add the
     normalised rows."""
     from starter_amd._lib import SK_OP_RMSNORM_GEMM, SK_PATH_GEMV, SK_PATH_MFMA
 
@@ -62,7 +62,7 @@ def test_norm_test_configs_valid(name, M):
     assert _lib.check_config(SK_OP_RMSNORM_GEMM, M, 6144, 2560, cfg) == SK_OK
     plain = _lib.workspace_bytes(SK_OP_GEMM, M, 6144, 2560, cfg)
     normed = _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, M, 6144, 2560, cfg)
-    if cfg.split > 1 or cfg.path == SK_PATH_MFMA:
+    if cfg.split > 1 or cfg.path != SK_PATH_GEMV:
         assert normed == (plain + 255) // 256 * 256 + M * 2560 * 2
     else:
         assert normed == plain, f"{name} should run the prologue fused"

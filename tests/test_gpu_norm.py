@@ -98,7 +98,7 @@ def test_rmsnorm_gemm_lm_logits(M):
     assert_parity(out, from_bits(oracle.gemm(o_h, bits(wc))), f"rmsnorm lm logits M={M}")
 
 
-NORM_CONFIGS = {   # fused (GEMV, LDS-fed MFMA) and unfused (global split, register-fragment MFMA)
+NORM_CONFIGS = {   # fused (GEMV, one split) and unfused (MFMA paths, global split)
     "gemv": SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=2),
     "gemv_4w": SkConfig.make(SK_PATH_GEMV, waves=4, ku=2, rows=2),
     "mfma_lds_256": SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16),
