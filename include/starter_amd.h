@@ -215,24 +215,37 @@ int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16
 /*
  * sk_decode_attention_bf16: split-K grouped-query flash-decoding with a
  * device-side length.  Replaces DecodeAttention (engine/kernels/attention.py:
- * 152-202, kernels 23-149) for chain masks (no draft tree):
+ * 152-202, kernels 23-149), chain and draft-tree masks:
  *   q      [B, HQ, R, D] bf16; k_cache, v_cache [B, HKV, cap, D] bf16
- *   pos    [B] int32 device array: query row t of sequence b sees keys 0 .. pos[b] + t
+ *   pos    [B] int32 device array: position of query row 0 of sequence b
+ *   tree   NULL: row t sees keys 0 .. pos[b] + t (chain);  else [R] int64
+ *          device array of ancestor bit masks: row t sees keys < pos[b] and
+ *          key pos[b] + j (j < R) iff bit j of tree[t] is set
  *   out    [B, R, HQ, D] bf16 (rows (b, t) of [B*R, HQ*D])
  *   max_len: the longest sequence the caller will attend over (bounds the
  *            splits; 0 = cap); nsplit: key splits per (b, kv head), 0 = default
- * (HQ/HKV) * R must be at most 8.  Scores and softmax statistics in fp32,
- * probabilities rounded to bf16 before the PV product, fp32 accumulation
- * (attention.py:9-11).  Needs a zero-filled workspace of
+ * (HQ/HKV) * R must be at most 64; query rows are processed 8 per workgroup
+ * (more rows stream the keys once per block of 8).  Scores and softmax
+ * statistics in fp32, probabilities rounded to bf16 before the PV product,
+ * fp32 accumulation (attention.py:9-11).  Needs a zero-filled workspace of
  * sk_decode_attention_workspace_bytes() bytes when it splits the keys; the
- * last workgroup of each (b, kv head) merges the splits in the same kernel and
- * leaves the workspace counters at zero.
+ * last workgroup of each (b, kv head, row block) merges the splits in the
+ * same kernel and leaves the workspace counters at zero.
  */
 size_t sk_decode_attention_workspace_bytes(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int nsplit);
 
 int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_bf16* v_cache, const int32_t* pos,
-                             sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
-                             int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
+                             const int64_t* tree, sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap,
+                             int max_len, float scale, int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Exact argmax plus approximate top-k over bf16 logits L[N, V] (row stride
+ * ld) in one pass.  Replaces fast_topk (engine/kernels/topk.py:17-46) with
+ * the same algorithm and results: 2048 lanes sweep each row with stride 2048,
+ * lane j keeping the first occurrence of the largest value at columns
+ * j, j+2048, ...; rank k is the largest remaining lane maximum (lowest column
+ * on ties) and removes its lane.  vals [N, K] fp32, idxs [N, K] int32; rank 0
+ * is the exact argmax.  1 <= K <= 64.  No workspace. */
+int sk_topk_bf16(const sk_bf16* L, int64_t ld, int N, int V, int K, float* vals, int32_t* idxs, hipStream_t stream);
 
 /* Out[M,I] = bf16(bf16(silu(g)) * u) for gu[M, 2I] = [g | u] (row stride ld_gu).
  * Replaces swiglu (engine/kernels/swiglu.py:14-33). */

@@ -60,8 +60,9 @@ def lib() -> ctypes.CDLL:
         _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
         h.oracle_qk_norm_rope_cache_bf16.argtypes = [_u16p, _i64, _u16p, _u16p, _u16p, _u16p, _i32p, _u16p, _u16p,
                                                      _u16p, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float]
-        h.oracle_decode_attention.argtypes = [_u16p, _u16p, _u16p, _i32p, _f32p, _f32p, _i32, _i32, _i32, _i32, _i32,
-                                              _i32, ctypes.c_float, _i32]
+        h.oracle_topk_bf16.argtypes = [_u16p, _i64, _i32, _i32, _i32, _f32p, _i32p]
+        h.oracle_decode_attention.argtypes = [_u16p, _u16p, _u16p, _i32p, ctypes.c_void_p, _f32p, _f32p, _i32, _i32,
+                                              _i32, _i32, _i32, _i32, ctypes.c_float, _i32]
         _lib = h
     return _lib
 
@@ -188,17 +189,30 @@ def qk_norm_rope_cache(qkv: np.ndarray, qw: np.ndarray, kw: np.ndarray, cos: np.
 
 
 def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, pos: np.ndarray,
-                     scale: float, with_abs: bool = False):
+                     scale: float, with_abs: bool = False, tree: np.ndarray | None = None):
     """Exact attention of each query row (engine/kernels/attention.py:221-242):
     q [B, HQ, R, D] bits, caches [B, HKV, cap, D] bits, pos [B] (row t sees keys
-    0 .. pos[b] + t).  Returns fp32 [B, R, HQ, D]; with ``with_abs`` also the
-    softmax-weighted mean of |v| per output element (error scale of bf16
-    probabilities)."""
+    0 .. pos[b] + t, or with ``tree`` [R] int64 the keys < pos[b] and draft key
+    pos[b] + j when bit j of tree[t] is set).  Returns fp32 [B, R, HQ, D]; with
+    ``with_abs`` also the softmax-weighted mean of |v| per output element
+    (error scale of bf16 probabilities)."""
     q, k_cache, v_cache = _u16(q), _u16(k_cache), _u16(v_cache)
     B, HQ, R, D = q.shape
     HKV, cap = k_cache.shape[1], k_cache.shape[2]
     out = np.empty((B, R, HQ, D), dtype=np.float32)
     wabs = np.empty_like(out)
     pos = np.ascontiguousarray(pos, dtype=np.int32)
-    lib().oracle_decode_attention(q, k_cache, v_cache, pos, out, wabs, B, HQ, HKV, D, R, cap, scale, threads())
+    tr = None if tree is None else np.ascontiguousarray(tree, dtype=np.int64)
+    lib().oracle_decode_attention(q, k_cache, v_cache, pos, None if tr is None else tr.ctypes.data, out, wabs, B, HQ,
+                                  HKV, D, R, cap, scale, threads())
     return (out, wabs) if with_abs else out
+
+
+def topk(logits: np.ndarray, k: int):
+    """fast_topk's algorithm (engine/kernels/topk.py:17-37): (vals [N, k] fp32, idxs [N, k] int32)."""
+    logits = _u16(logits)
+    N, V = logits.shape
+    vals = np.empty((N, k), dtype=np.float32)
+    idxs = np.empty((N, k), dtype=np.int32)
+    lib().oracle_topk_bf16(logits, logits.shape[1], N, V, k, vals, idxs)
+    return vals, idxs

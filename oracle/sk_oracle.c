@@ -279,14 +279,15 @@ void oracle_qk_norm_rope_cache_bf16(const uint16_t* qkv, int64_t ld, const uint1
 
 /* Decode attention (engine/kernels/attention.py:221-242, SDPA over the valid
  * keys): query row t of sequence b (head h, KV head h / (HQ/HKV)) attends to
- * keys 0 .. pos[b] + t with scores scale * q.k; softmax and the weighted sum
+ * keys 0 .. pos[b] + t (tree == NULL) or to keys < pos[b] and the draft keys
+ * pos[b] + j with bit j of tree[t] set, with scores scale * q.k; softmax and the weighted sum
  * of V are formed in fp64 from the bf16 inputs (exact attention, no bf16
  * probabilities); out [B, R, HQ, D] fp32.  wabs (optional, same shape) gets
  * sum_n p_n |v_n| / sum_n p_n, the scale of the error that rounding the
  * probabilities to bf16 can cause.  OpenMP over (b, h). */
 void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* pos,
-                             float* out, float* wabs, int B, int HQ, int HKV, int D, int R, int cap, float scale,
-                             int threads) {
+                             const int64_t* tree, float* out, float* wabs, int B, int HQ, int HKV, int D, int R,
+                             int cap, float scale, int threads) {
   const int G = HQ / HKV;
 #pragma omp parallel for collapse(2) schedule(dynamic) num_threads(threads > 0 ? threads : 1)
   for (int b = 0; b < B; ++b)
@@ -298,18 +299,30 @@ void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const u
       double* acc = (double*)malloc(sizeof(double) * (size_t)D * 2);   /* [sum p v | sum p |v|] */
       for (int t = 0; t < R; ++t) {
         const uint16_t* qr = q + ((int64_t)(b * HQ + h) * R + t) * D;
-        int L = pos[b] + t + 1;
+        /* visible keys: 0 .. pos + t (chain), or keys < pos plus the draft
+           keys pos + j whose bit j is set in tree[t] (attention.py:229-236) */
+        int L = tree ? pos[b] + R : pos[b] + t + 1;
         if (L > cap) L = cap;
         double mx = -INFINITY;
+        int any = 0;
         for (int n = 0; n < L; ++n) {
+          const int rel = n - pos[b];
+          const int vis = !tree || rel < 0 || ((tree[t] >> rel) & 1);
+          if (!vis) {
+            sc[n] = -INFINITY;
+            continue;
+          }
           double d = 0.0;
           for (int i = 0; i < D; ++i) d += (double)bf2f(qr[i]) * (double)bf2f(K[(int64_t)n * D + i]);
           sc[n] = d * (double)scale;
           if (sc[n] > mx) mx = sc[n];
+          any = 1;
         }
+        if (!any) L = 0;
         double den = 0.0;
         for (int i = 0; i < 2 * D; ++i) acc[i] = 0.0;
         for (int n = 0; n < L; ++n) {
+          if (sc[n] == -INFINITY) continue;
           const double p = exp(sc[n] - mx);
           den += p;
           for (int i = 0; i < D; ++i) {
@@ -327,4 +340,43 @@ void oracle_decode_attention(const uint16_t* q, const uint16_t* k_cache, const u
       free(sc);
       free(acc);
     }
+}
+
+/* fast_topk (engine/kernels/topk.py:17-37): 2048 lanes sweep each row with
+ * stride 2048 (strictly larger replaces: the first occurrence of a value keeps
+ * its lane); rank k = largest remaining lane maximum, lowest column among the
+ * lanes holding it; every lane holding that column is then cleared to -inf.
+ * vals [N, K] fp32, idxs [N, K] int32. */
+void oracle_topk_bf16(const uint16_t* L, int64_t ld, int N, int V, int K, float* vals, int32_t* idxs) {
+  enum { LANES = 2048 };
+  float best[LANES];
+  int bidx[LANES];
+  for (int r = 0; r < N; ++r) {
+    const uint16_t* x = L + (int64_t)r * ld;
+    for (int j = 0; j < LANES; ++j) {
+      best[j] = -INFINITY;
+      bidx[j] = 0;
+    }
+    for (int start = 0; start < V; start += LANES)
+      for (int j = 0; j < LANES; ++j) {
+        const int c = start + j;
+        const float v = c < V ? bf2f(x[c]) : -INFINITY;
+        if (v > best[j]) {
+          best[j] = v;
+          bidx[j] = c;
+        }
+      }
+    for (int k = 0; k < K; ++k) {
+      float m = -INFINITY;
+      for (int j = 0; j < LANES; ++j)
+        if (best[j] > m) m = best[j];
+      int ci = 0x7FFFFFFF;
+      for (int j = 0; j < LANES; ++j)
+        if (best[j] == m && bidx[j] < ci) ci = bidx[j];
+      vals[(int64_t)r * K + k] = m;
+      idxs[(int64_t)r * K + k] = ci;
+      for (int j = 0; j < LANES; ++j)
+        if (bidx[j] == ci) best[j] = -INFINITY;
+    }
+  }
 }

@@ -44,6 +44,7 @@ EXPORTS = (
     "sk_add_rmsnorm_bf16", "sk_swiglu_bf16",
     "sk_rmsnorm_gemm_bf16", "sk_rmsnorm_gateup_swiglu_bf16", "sk_rmsnorm_lm_argmax_bf16",
     "sk_qk_norm_rope_cache_bf16", "sk_decode_attention_workspace_bytes", "sk_decode_attention_bf16",
+    "sk_topk_bf16",
 )
 
 
@@ -109,7 +110,8 @@ _SIGNATURES = {
     "sk_qk_norm_rope_cache_bf16": (_i32, [_p, _i64, _p, _p, _p, _p, _i32, _p, _p, _p, _p,
                                           _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p]),
     "sk_decode_attention_workspace_bytes": (_sz, [_i32] * 8),
-    "sk_decode_attention_bf16": (_i32, [_p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+    "sk_topk_bf16": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _p, _p]),
+    "sk_decode_attention_bf16": (_i32, [_p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                         ctypes.c_float, _i32, _p, _sz, _p]),
 }
 

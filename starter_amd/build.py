@@ -39,7 +39,8 @@ NORM_EPIS = (5, 6, 7)   # the first three with the norm prologue (GEMV path only
 
 
 def _units() -> list[tuple[Path, list[str], Path]]:
-    units = [(CSRC / "sk_abi.hip", [], BUILD / "sk_abi.o"), (CSRC / "sk_attn.hip", [], BUILD / "sk_attn.o")]
+    units = [(CSRC / "sk_abi.hip", [], BUILD / "sk_abi.o"), (CSRC / "sk_attn.hip", [], BUILD / "sk_attn.o"),
+             (CSRC / "sk_topk.hip", [], BUILD / "sk_topk.o")]
     for epi in range(N_EPI):
         units.append((CSRC / "sk_inst_mfma.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfma_{epi}.o"))
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))

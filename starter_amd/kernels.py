@@ -18,6 +18,7 @@ _norm_stats + _normed_tile   rmsnorm_gemm / rmsnorm_gateup_swiglu / rmsnorm_lm_a
 add_rms_norm  add_rmsnorm.py add_rms_norm (sk_add_rmsnorm_bf16)
 swiglu        swiglu.py      swiglu (sk_swiglu_bf16)
 fast_topk[0]  topk.py:40     argmax (sk_argmax_bf16)
+fast_topk     topk.py:40     fast_topk (sk_topk_bf16, same lane-sweep algorithm)
 qk_norm_rope_cache rope.py   qk_norm_rope_cache (sk_qk_norm_rope_cache_bf16)
 DecodeAttention attention.py DecodeAttention (sk_decode_attention_bf16, chain masks)
 logits.argmax engine.py:207  LmArgmax (sk_lm_argmax_bf16, fused into lm_head)
@@ -47,7 +48,7 @@ __all__ = [
     "add_rms_norm", "swiglu", "pick_matmul", "pick_gateup", "pick_normed", "pick_lm_argmax", "SkConfig",
     "SK_PATH_MFMA", "SK_PATH_GEMV", "SK_OP_GEMM", "SK_OP_GATEUP", "SK_OP_LM_ARGMAX", "SK_OP_ARGMAX",
     "SK_OP_RMSNORM_GEMM", "SK_OP_RMSNORM_GATEUP", "SK_OP_RMSNORM_LM_ARGMAX",
-    "qk_norm_rope_cache", "DecodeAttention",
+    "qk_norm_rope_cache", "DecodeAttention", "ancestor_masks", "fast_topk",
 ]
 
 
@@ -255,6 +256,19 @@ def argmax(logits: torch.Tensor, ws: torch.Tensor | None = None):
     return ids, maxv
 
 
+def fast_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """[N, V] bf16 -> (values [N, k] float32, indices [N, k] int32); indices[:, 0]
+    is the exact argmax (engine/kernels/topk.py:40-46, same algorithm)."""
+    _mat(logits, "logits")
+    N, V = logits.shape
+    vals = torch.empty((N, k), dtype=torch.float32, device=logits.device)
+    idxs = torch.empty((N, k), dtype=torch.int32, device=logits.device)
+    _device_guard(logits)
+    check(lib().sk_topk_bf16(logits.data_ptr(), logits.stride(0), N, V, k, vals.data_ptr(), idxs.data_ptr(),
+                             _stream(logits)), "sk_topk_bf16")
+    return vals, idxs
+
+
 def add_rms_norm(x: torch.Tensor, y: torch.Tensor, weight: torch.Tensor, eps: float,
                  xout: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """``xout = x + y`` (bf16; in place into ``x`` when ``xout`` is None), returns
@@ -330,16 +344,17 @@ class DecodeAttention:
     (engine/kernels/attention.py:152-202).  Split count and key ranges are
     fixed at construction from ``maxlen`` (default cap); the valid length of
     each sequence is read from ``pos`` on the device at every call, so one
-    instance replays inside a graph while the sequences grow.  Draft trees are
-    not supported; ``block_n``/``num_warps``/``num_stages`` are accepted for
-    signature compatibility."""
+    instance replays inside a graph while the sequences grow.  ``R`` query rows
+    per sequence (speculative verify), chain-masked, or with ``tree=True``
+    masked by per-row ancestor bit masks passed at call time.
+    ``block_n``/``num_warps``/``num_stages`` are accepted for signature
+    compatibility."""
 
     def __init__(self, B: int, HQ: int, HKV: int, D: int, cap: int, device, nsplit: int | None = None,
                  block_n: int = 64, num_warps: int = 4, num_stages: int = 2, R: int = 1, tree: bool = False,
                  maxlen: int | None = None):
-        if tree:
-            raise NotImplementedError("draft-tree masks are not supported")
         self.B, self.HQ, self.HKV, self.D, self.cap, self.R = B, HQ, HKV, D, cap, R
+        self.tree = tree
         self.maxlen = maxlen or 0
         self.nsplit = nsplit or 0
         self.scale = 1.0 / math.sqrt(D)
@@ -349,20 +364,37 @@ class DecodeAttention:
     def __call__(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
                  out: torch.Tensor, tree: torch.Tensor | None = None) -> None:
         """q [B, HQ, R, D] bf16; k/v_cache [B, HKV, cap, D]; pos [B] int32 (position of
-        query row 0); out [B, R, HQ, D] bf16."""
-        if tree is not None:
-            raise NotImplementedError("draft-tree masks are not supported")
+        query row 0); out [B, R, HQ, D] bf16; tree [R] int64 ancestor masks when this
+        instance was built with tree=True."""
         B, HQ, HKV, D, R, cap = self.B, self.HQ, self.HKV, self.D, self.R, self.cap
         _need(q.shape == (B, HQ, R, D) and q.is_contiguous() and q.dtype == BF16, "q must be [B, HQ, R, D] bf16")
         _need(k_cache.shape == (B, HKV, cap, D) and v_cache.shape == k_cache.shape, "cache shapes")
         _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous caches")
         _need(out.shape == (B, R, HQ, D) and out.is_contiguous(), "out must be [B, R, HQ, D]")
         _i32_dev(pos, "pos")
+        if self.tree:
+            _need(tree is not None and tree.is_cuda and tree.dtype == torch.int64 and tree.numel() == R,
+                  "tree=True needs tree [R] int64 on the device")
+        else:
+            _need(tree is None, "this instance was built without tree masks")
         _device_guard(q)
         wp, wn = _ws_args(self.ws)
         check(lib().sk_decode_attention_bf16(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(),
-                                             out.data_ptr(), B, HQ, HKV, D, R, cap, self.maxlen, float(self.scale),
-                                             self.nsplit, wp, wn, _stream(q)), "sk_decode_attention_bf16")
+                                             tree.data_ptr() if tree is not None else None, out.data_ptr(), B, HQ,
+                                             HKV, D, R, cap, self.maxlen, float(self.scale), self.nsplit, wp, wn,
+                                             _stream(q)), "sk_decode_attention_bf16")
+
+
+def ancestor_masks(parent: list[int]) -> list[int]:
+    """Per-node int64 bit mask of the node and its ancestors (engine/kernels/attention.py:245-254)."""
+    masks = []
+    for i in range(len(parent)):
+        m, n = 0, i
+        while n >= 0:
+            m |= 1 << n
+            n = parent[n]
+        masks.append(m - (1 << 64) if m >= (1 << 63) else m)
+    return masks
 
 
 # ---------------------------------------------------------------------------

@@ -193,3 +193,39 @@ def test_decode_attention_visible_key_boundary(nsplit):
         for kh in range(HKV):
             o = out[b, 0, kh * (HQ // HKV)].float().cpu()
             assert torch.allclose(o, vc[b, kh, pos[b]].float(), atol=0.05), (b, kh)
+
+
+@pytest.mark.parametrize("R,nsplit", [(5, None), (8, 3), (3, 1)])
+def test_decode_attention_verify_rows_chain(R, nsplit):
+    """Speculative verify: R query rows per sequence (G*R up to 32 here, so
+    several 8-row blocks), chain mask (row t sees keys <= pos + t)."""
+    B, HQ, HKV, CAP = 4, 32, 8, 700
+    g = torch.Generator().manual_seed(R * 10 + (nsplit or 0))
+    q = randn_bf16((B, HQ, R, D), 1.0, g)
+    kc = randn_bf16((B, HKV, CAP, D), 1.0, g)
+    vc = randn_bf16((B, HKV, CAP, D), 1.0, g)
+    pos = np.array([0, 100, 511, 690 - R], np.int32)
+    attn = K.DecodeAttention(B, HQ, HKV, D, CAP, DEV, R=R, nsplit=nsplit)
+    out = torch.empty(B, R, HQ, D, dtype=BF16, device=DEV)
+    attn(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.from_numpy(pos).to(DEV), out)
+    ref = oracle.decode_attention(bits(q), bits(kc), bits(vc), pos, D ** -0.5, with_abs=True)
+    _check_attention(out, ref, f"verify chain R={R} nsplit={nsplit}")
+
+
+@pytest.mark.parametrize("nsplit", [None, 2])
+def test_decode_attention_draft_tree(nsplit):
+    """Draft tree (attention.py:229-236): row t sees keys < pos and the draft
+    keys on its ancestor path (masks from kernels.ancestor_masks)."""
+    B, HQ, HKV, CAP, R = 3, 32, 8, 400, 6
+    parent = [-1, 0, 0, 1, 1, 2]
+    tree = torch.tensor(K.ancestor_masks(parent), dtype=torch.int64)
+    g = torch.Generator().manual_seed(17)
+    q = randn_bf16((B, HQ, R, D), 1.0, g)
+    kc = randn_bf16((B, HKV, CAP, D), 1.0, g)
+    vc = randn_bf16((B, HKV, CAP, D), 1.0, g)
+    pos = np.array([10, 200, 393], np.int32)
+    attn = K.DecodeAttention(B, HQ, HKV, D, CAP, DEV, R=R, tree=True, nsplit=nsplit)
+    out = torch.empty(B, R, HQ, D, dtype=BF16, device=DEV)
+    attn(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.from_numpy(pos).to(DEV), out, tree.to(DEV))
+    ref = oracle.decode_attention(bits(q), bits(kc), bits(vc), pos, D ** -0.5, with_abs=True, tree=tree.numpy())
+    _check_attention(out, ref, f"tree nsplit={nsplit}")

@@ -436,3 +436,68 @@ def test_oracle_attention_special_cases():
     for b in range(B):
         mean = vc[b, 0, : int(pos[b]) + 1].double().mean(0).numpy()
         assert np.abs(out[b, 0, 0] - mean).max() < 1e-6
+
+
+# --------------------------------------------------------------------------
+# fast_topk (engine/kernels/topk.py)
+# --------------------------------------------------------------------------
+
+def _exact_topk(L: torch.Tensor, k: int):
+    """Exact top-k with the lowest column first among equal values (stable sort)."""
+    s = torch.sort(L.float(), dim=-1, descending=True, stable=True)
+    return s.values[:, :k].numpy(), s.indices[:, :k].to(torch.int32).numpy()
+
+
+@pytest.mark.parametrize("V", [5, 1500, 2048])
+def test_oracle_topk_is_exact_when_every_column_has_its_own_lane(V):
+    """V <= 2048: each lane sees one column, so the lane sweep is an exact
+    top-k with the lowest-index tie rule (values drawn coarse to force ties)."""
+    g = torch.Generator().manual_seed(V)
+    L = (torch.randint(-40, 40, (4, V), generator=g).float() / 8).to(BF16)
+    k = min(8, V)
+    v, i = oracle.topk(bits(L), k)
+    ev, ei = _exact_topk(L, k)
+    assert np.array_equal(v, ev) and np.array_equal(i, ei)
+
+
+def test_oracle_topk_rank0_is_torch_argmax_and_lane_collisions_are_missed():
+    V = 151936
+    g = torch.Generator().manual_seed(1)
+    L = randn_bf16((3, V), 1.0, g)
+    L[0, 5000] = 20.0
+    L[0, 5000 + 2048] = 19.0      # same lane as column 5000: the documented miss
+    L[0, 77] = 18.0
+    L[1, 100] = L[1, 9000] = 30.0  # exact tie in different lanes: lowest index first
+    v, i = oracle.topk(bits(L), 4)
+    assert np.array_equal(i[:, 0], torch.argmax(L, -1).numpy())
+    assert list(i[0, :2]) == [5000, 77] and 5000 + 2048 not in i[0]
+    assert list(i[1, :2]) == [100, 9000] and v[1, 0] == v[1, 1] == 30.0
+
+
+def test_oracle_attention_tree_mask_matches_sdpa():
+    """Draft-tree masks (engine/kernels/attention.py:229-236): row t sees every
+    key before pos and the draft keys on its ancestor path."""
+    B, HQ, HKV, R, CAP = 2, 8, 2, 5, 120
+    q, kc, vc = _attn_inputs(B, HQ, HKV, R, CAP, seed=21)
+    parent = [-1, 0, 0, 1, 2]
+    masks = []
+    for i in range(R):
+        m, n = 0, i
+        while n >= 0:
+            m |= 1 << n
+            n = parent[n]
+        masks.append(m)
+    tree = np.array(masks, np.int64)
+    pos = np.array([50, 100], np.int32)
+    scale = 128 ** -0.5
+    out = oracle.decode_attention(bits(q), bits(kc), bits(vc), pos, scale, tree=tree)
+    for b in range(B):
+        p = int(pos[b])
+        L = p + R
+        k = kc[b, :, :L].double().repeat_interleave(HQ // HKV, dim=0)
+        v = vc[b, :, :L].double().repeat_interleave(HQ // HKV, dim=0)
+        draft = torch.tensor([[(masks[t] >> j) & 1 for j in range(R)] for t in range(R)], dtype=torch.bool)
+        mask = torch.cat([torch.ones(R, p, dtype=torch.bool), draft], dim=1)
+        ref = F.scaled_dot_product_attention(q[b].double(), k, v, attn_mask=mask[None], scale=scale)
+        got = torch.from_numpy(out[b]).transpose(0, 1).double()
+        assert (got - ref).abs().max().item() < 1e-5
