@@ -397,6 +397,23 @@ def ancestor_masks(parent: list[int]) -> list[int]:
     return masks
 
 
+def chain_tree(R: int, device) -> torch.Tensor:
+    """Ancestor masks of a plain chain, row t sees draft rows 0..t
+    (engine/kernels/attention.py:257-259)."""
+    return torch.tensor(ancestor_masks([t - 1 for t in range(R)]), dtype=torch.int64, device=device)
+
+
+def pick_attention(B: int, HQ: int, HKV: int, D: int, cap: int, typical_len: int, device, log=None, R: int = 1,
+                   tree: bool = False, maxlen: int | None = None) -> DecodeAttention:
+    """engine/kernels/attention.py:262-314 signature.  The split count comes from
+    the library's plan (about 256 workgroups over the key range ``maxlen``), so
+    nothing is timed at warmup; ``typical_len`` only feeds the log line."""
+    attn = DecodeAttention(B, HQ, HKV, D, cap, device, R=R, tree=tree, maxlen=maxlen)
+    if log:
+        log(f"attention B={B} R={R} len={typical_len}: HIP decode attention, tree={tree}, maxlen={maxlen or cap}")
+    return attn
+
+
 # ---------------------------------------------------------------------------
 # Reference-shaped classes: fixed (M, N, K) and config per instance.
 # ---------------------------------------------------------------------------
