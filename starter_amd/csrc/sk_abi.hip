@@ -276,10 +276,10 @@ struct Tuned {
 
 const Tuned kTuned[] = {
     {SK_OP_GEMM, 6144, 2560, 1, {2, 1, 5, 2, 1, 0}},  // qkv        7.29 us  4315 GB/s
-    {SK_OP_GEMM, 6144, 2560, 2, {3, 10, 8, 16, 1, 0}},  // qkv        8.27 us  3807 GB/s
-    {SK_OP_GEMM, 6144, 2560, 4, {3, 10, 8, 16, 1, 0}},  // qkv        8.44 us  3733 GB/s
-    {SK_OP_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 0}},  // qkv        8.75 us  3612 GB/s
-    {SK_OP_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv        9.71 us  3268 GB/s
+    {SK_OP_GEMM, 6144, 2560, 2, {3, 10, 8, 32, 1, 192}},  // qkv        7.72 us  4079 GB/s
+    {SK_OP_GEMM, 6144, 2560, 4, {3, 10, 8, 32, 1, 0}},  // qkv        7.88 us  4001 GB/s
+    {SK_OP_GEMM, 6144, 2560, 8, {3, 10, 8, 32, 1, 192}},  // qkv        8.33 us  3793 GB/s
+    {SK_OP_GEMM, 6144, 2560, 16, {3, 10, 8, 32, 1, 192}},  // qkv        9.35 us  3394 GB/s
     {SK_OP_GEMM, 6144, 2560, 32, {3, 5, 16, 16, 1, 0}},  // qkv       13.87 us  2308 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {1, 16, 5, 16, 1, 0}},  // qkv       17.01 us  1890 GB/s
     {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
@@ -288,30 +288,31 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     7.22 us  2912 GB/s
     {SK_OP_GEMM, 2560, 4096, 8, {3, 16, 8, 16, 1, 0}},  // o_proj     7.77 us  2712 GB/s
     {SK_OP_GEMM, 2560, 4096, 16, {3, 8, 16, 16, 1, 0}},  // o_proj     9.39 us  2256 GB/s
-    {SK_OP_GEMM, 2560, 4096, 32, {3, 8, 16, 16, 1, 0}},  // o_proj    13.42 us  1594 GB/s
+    {SK_OP_GEMM, 2560, 4096, 32, {3, 8, 8, 32, 2, 0}},  // o_proj    13.50 us  1585 GB/s
     {SK_OP_GEMM, 2560, 4096, 40, {3, 8, 8, 32, 2, 0}},  // o_proj    15.86 us  1356 GB/s
     {SK_OP_GEMM, 2560, 4096, 64, {3, 8, 8, 16, 2, 0}},  // o_proj    20.33 us  1073 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // gate_up   17.94 us  5553 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 2, {3, 5, 16, 16, 1, 0}},  // gate_up   18.39 us  5421 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 4, {3, 5, 16, 16, 1, 0}},  // gate_up   18.67 us  5340 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 8, {3, 5, 16, 16, 1, 0}},  // gate_up   19.36 us  5155 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 16, {3, 5, 16, 16, 1, 0}},  // gate_up   20.53 us  4872 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
+    {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
+    {SK_OP_GATEUP, 9728, 2560, 2, {3, 10, 8, 16, 1, 203}},  // gate_up   17.33 us  5751 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 4, {3, 10, 8, 16, 1, 203}},  // gate_up   17.56 us  5678 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 8, {3, 10, 8, 16, 1, 203}},  // gate_up   18.02 us  5539 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 16, {3, 10, 8, 16, 1, 203}},  // gate_up   19.11 us  5233 GB/s
     {SK_OP_GATEUP, 9728, 2560, 32, {3, 5, 8, 16, 2, 0}},  // gate_up   32.85 us  3056 GB/s
     {SK_OP_GATEUP, 9728, 2560, 40, {1, 8, 10, 16, 1, 0}},  // gate_up   35.69 us  2819 GB/s
     {SK_OP_GATEUP, 9728, 2560, 64, {1, 5, 8, 16, 2, 0}},  // gate_up   56.95 us  1777 GB/s
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
-    {SK_OP_GEMM, 2560, 9728, 2, {2, 2, 10, 2, 1, 0}},  // down      13.01 us  3831 GB/s
+    {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      13.60 us  3666 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {2, 4, 5, 2, 1, 0}},  // down      12.89 us  3870 GB/s
-    {SK_OP_GEMM, 2560, 9728, 8, {3, 7, 16, 32, 3, 0}},  // down      14.74 us  3393 GB/s
+    {SK_OP_GEMM, 2560, 9728, 8, {3, 13, 8, 32, 3, 240}},  // down      13.97 us  3579 GB/s
     {SK_OP_GEMM, 2560, 9728, 16, {3, 13, 8, 16, 3, 0}},  // down      16.79 us  2990 GB/s
     {SK_OP_GEMM, 2560, 9728, 32, {3, 7, 16, 16, 3, 0}},  // down      23.23 us  2178 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {1, 16, 5, 16, 4, 0}},  // down      26.15 us  1942 GB/s
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 16, 5, 0}},  // down      36.59 us  1404 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 5, 16, 16, 1, 0}},  // lm_head  114.77 us  6778 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 4, {3, 10, 8, 16, 1, 0}},  // lm_head  114.94 us  6768 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 8, {3, 10, 8, 16, 1, 0}},  // lm_head  115.46 us  6738 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 16, {3, 5, 16, 16, 1, 0}},  // lm_head  115.83 us  6717 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 16, 1, 0}},  // lm_head  118.23 us  6580 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 4, {3, 10, 8, 32, 1, 0}},  // lm_head  113.88 us  6831 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 8, {3, 10, 8, 32, 1, 0}},  // lm_head  114.03 us  6822 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 16, {3, 10, 8, 32, 1, 0}},  // lm_head  114.85 us  6774 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 32, {3, 5, 16, 16, 1, 0}},  // lm_head  119.79 us  6495 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {1, 8, 10, 16, 1, 0}},  // lm_head  160.11 us  4860 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {1, 8, 10, 16, 1, 0}},  // lm_head  190.38 us  4088 GB/s
@@ -422,10 +423,21 @@ int mfma_search_config(int op, int M, int N, int K, int num_cu, sk_config* out) 
 
 int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   if (M < 1 || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
-  op = base_op(op);   // a norm op uses its projection's configuration
-  if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   const int Mk = M > kMaxM ? kMaxM : M;
   Plan pl;
+  // A norm op takes its own entry where the table has one (the fused GEMV
+  // prologue can beat a faster projection plus a separate norm launch), else
+  // its projection's configuration.
+  if (is_norm_op(op)) {
+    if (const Tuned* t = tuned_lookup(op, Mk, N, K)) {
+      if (plan_shape(op, Mk, N, K, t->cfg, &pl) == SK_OK) {
+        *out = t->cfg;
+        return SK_OK;
+      }
+    }
+  }
+  op = base_op(op);
+  if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   if (const Tuned* t = tuned_lookup(op, Mk, N, K)) {
     if (plan_shape(op, Mk, N, K, t->cfg, &pl) == SK_OK) {
       *out = t->cfg;

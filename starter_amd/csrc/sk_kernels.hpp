@@ -262,10 +262,26 @@ __device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int n
   const int nout = M * OUT_ROWS;
   for (int idx = tid; idx < nout; idx += nthr) {
     const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
+    // All waves' partials are read first (independent LDS loads in flight
+    // together), then summed in wave order 0..nw-1.
+    // Four waves' partials per step are read together (independent LDS loads
+    // in flight), then added in wave order 0..nw-1; slots past nw-1 read wave
+    // nw-1's slot (in bounds) and are masked to +0.
     float g = 0.f, u = 0.f;
-    for (int w = 0; w < nw; ++w) {
-      g += P[(w * M + m) * ROWS + r];
-      if constexpr (GU) u += P[(w * M + m) * ROWS + r + OUT_ROWS];
+    for (int w0 = 0; w0 < nw; w0 += 4) {
+      float pg[4], pu[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ws = min(w0 + i, nw - 1);
+        pg[i] = P[(ws * M + m) * ROWS + r];
+        if constexpr (GU) pu[i] = P[(ws * M + m) * ROWS + r + OUT_ROWS];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t keep = w0 + i < nw ? 0xFFFFFFFFu : 0u;
+        g += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pg[i]) & keep);
+        if constexpr (GU) u += __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, pu[i]) & keep);
+      }
     }
     const int sidx = (j * M + m) * OUT_ROWS + r;
     if constexpr (EPI == EPI_STORE) {
@@ -559,7 +575,7 @@ __device__ __forceinline__ void mfma_body(Args p) {
 // rows are loaded into registers while the current tile is multiplied.
 // ---------------------------------------------------------------------------
 template <int MT, int NT, int KW, int EPI>
-__device__ __forceinline__ void mfmt_body(Args p) {
+__device__ __forceinline__ void mfmt_tile_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int BASE = EpiTraits<EPI>::base;   // epilogue without the norm prologue
   static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
@@ -734,6 +750,160 @@ __device__ __forceinline__ void mfmt_body(Args p) {
     if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU)
       splitk_fixup<OUT_ROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
   }
+}
+
+// ---------------------------------------------------------------------------
+// Ring-streamed variant of the path above for 256-column chunks (KW = 256).
+// A load instruction reads 512 B of each of two rows (lanes 0-31: row 2q,
+// lanes 32-63: row 2q+1), so one 16-row slab is 8 instructions.  The wave
+// keeps exactly one slab of loads in flight in an 8-register ring and
+// refills each register as soon as it has been written to the staging
+// region, so new loads are issued one at a time while the previous slab is
+// multiplied, across slab and tile boundaries alike; only the last slab of
+// the last tile issues nothing.  The activation fragments are loaded before
+// the first slab, so no wait for them remains inside the stream.
+// ---------------------------------------------------------------------------
+template <int MT, int NT, int EPI>
+__device__ __forceinline__ void mfmt_ring_body(Args p) {
+  constexpr bool GATEUP = EpiTraits<EPI>::gateup;
+  constexpr int BASE = EpiTraits<EPI>::base;
+  static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
+  static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
+  constexpr int KW = 256;
+  constexpr int ROWS = 16 * NT;                  // weight rows per tile
+  constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
+  constexpr int UNITS = KW / 32;                 // MFMA K steps per slab
+  constexpr int RING = 8;                        // load instructions per 16-row slab
+  constexpr int PITCH = 2 * KW + 16;             // LDS bytes per staged row
+
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = p.nw;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int M = p.M;
+
+  const int S = p.S;
+  const int slice = blockIdx.x % S;
+  const int rbstep = p.rbstep;
+  const int rb0 = blockIdx.x / S;
+  const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
+  const int chunks = (p.K + KW - 1) / KW;
+  const int c_lo = slice * p.slice_units;
+  const int c_hi = min(c_lo + p.slice_units, chunks);
+  const int chunk = c_lo + wave;
+  const bool has_chunk = chunk < c_hi;   // wave-uniform
+  const int k0 = min(chunk, chunks - 1) * KW;
+
+  char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
+  float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
+  const int part_floats = nw * M * ROWS;
+  void* stage = parts + 2 * part_floats;
+  unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
+  if constexpr (BASE == EPI_ARGMAX) {
+    if (tid < M) lds_best[tid] = 0ull;
+  }
+
+  // Activation fragments (lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8]);
+  // rows m >= M repeat row M-1 and only feed MFMA columns that are never read.
+  const bool full_chunk = has_chunk && k0 + KW <= p.K;
+  bf16x8 af[MT][UNITS];
+  auto load_acts = [&](auto full) {
+    constexpr bool FULL = decltype(full)::value;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int64_t roff = (int64_t)min(16 * mt + r16, M - 1) * p.lda;
+#pragma unroll
+      for (int u = 0; u < UNITS; ++u) {
+        const int k = k0 + 32 * u + 8 * g4;
+        u32x4 v = ld16(p.A + roff + (FULL ? k : min(k, p.K - 8)));
+        if (!(FULL || (k < p.K && has_chunk))) v = u32x4{0u, 0u, 0u, 0u};
+        af[mt][u] = __builtin_bit_cast(bf16x8, v);
+      }
+    }
+  };
+  if (full_chunk) load_acts(std::true_type{});
+  else load_acts(std::false_type{});
+
+  // Instruction q of slab (rb, nt): rows 2q + lane/32 of the slab, 8 columns at
+  // k0 + 8*(lane%32) (clamped in bounds; padding meets zero activations).
+  const int lcol = min(k0 + 8 * (lane & 31), p.K - 8);
+  const int lrow = lane >> 5;
+  auto wsrc = [&](int rb, int nt, int q) -> const uint16_t* {
+    const int t = 2 * q + lrow;
+    if constexpr (GATEUP) {
+      const int row = min(rb * 16 + t, p.N - 1);
+      return (nt == 0 ? p.W0 : p.W1) + (int64_t)row * p.ldw + lcol;
+    } else {
+      const int row = min(rb * ROWS + 16 * nt + t, p.N - 1);
+      return p.W0 + (int64_t)row * p.ldw + lcol;
+    }
+  };
+  char* const wdst = tr + lrow * PITCH + 16 * (lane & 31);
+
+  u32x4 ring[RING];
+  if (ntiles > 0) {
+#pragma unroll
+    for (int q = 0; q < RING; ++q) ring[q] = ld16_stream(wsrc(rb0, 0, q));
+  }
+
+  auto tile = [&](int j, auto last) {
+    constexpr bool LAST = decltype(last)::value;
+    const int rb = rb0 + j * rbstep;
+    f32x4 acc[NT][MT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const bool wrap = nt + 1 == NT;
+      const int rbn = wrap ? rb + rbstep : rb;
+      const int ntn = wrap ? 0 : nt + 1;
+      // Stage the slab (wave-private region; one wave's LDS accesses execute
+      // in order, so the previous slab's fragment reads are done) and refill.
+#pragma unroll
+      for (int q = 0; q < RING; ++q) {
+        *reinterpret_cast<u32x4*>(wdst + 2 * q * PITCH) = ring[q];
+        if (!(LAST && wrap)) ring[q] = ld16_stream(wsrc(rbn, ntn, q));
+        __builtin_amdgcn_sched_barrier(0);   // keep each refill next to its staging store
+      }
+#pragma unroll
+      for (int u = 0; u < UNITS; ++u) {
+        const bf16x8 wv = *reinterpret_cast<const bf16x8*>(tr + r16 * PITCH + 64 * u + 16 * g4);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[mt][u], acc[nt][mt], 0, 0, 0);
+      }
+    }
+    float* P = parts + (j & 1) * part_floats;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + r16;
+        if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
+      }
+    lds_barrier();
+    tile_reduce<ROWS, BASE>(p, P, nw, rb, j, stage, lds_best);
+  };
+
+  int j = 0;
+  for (; j + 1 < ntiles; ++j) tile(j, std::false_type{});
+  if (ntiles > 0) tile(j, std::true_type{});
+  lds_barrier();
+  if constexpr (BASE == EPI_ARGMAX) {
+    argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
+  } else {
+    flush_stage<OUT_ROWS, BASE>(p, stage, ntiles, rb0, slice);
+    if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU)
+      splitk_fixup<OUT_ROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+  }
+}
+
+template <int MT, int NT, int KW, int EPI>
+__device__ __forceinline__ void mfmt_body(Args p) {
+  if constexpr (KW == 256) mfmt_ring_body<MT, NT, EPI>(p);
+  else mfmt_tile_body<MT, NT, KW, EPI>(p);
 }
 
 // ---------------------------------------------------------------------------

@@ -31,9 +31,10 @@ constexpr int gemv_regs(int MR, int RR, int KU, bool norm = false) {
   return 4 * KU * (MR + RR) + RR * MR + 24 + (norm ? norm_extra(4 * KU * MR, 4 * KU * RR, 4 * KU) : 0);
 }
 // LDS-transposed MFMA: KW/32 activation units per tile row block plus the
-// staged weight rows (KW/512 rows per load instruction).
+// weight rows in flight: a whole tile (16*NT rows of KW/512 rows per load
+// instruction) for KW = 512, an 8-instruction ring for KW = 256.
 constexpr int mfmt_regs(int MT, int NT, int KW) {
-  return 4 * (KW / 32) * MT + 4 * (16 * NT * KW / 512) + 4 * NT * MT + 32;
+  return 4 * (KW / 32) * MT + (KW == 256 ? 4 * 8 : 4 * (16 * NT * KW / 512)) + 4 * NT * MT + 32;
 }
 // Waves per workgroup an instance is compiled for (its __launch_bounds__):
 // 16 waves leave 128 VGPRs per lane, 8 waves 256; norm-prologue instances

@@ -77,11 +77,12 @@ def test_default_config_is_valid_for_every_decode_shape(name, M):
 
 
 def test_tuned_table_drives_the_decode_shapes():
-    """Measured winners: VALU GEMV at M = 1, LDS-transposed MFMA at M = 8."""
+    """Measured winners: VALU GEMV for qkv at M = 1, LDS-transposed MFMA at M = 8
+    (gate/up: ten 256-column waves, three tiles per workgroup)."""
     assert _lib.default_config(SK_OP_GEMM, 1, 6144, 2560).path == SK_PATH_GEMV
     assert _lib.default_config(SK_OP_GEMM, 8, 6144, 2560).path == SK_PATH_MFMA_LDS
     assert _lib.default_config(SK_OP_GATEUP, 8, 9728, 2560).as_dict() == \
-        {"path": SK_PATH_MFMA_LDS, "waves": 5, "ku": 16, "rows": 16, "split": 1, "grid": 0}
+        {"path": SK_PATH_MFMA_LDS, "waves": 10, "ku": 8, "rows": 16, "split": 1, "grid": 203}
     assert _lib.default_config(SK_OP_LM_ARGMAX, 8, 151936, 2560).path == SK_PATH_MFMA_LDS
     # the lm_head logits GEMM shares the argmax entries; M = 5 takes the M = 8 entry
     assert _lib.default_config(SK_OP_GEMM, 5, 151936, 2560).as_dict() == \
@@ -199,14 +200,17 @@ def _rms_gemm(lib, x=X0, y=Y0, nw=NW0, xo=XO0, ldx=2560, W=W0, C=C0, M=8, N=6144
 @pytest.mark.parametrize("name", list(NORMED))
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 40, 64])
 def test_normed_default_config_valid_and_fused_at_decode_m(name, M):
-    """The norm ops use their projection's tuned configuration; on the GEMV
-    path with one K split (the M <= 4 defaults) the prologue runs inside the
-    projection kernel, so the workspace is the projection's own.  Otherwise the
-    workspace adds the normalised rows [M, K] bf16 after the projection's part."""
+    """The norm ops use their projection's tuned configuration (gate/up at
+    M = 1 has its own entry: the fused GEMV beats the faster LDS-fed MFMA
+    projection plus a separate norm launch); on the GEMV path with one K split
+    the prologue runs inside the projection kernel, so the workspace is the
+    projection's own.  Otherwise the workspace adds the normalised rows [M, K]
+    bf16 after the projection's part."""
     op, N, K = NORMED[name]
     cfg = _lib.default_config(op, M, N, K)
     base = _lib.default_config(BASE[op], M, N, K)
-    assert cfg.as_dict() == base.as_dict()
+    if not (M == 1 and name == "gu"):   # the table's one norm-specific entry
+        assert cfg.as_dict() == base.as_dict()
     assert _lib.check_config(op, M, N, K, cfg) == SK_OK
     plain = _lib.workspace_bytes(BASE[op], M, N, K, cfg)
     normed = _lib.workspace_bytes(op, M, N, K, cfg)
