@@ -179,16 +179,17 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     if (c.waves > sk::max_waves_for_regs(sk::mfma_regs(pl->tm, pl->tn, pl->tku < 0 ? 20 : pl->tku)))
       return SK_ERR_CONFIG;
   } else if (c.path == SK_PATH_MFMA_LDS) {
-    // One K chunk of KW = 32*ku columns (512 or 256) per wave.
+    // One K range of KW = 32*ku columns per wave: 256 or 1024 (one or four
+    // 256-column chunks, ring-streamed) or 512 (whole tiles in flight).
     if (gateup ? c.rows != 16 : (c.rows != 16 && c.rows != 32)) return SK_ERR_CONFIG;
-    if (c.ku != 16 && c.ku != 8) return SK_ERR_CONFIG;
+    if (c.ku != 8 && c.ku != 16 && c.ku != 32) return SK_ERR_CONFIG;
     const int KW = 32 * c.ku;
     units = cdiv(K, KW);
     pl->tm = cdiv(M, 16);
     pl->tn = gateup ? 2 : c.rows / 16;
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
-    if (c.waves > sk::max_waves_for_regs(sk::mfmt_regs(pl->tm, pl->tn, KW))) return SK_ERR_CONFIG;
+    if (c.waves > sk::mfmt_max_waves(pl->tm, pl->tn, KW)) return SK_ERR_CONFIG;
     pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
@@ -287,8 +288,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     6.57 us  3196 GB/s
     {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     7.22 us  2912 GB/s
     {SK_OP_GEMM, 2560, 4096, 8, {3, 16, 8, 16, 1, 0}},  // o_proj     7.77 us  2712 GB/s
-    {SK_OP_GEMM, 2560, 4096, 16, {3, 8, 16, 16, 1, 0}},  // o_proj     9.39 us  2256 GB/s
-    {SK_OP_GEMM, 2560, 4096, 32, {3, 8, 8, 32, 2, 0}},  // o_proj    13.50 us  1585 GB/s
+    {SK_OP_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj     9.01 us  2351 GB/s
+    {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj    12.35 us  1733 GB/s
     {SK_OP_GEMM, 2560, 4096, 40, {3, 8, 8, 32, 2, 0}},  // o_proj    15.86 us  1356 GB/s
     {SK_OP_GEMM, 2560, 4096, 64, {3, 8, 8, 16, 2, 0}},  // o_proj    20.33 us  1073 GB/s
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
@@ -302,10 +303,10 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 64, {1, 5, 8, 16, 2, 0}},  // gate_up   56.95 us  1777 GB/s
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      13.60 us  3666 GB/s
-    {SK_OP_GEMM, 2560, 9728, 4, {2, 4, 5, 2, 1, 0}},  // down      12.89 us  3870 GB/s
+    {SK_OP_GEMM, 2560, 9728, 4, {3, 13, 8, 32, 3, 0}},  // down      12.73 us  3920 GB/s
     {SK_OP_GEMM, 2560, 9728, 8, {3, 13, 8, 32, 3, 240}},  // down      13.97 us  3579 GB/s
-    {SK_OP_GEMM, 2560, 9728, 16, {3, 13, 8, 16, 3, 0}},  // down      16.79 us  2990 GB/s
-    {SK_OP_GEMM, 2560, 9728, 32, {3, 7, 16, 16, 3, 0}},  // down      23.23 us  2178 GB/s
+    {SK_OP_GEMM, 2560, 9728, 16, {3, 4, 32, 32, 3, 0}},  // down      15.90 us  3157 GB/s
+    {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      22.29 us  2270 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {1, 16, 5, 16, 4, 0}},  // down      26.15 us  1942 GB/s
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 16, 5, 0}},  // down      36.59 us  1404 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s

@@ -11,7 +11,7 @@
 namespace sk {
 
 template <int MT, int NT, int KW, int EPI>
-__global__ void __launch_bounds__(64 * max_waves_for_regs(mfmt_regs(MT, NT, KW)))
+__global__ void __launch_bounds__(64 * mfmt_max_waves(MT, NT, KW))
 mfmt_entry(Args p) {
   mfmt_body<MT, NT, KW, EPI>(p);
 }
@@ -19,7 +19,8 @@ mfmt_entry(Args p) {
 #define SK_C(MT, NT, KW) \
   case MT * 100000 + NT * 1000 + KW: return &mfmt_entry<MT, NT, KW, SK_EPI>;
 #define SK_LIST(NT) \
-  SK_C(1, NT, 512) SK_C(2, NT, 512) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(3, NT, 256) SK_C(4, NT, 256)
+  SK_C(1, NT, 512) SK_C(2, NT, 512) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(3, NT, 256) SK_C(4, NT, 256) \
+  SK_C(1, NT, 1024) SK_C(2, NT, 1024)
 
 KernelFn SK_CAT(mfmt_for_epi, SK_EPI)(int MT, int NT, int KW) {
   switch (MT * 100000 + NT * 1000 + KW) {

@@ -138,6 +138,11 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
 
 // Weight loads are streamed once per call: mark them non-temporal so they do
 // not evict the activations and partials from L2/MALL.
+// 128 zero bytes in device memory (never written): the source of loads for
+// columns outside K, so that such loads need neither a branch nor a mask on
+// the loaded data.
+static __device__ __attribute__((aligned(128))) uint32_t kZeroLine[32] = {};
+
 __device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
@@ -753,28 +758,35 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
 }
 
 // ---------------------------------------------------------------------------
-// Ring-streamed variant of the path above for 256-column chunks (KW = 256).
+// Ring-streamed variant of the path above for 256-column slabs.  A wave owns
+// KW = 256*CPW columns of the K slice (CPW consecutive 256-column chunks).
 // A load instruction reads 512 B of each of two rows (lanes 0-31: row 2q,
-// lanes 32-63: row 2q+1), so one 16-row slab is 8 instructions.  The wave
-// keeps exactly one slab of loads in flight in an 8-register ring and
-// refills each register as soon as it has been written to the staging
+// lanes 32-63: row 2q+1), so one 16-row slab of one chunk is 8 instructions.
+// The wave keeps exactly one slab of loads in flight in an 8-register ring
+// and refills each register as soon as it has been written to the staging
 // region, so new loads are issued one at a time while the previous slab is
-// multiplied, across slab and tile boundaries alike; only the last slab of
-// the last tile issues nothing.  The activation fragments are loaded before
-// the first slab, so no wait for them remains inside the stream.
+// multiplied, across chunk, slab and tile boundaries alike; only the last
+// slab of the last tile issues nothing.  Slab order within a tile: chunk-
+// major, then the NT 16-row groups, so a chunk's activation fragments serve
+// NT slabs.  With one chunk per wave the activations are loaded once, before
+// the first slab; with several, each chunk's are loaded when it starts (L2
+// hits: the first fragment use waits for them while that slab's weight
+// refills are already in flight).
 // ---------------------------------------------------------------------------
-template <int MT, int NT, int EPI>
+template <int MT, int NT, int CPW, int EPI>
 __device__ __forceinline__ void mfmt_ring_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int BASE = EpiTraits<EPI>::base;
   static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
   static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
-  constexpr int KW = 256;
+  static_assert(CPW >= 1, "chunks per wave");
+  constexpr int CW = 256;                        // columns per chunk (slab width)
+  constexpr int KW = CW * CPW;                   // columns per wave
   constexpr int ROWS = 16 * NT;                  // weight rows per tile
   constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
-  constexpr int UNITS = KW / 32;                 // MFMA K steps per slab
+  constexpr int UNITS = CW / 32;                 // MFMA K steps per slab
   constexpr int RING = 8;                        // load instructions per 16-row slab
-  constexpr int PITCH = 2 * KW + 16;             // LDS bytes per staged row
+  constexpr int PITCH = 2 * CW + 16;             // LDS bytes per staged row
 
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x;
@@ -789,12 +801,12 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   const int rbstep = p.rbstep;
   const int rb0 = blockIdx.x / S;
   const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
-  const int chunks = (p.K + KW - 1) / KW;
+  const int units = (p.K + KW - 1) / KW;
   const int c_lo = slice * p.slice_units;
-  const int c_hi = min(c_lo + p.slice_units, chunks);
-  const int chunk = c_lo + wave;
-  const bool has_chunk = chunk < c_hi;   // wave-uniform
-  const int k0 = min(chunk, chunks - 1) * KW;
+  const int c_hi = min(c_lo + p.slice_units, units);
+  const int unit = c_lo + wave;
+  const bool has_unit = unit < c_hi;   // wave-uniform
+  const int kw0 = min(unit, units - 1) * KW;
 
   char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
   float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
@@ -805,39 +817,46 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
     if (tid < M) lds_best[tid] = 0ull;
   }
 
-  // Activation fragments (lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8]);
-  // rows m >= M repeat row M-1 and only feed MFMA columns that are never read.
-  const bool full_chunk = has_chunk && k0 + KW <= p.K;
+  // Loads are never masked or branched around: a column group past K (or any
+  // column of a wave without a K unit) loads 16 zero bytes from kZeroLine
+  // instead, for weights and activations alike, so every load is issued
+  // unconditionally and nothing forces an early wait.
+  const uint16_t* const zero16 = reinterpret_cast<const uint16_t*>(kZeroLine);
+
+  // Activation fragments of chunk c (lane holds A[16*mt + r16][k0 + 32u + 8*g4 .. +8]).
+  // Rows m >= M repeat row M-1 and only feed MFMA columns that are never read.
   bf16x8 af[MT][UNITS];
-  auto load_acts = [&](auto full) {
-    constexpr bool FULL = decltype(full)::value;
+  auto load_acts = [&](int c) {
+    // The chunk's first column is laundered so that later chunks' addresses
+    // are computed here, not hoisted out of the tile loop.
+    int kc = kw0 + CW * c;
+    if constexpr (CPW > 1) asm volatile("" : "+v"(kc));
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int64_t roff = (int64_t)min(16 * mt + r16, M - 1) * p.lda;
 #pragma unroll
       for (int u = 0; u < UNITS; ++u) {
-        const int k = k0 + 32 * u + 8 * g4;
-        u32x4 v = ld16(p.A + roff + (FULL ? k : min(k, p.K - 8)));
-        if (!(FULL || (k < p.K && has_chunk))) v = u32x4{0u, 0u, 0u, 0u};
-        af[mt][u] = __builtin_bit_cast(bf16x8, v);
+        const int k = kc + 32 * u + 8 * g4;
+        const uint16_t* src = (has_unit && k < p.K) ? p.A + roff + k : zero16;
+        af[mt][u] = __builtin_bit_cast(bf16x8, ld16(src));
       }
     }
   };
-  if (full_chunk) load_acts(std::true_type{});
-  else load_acts(std::false_type{});
+  load_acts(0);
 
-  // Instruction q of slab (rb, nt): rows 2q + lane/32 of the slab, 8 columns at
-  // k0 + 8*(lane%32) (clamped in bounds; padding meets zero activations).
-  const int lcol = min(k0 + 8 * (lane & 31), p.K - 8);
+  // Instruction q of slab (rb, c, nt): rows 2q + lane/32 of the 16-row group nt,
+  // 8 columns at kw0 + 256c + 8*(lane%32) (rows clamped in bounds).
   const int lrow = lane >> 5;
-  auto wsrc = [&](int rb, int nt, int q) -> const uint16_t* {
+  auto col_of = [&](int c) { return kw0 + CW * c + 8 * (lane & 31); };
+  auto wsrc_col = [&](int rb, int col, int nt, int q) -> const uint16_t* {
     const int t = 2 * q + lrow;
+    if (!(has_unit && col < p.K)) return zero16;
     if constexpr (GATEUP) {
       const int row = min(rb * 16 + t, p.N - 1);
-      return (nt == 0 ? p.W0 : p.W1) + (int64_t)row * p.ldw + lcol;
+      return (nt == 0 ? p.W0 : p.W1) + (int64_t)row * p.ldw + col;
     } else {
       const int row = min(rb * ROWS + 16 * nt + t, p.N - 1);
-      return p.W0 + (int64_t)row * p.ldw + lcol;
+      return p.W0 + (int64_t)row * p.ldw + col;
     }
   };
   char* const wdst = tr + lrow * PITCH + 16 * (lane & 31);
@@ -845,7 +864,7 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   u32x4 ring[RING];
   if (ntiles > 0) {
 #pragma unroll
-    for (int q = 0; q < RING; ++q) ring[q] = ld16_stream(wsrc(rb0, 0, q));
+    for (int q = 0; q < RING; ++q) ring[q] = ld16_stream(wsrc_col(rb0, col_of(0), 0, q));
   }
 
   auto tile = [&](int j, auto last) {
@@ -853,26 +872,41 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
     const int rb = rb0 + j * rbstep;
     f32x4 acc[NT][MT];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const bool wrap = nt + 1 == NT;
-      const int rbn = wrap ? rb + rbstep : rb;
-      const int ntn = wrap ? 0 : nt + 1;
-      // Stage the slab (wave-private region; one wave's LDS accesses execute
-      // in order, so the previous slab's fragment reads are done) and refill.
 #pragma unroll
-      for (int q = 0; q < RING; ++q) {
-        *reinterpret_cast<u32x4*>(wdst + 2 * q * PITCH) = ring[q];
-        if (!(LAST && wrap)) ring[q] = ld16_stream(wsrc(rbn, ntn, q));
-        __builtin_amdgcn_sched_barrier(0);   // keep each refill next to its staging store
+    for (int c = 0; c < CPW; ++c) {
+      if constexpr (CPW > 1) {
+        if (c > 0 || j > 0) load_acts(c);
+        __builtin_amdgcn_sched_barrier(0);   // chunks are scheduled one after another
       }
 #pragma unroll
-      for (int u = 0; u < UNITS; ++u) {
-        const bf16x8 wv = *reinterpret_cast<const bf16x8*>(tr + r16 * PITCH + 64 * u + 16 * g4);
+      for (int nt = 0; nt < NT; ++nt) {
+        const bool last_slab = (c + 1 == CPW) && (nt + 1 == NT);
+        const int rbn = last_slab ? rb + rbstep : rb;
+        const int cn = nt + 1 < NT ? c : (c + 1 < CPW ? c + 1 : 0);
+        const int ntn = nt + 1 < NT ? nt + 1 : 0;
+        // The refill column is recomputed here (an empty asm hides it from
+        // loop-invariant hoisting, which would keep every chunk's addresses
+        // live across the tile loop).
+        int coln = col_of(cn);
+        if constexpr (CPW > 1) asm volatile("" : "+v"(coln));
+        // Stage the slab (wave-private region; one wave's LDS accesses execute
+        // in order, so the previous slab's fragment reads are done) and refill.
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[mt][u], acc[nt][mt], 0, 0, 0);
+        for (int q = 0; q < RING; ++q) {
+          *reinterpret_cast<u32x4*>(wdst + 2 * q * PITCH) = ring[q];
+          if (!(LAST && last_slab)) ring[q] = ld16_stream(wsrc_col(rbn, coln, ntn, q));
+          __builtin_amdgcn_sched_barrier(0);   // keep each refill next to its staging store
+        }
+#pragma unroll
+        for (int u = 0; u < UNITS; ++u) {
+          const bf16x8 wv = *reinterpret_cast<const bf16x8*>(tr + r16 * PITCH + 64 * u + 16 * g4);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[mt][u], acc[nt][mt], 0, 0, 0);
+        }
       }
     }
     float* P = parts + (j & 1) * part_floats;
@@ -883,6 +917,8 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
         const int m = 16 * mt + r16;
         if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
       }
+    // The barrier keeps the waves of a workgroup on the same tile rows
+    // (measured faster than deferring every reduction to the end).
     lds_barrier();
     tile_reduce<ROWS, BASE>(p, P, nw, rb, j, stage, lds_best);
   };
@@ -902,8 +938,8 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
 
 template <int MT, int NT, int KW, int EPI>
 __device__ __forceinline__ void mfmt_body(Args p) {
-  if constexpr (KW == 256) mfmt_ring_body<MT, NT, EPI>(p);
-  else mfmt_tile_body<MT, NT, KW, EPI>(p);
+  if constexpr (KW == 512) mfmt_tile_body<MT, NT, KW, EPI>(p);
+  else mfmt_ring_body<MT, NT, KW / 256, EPI>(p);
 }
 
 // ---------------------------------------------------------------------------

@@ -30,18 +30,22 @@ constexpr int norm_extra(int act_regs, int weight_regs, int unit_regs) {
 constexpr int gemv_regs(int MR, int RR, int KU, bool norm = false) {
   return 4 * KU * (MR + RR) + RR * MR + 24 + (norm ? norm_extra(4 * KU * MR, 4 * KU * RR, 4 * KU) : 0);
 }
-// LDS-transposed MFMA: KW/32 activation units per tile row block plus the
-// weight rows in flight: a whole tile (16*NT rows of KW/512 rows per load
-// instruction) for KW = 512, an 8-instruction ring for KW = 256.
+// LDS-transposed MFMA.  KW = 512: one chunk's activation units plus a whole
+// tile of weight rows in flight (16*NT rows, one row per load instruction).
+// Otherwise (ring, KW = 256 * chunks per wave): one 256-column chunk's
+// activation units plus an 8-instruction ring.
 constexpr int mfmt_regs(int MT, int NT, int KW) {
-  return 4 * (KW / 32) * MT + (KW == 256 ? 4 * 8 : 4 * (16 * NT * KW / 512)) + 4 * NT * MT + 32;
+  return KW == 512 ? 4 * 16 * MT + 4 * 16 * NT + 4 * NT * MT + 32 : 4 * 8 * MT + 4 * 8 + 4 * NT * MT + 32;
 }
+
 // Waves per workgroup an instance is compiled for (its __launch_bounds__):
 // 16 waves leave 128 VGPRs per lane, 8 waves 256; norm-prologue instances
 // also have a 12-wave tier (168 VGPRs).
 constexpr int max_waves_for_regs(int regs, bool norm = false) {
   return regs <= 128 ? 16 : (norm && regs <= 168 ? 12 : (regs <= 256 ? 8 : 4));
 }
+// Waves per workgroup an LDS-fed MFMA instance is compiled for.
+constexpr int mfmt_max_waves(int MT, int NT, int KW) { return max_waves_for_regs(mfmt_regs(MT, NT, KW)); }
 
 KernelFn mfma_for_epi0(int MT, int NT, int KU);
 KernelFn mfma_for_epi1(int MT, int NT, int KU);

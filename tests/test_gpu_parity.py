@@ -411,11 +411,15 @@ def test_workspace_counters_reset_between_calls():
         assert torch.equal(ids.cpu(), torch.argmax(L.cpu(), -1))
 
 
-MFMT_CASES = {  # shape, K-chunk units (16: 512 columns, 8: 256), rows, global split
+MFMT_CASES = {  # shape, 32-column units per wave (8: 256, 16: 512, 32: 1024), rows, global split
     "qkv": (QKV, 16, 16, 1),
     "o_proj": (O, 16, 16, 1),
     "down": (D, 16, 16, 3),
     "qkv_kw256_rows32": (QKV, 8, 32, 2),
+    # four 256-column chunks per wave: down's last wave covers 1.5 chunks past K
+    "down_kw1024": (D, 32, 16, 1),
+    "down_kw1024_rows32": (D, 32, 32, 1),
+    "o_proj_kw1024_split2": (O, 32, 16, 2),
 }
 
 
@@ -440,6 +444,20 @@ def test_mfma_lds_path_qwen_shapes(case, M):
     x = _acts(M, Kd, seed=N)
     out = K.gemm(x.to(DEV), _gpu(w), config=cfg)
     assert_parity(out, _oracle_gemm(x, w), f"mfma_lds {case} M={M} {cfg}")
+
+
+@pytest.mark.parametrize("Kd", [2592, 1056, 4096 + 288])
+@pytest.mark.parametrize("M", [3, 16])
+def test_mfma_lds_multi_chunk_ragged_k(Kd, M):
+    """Waves of four 256-column chunks where K ends inside a chunk (per-lane
+    zero columns) and inside a wave (chunks past K load zeros)."""
+    N = 200
+    units = -(-Kd // 1024)
+    cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=units, ku=32, rows=16, split=1)
+    w = _weights(N, Kd, seed=Kd)
+    x = _acts(M, Kd, seed=Kd + 1)
+    out = K.gemm(x.to(DEV), _gpu(w), config=cfg)
+    assert_parity(out, _oracle_gemm(x, w), f"mfma_lds ragged K={Kd} M={M} {cfg}")
 
 
 @pytest.mark.parametrize("M", [1, 8, 40])
