@@ -216,11 +216,13 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
       vv[j] = ld16(a.v + (kv_row0 + kv) * HEAD_D + 8 * dg);
     }
   };
-  u32x4 kf[HEAD_D / 32], vv[4];
-  if (start < end) load_block(start, kf, vv);
-  for (int n0 = start; n0 < end; n0 += step) {
-    u32x4 kn[HEAD_D / 32], vn[4];
-    load_block(n0 + step, kn, vn);
+  // Two blocks in flight beyond the one being processed.  Three buffers with
+  // fixed roles rotate through a three-block loop body with a single exit,
+  // so no buffer is ever copied (a loop-carried copy makes the compiler wait
+  // for the prefetched loads at the end of every iteration).  Blocks past
+  // `end` in the last iteration are fully masked; their loads read the last
+  // valid row (one cached line).
+  auto process = [&](int n0, const u32x4* kf, const u32x4* vv) {
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < HEAD_D / 32; ++st)
@@ -275,10 +277,26 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
       l[r] = lsum;
       m[r] = mx;
     }
-#pragma unroll
-    for (int st = 0; st < HEAD_D / 32; ++st) kf[st] = kn[st];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vv[j] = vn[j];
+  };
+  u32x4 kA[HEAD_D / 32], vA[4], kB[HEAD_D / 32], vB[4], kC[HEAD_D / 32], vC[4];
+  if (start < end) {
+    load_block(start, kA, vA);
+    load_block(start + step, kB, vB);
+  }
+  // The scheduling fences keep every prefetch ahead of the block it overlaps.
+  for (int n0 = start; n0 < end; n0 += 3 * step) {
+    load_block(n0 + 2 * step, kC, vC);
+    __builtin_amdgcn_sched_barrier(0);
+    process(n0, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    load_block(n0 + 3 * step, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    process(n0 + step, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    load_block(n0 + 4 * step, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    process(n0 + 2 * step, kC, vC);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // Merge the 4 lane-group streams of each wave (lanes l, l^16, l^32, l^48
