@@ -60,7 +60,12 @@ typedef enum sk_op {
   SK_OP_ARGMAX = 3,       /* ids/maxv = argmax over given bf16 logits     */
   SK_OP_RMSNORM_GEMM = 4,       /* SK_OP_GEMM with A = rmsnorm(x + y)      */
   SK_OP_RMSNORM_GATEUP = 5,     /* SK_OP_GATEUP with A = rmsnorm(x + y)    */
-  SK_OP_RMSNORM_LM_ARGMAX = 6   /* SK_OP_LM_ARGMAX with A = rmsnorm(x + y) */
+  SK_OP_RMSNORM_LM_ARGMAX = 6,  /* SK_OP_LM_ARGMAX with A = rmsnorm(x + y) */
+  /* Residual hand-off (a decode step split across kernel boundaries):      */
+  SK_OP_RESID_GEMM = 7,         /* r_out = bf16(r + bf16(A @ W^T)), + sums  */
+  SK_OP_PRE_GEMM = 8,           /* SK_OP_GEMM on rmsnorm(x) from the sums   */
+  SK_OP_PRE_GATEUP = 9,         /* SK_OP_GATEUP on rmsnorm(x) from the sums */
+  SK_OP_PRE_LM_ARGMAX = 10      /* SK_OP_LM_ARGMAX on rmsnorm(x) from sums  */
 } sk_op;
 
 typedef enum sk_path {
@@ -80,7 +85,8 @@ typedef enum sk_path {
  *   waves  : wavefronts per workgroup; they split the workgroup's K slice and
  *            their fp32 partials are summed in LDS in fixed wave order
  *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns;
- *            MFMA_LDS: 16 or 8, i.e. one 512- or 256-column chunk per wave)
+ *            MFMA_LDS: 8, 16 or 32, i.e. 256, 512 or 1024 columns per wave;
+ *            256 and 1024 stream 256-column chunks through an 8-load ring)
  *   rows   : weight rows per workgroup tile (MFMA: 16 or 32; GEMV: 1..8)
  *   split  : global K splits; >1 writes fp32 partials to the workspace and
  *            the last workgroup to finish a tile sums them in fixed split
@@ -193,6 +199,55 @@ int sk_rmsnorm_gateup_swiglu_bf16(const sk_bf16* x, const sk_bf16* y, const sk_b
 int sk_rmsnorm_lm_argmax_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16* w_norm, float eps, sk_bf16* xout,
                               int64_t ldx, const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M, int V,
                               int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* Residual hand-off: the residual add and RMSNorm that sit between two
+ * projections of a decoder layer (engine/model.py:202-210: xa = x + y before
+ * mm["qkv"], xb = xa + o before mm["gu"], and the final norm before mm["lm"])
+ * are split across the producing and the consuming projection kernels, so no
+ * separate norm kernel runs between them.  No counterpart in the reference's
+ * operator API (its prologue, gemm.py:28-56, recomputes every row's norm in
+ * every tile); results follow the same casts:
+ *
+ * sk_gemm_residual_bf16 (producer, e.g. o_proj / down):
+ *   y = bf16(A @ W^T) as sk_gemm_bf16 (not stored);
+ *   r_out[m, n] = bf16(r[m, n] + y[m, n])            (bit-exact, the xout of
+ *                                                      the reference prologue)
+ *   sq[m * sq_ld + g] = sum of r_out[m, n]^2 over n in [16g, 16g+16) (fp32,
+ *                       fixed order), sq_ld = ceil(N / 16).
+ *   r and r_out are [M, N] with row stride ldr (r_out may equal r; neither may
+ *   overlap A).  Query the workspace with SK_OP_RESID_GEMM.
+ *
+ * sk_rmsnorm_pre_{gemm,gateup_swiglu,lm_argmax}_bf16 (consumer):
+ *   rstd[m] = 1/sqrt(sum_g sq[m * (K/16) + g] / K + eps)   (fixed order)
+ *   A = bf16(w_norm * bf16(x * rstd))   with x = the producer's r_out
+ *   then the projection of A as sk_gemm_bf16 / sk_gateup_swiglu_bf16 /
+ *   sk_lm_argmax_bf16.  rstd may differ from a sequential sum's in the last
+ *   fp32 bit, which can move rare elements of A by one bf16 ulp (within the
+ *   projections' tolerance).  K must be a multiple of 16; the outputs must not
+ *   overlap x or sq.  Query the workspace with SK_OP_PRE_* ops.
+ *
+ * Both run on the ring-streamed LDS-fed MFMA path (a configuration with
+ * path 3 and ku 8, or ku 8 / 32 with any split for the producer); cfg NULL or
+ * path AUTO picks the tuned configuration when it is such a path, else the
+ * first ring configuration that fits.  M <= 64; a consumer holds all of K in
+ * one workgroup (16 waves of 256 columns at M <= 16, 8 above), so shapes with
+ * no such configuration return SK_ERR_CONFIG. */
+int sk_gemm_residual_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, const sk_bf16* r,
+                          sk_bf16* r_out, int64_t ldr, float* sq, int M, int N, int K, const sk_config* cfg, void* ws,
+                          size_t ws_bytes, hipStream_t stream);
+
+int sk_rmsnorm_pre_gemm_bf16(const sk_bf16* x, int64_t ldx, const float* sq, const sk_bf16* w_norm, float eps,
+                             const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N, int K,
+                             const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+int sk_rmsnorm_pre_gateup_swiglu_bf16(const sk_bf16* x, int64_t ldx, const float* sq, const sk_bf16* w_norm,
+                                      float eps, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw, sk_bf16* Out,
+                                      int64_t ldo, int M, int I, int K, const sk_config* cfg, void* ws,
+                                      size_t ws_bytes, hipStream_t stream);
+
+int sk_rmsnorm_pre_lm_argmax_bf16(const sk_bf16* x, int64_t ldx, const float* sq, const sk_bf16* w_norm, float eps,
+                                  const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M, int V, int K,
+                                  const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
 
 /*
  * Attention side of the decode step (head width D = 128 only).

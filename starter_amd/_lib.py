@@ -31,6 +31,10 @@ SK_OP_ARGMAX = 3
 SK_OP_RMSNORM_GEMM = 4
 SK_OP_RMSNORM_GATEUP = 5
 SK_OP_RMSNORM_LM_ARGMAX = 6
+SK_OP_RESID_GEMM = 7
+SK_OP_PRE_GEMM = 8
+SK_OP_PRE_GATEUP = 9
+SK_OP_PRE_LM_ARGMAX = 10
 
 SK_PATH_AUTO = 0
 SK_PATH_MFMA = 1
@@ -43,6 +47,8 @@ EXPORTS = (
     "sk_gemm_bf16", "sk_gateup_swiglu_bf16", "sk_lm_argmax_bf16", "sk_argmax_bf16",
     "sk_add_rmsnorm_bf16", "sk_swiglu_bf16",
     "sk_rmsnorm_gemm_bf16", "sk_rmsnorm_gateup_swiglu_bf16", "sk_rmsnorm_lm_argmax_bf16",
+    "sk_gemm_residual_bf16", "sk_rmsnorm_pre_gemm_bf16", "sk_rmsnorm_pre_gateup_swiglu_bf16",
+    "sk_rmsnorm_pre_lm_argmax_bf16",
     "sk_qk_norm_rope_cache_bf16", "sk_decode_attention_workspace_bytes", "sk_decode_attention_bf16",
     "sk_topk_bf16",
 )
@@ -107,6 +113,13 @@ _SIGNATURES = {
                                              _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
     "sk_rmsnorm_lm_argmax_bf16": (_i32, [_p, _p, _p, ctypes.c_float, _p, _i64,
                                          _p, _i64, _p, _p, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
+    "sk_gemm_residual_bf16": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
+    "sk_rmsnorm_pre_gemm_bf16": (_i32, [_p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p, _i64, _i32, _i32, _i32,
+                                        _cfgp, _p, _sz, _p]),
+    "sk_rmsnorm_pre_gateup_swiglu_bf16": (_i32, [_p, _i64, _p, _p, ctypes.c_float, _p, _p, _i64, _p, _i64, _i32,
+                                                 _i32, _i32, _cfgp, _p, _sz, _p]),
+    "sk_rmsnorm_pre_lm_argmax_bf16": (_i32, [_p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p, _p, _i32, _i32, _i32,
+                                             _cfgp, _p, _sz, _p]),
     "sk_qk_norm_rope_cache_bf16": (_i32, [_p, _i64, _p, _p, _p, _p, _i32, _p, _p, _p, _p,
                                           _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p]),
     "sk_decode_attention_workspace_bytes": (_sz, [_i32] * 8),

@@ -124,8 +124,15 @@ int base_op(int op) { return is_norm_op(op) ? op - SK_OP_RMSNORM_GEMM : op; }
 bool is_gemm_family(int op) { return op == SK_OP_GEMM || op == SK_OP_GATEUP || op == SK_OP_LM_ARGMAX; }
 
 // The epilogue proper of an instance's epilogue id (the norm-prologue ids
-// 5..7 share the layout of 0..2).
-int epi_base(int epi) { return epi >= sk::EPI_STORE_NORM ? epi - sk::EPI_STORE_NORM : epi; }
+// 5..7 and the residual hand-off consumers 8..10 share the layout of 0..2;
+// the hand-off producers 11 and 12 that of STORE and PART).
+int epi_base(int epi) {
+  if (epi >= sk::EPI_STORE_NORM && epi <= sk::EPI_ARGMAX_NORM) return epi - sk::EPI_STORE_NORM;
+  if (epi >= sk::EPI_STORE_PRE && epi <= sk::EPI_ARGMAX_PRE) return epi - sk::EPI_STORE_PRE;
+  if (epi == sk::EPI_STORE_RESID) return sk::EPI_STORE;
+  if (epi == sk::EPI_PART_RESID) return sk::EPI_PART;
+  return epi;
+}
 
 // Staged output bytes per element of each epilogue (see EpiTraits).
 size_t stage_bytes(int epi) {
@@ -158,15 +165,27 @@ int epi_for(int op, int split) {
 // Pure host logic: fills everything except fn/grid-from-occupancy.  op is a
 // projection (GEMM / GATEUP / LM_ARGMAX); `fused` selects the instances with
 // the norm prologue.
-int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused, Plan* pl) {
+// variant: 0 plain, 1 residual hand-off consumer (EPI_*_PRE), 2 producer
+// (EPI_*_RESID); both run on the ring-streamed LDS-fed MFMA path only.
+int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused, Plan* pl, int variant = 0) {
   if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   if (M < 1 || M > kMaxM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
   if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0) return SK_ERR_CONFIG;
   if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
   const bool gateup = (op == SK_OP_GATEUP);
   if (fused && (c.split != 1 || c.path != SK_PATH_GEMV)) return SK_ERR_CONFIG;
+  if (variant != 0) {
+    if (fused || c.path != SK_PATH_MFMA_LDS || c.ku == 16) return SK_ERR_CONFIG;
+    // consumers: one K split; the prologue loads each wave's share of the
+    // partial sums in one pass (rows <= 4 per wave, <= 256 groups per row)
+    if (variant == 1 && (c.ku != 8 || c.split != 1 || (K & 15) != 0 || M > 4 * c.waves || K > 4096))
+      return SK_ERR_CONFIG;
+    if (variant == 2 && op != SK_OP_GEMM) return SK_ERR_CONFIG;
+  }
   pl->cfg = c;
   pl->epi = epi_for(op, c.split) + (fused ? sk::EPI_STORE_NORM : 0);
+  if (variant == 1) pl->epi = epi_for(op, c.split) + sk::EPI_STORE_PRE;
+  if (variant == 2) pl->epi = c.split > 1 ? sk::EPI_PART_RESID : sk::EPI_STORE_RESID;
   pl->fused = fused;
   int units, partial_rows;
   if (c.path == SK_PATH_MFMA) {
@@ -672,6 +691,155 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
   return SK_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Residual hand-off ops (SK_OP_RESID_GEMM, SK_OP_PRE_*).
+// ---------------------------------------------------------------------------
+bool is_handoff_op(int op) { return op >= SK_OP_RESID_GEMM && op <= SK_OP_PRE_LM_ARGMAX; }
+int handoff_base(int op) {
+  return op == SK_OP_PRE_GATEUP ? SK_OP_GATEUP : (op == SK_OP_PRE_LM_ARGMAX ? SK_OP_LM_ARGMAX : SK_OP_GEMM);
+}
+int handoff_variant(int op) { return op == SK_OP_RESID_GEMM ? 2 : 1; }
+
+// Configuration of a hand-off op: the explicit one, else the projection's
+// tuned one when it is a supported ring configuration, else a ring one with
+// one 256-column chunk per wave (four for a producer whose K needs more than
+// 16 waves), one K split.
+int handoff_config(int op, int M, int N, int K, const sk_config* cfg, sk_config* out) {
+  const int bop = handoff_base(op), variant = handoff_variant(op);
+  Plan pl;
+  if (cfg && cfg->path != SK_PATH_AUTO) {
+    *out = *cfg;
+    return SK_OK;
+  }
+  sk_config d;
+  if (default_config(bop, M, N, K, 0, &d) == SK_OK && plan_shape_impl(bop, M, N, K, d, false, &pl, variant) == SK_OK) {
+    *out = d;
+    return SK_OK;
+  }
+  // Ring candidates in order: one K split with 256-column chunks, then (the
+  // producer only) four chunks per wave, then global K splits.
+  for (int ku : {8, 32}) {
+    if (ku == 32 && variant == 1) continue;
+    for (int split = 1; split <= (variant == 2 ? 4 : 1); ++split) {
+      memset(&d, 0, sizeof(d));
+      d.path = SK_PATH_MFMA_LDS;
+      d.rows = 16;
+      d.ku = ku;
+      d.split = split;
+      const int units = (K + 32 * ku - 1) / (32 * ku);
+      d.waves = (units + split - 1) / split;
+      if (d.waves <= 16 && plan_shape_impl(bop, M, N, K, d, false, &pl, variant) == SK_OK) {
+        *out = d;
+        return SK_OK;
+      }
+    }
+  }
+  return SK_ERR_CONFIG;
+}
+
+int plan_handoff(int op, int M, int N, int K, const sk_config* cfg, Plan* pl) {
+  if (M < 1 || M > kMaxM || N < 1 || K < 32) return SK_ERR_SHAPE;
+  sk_config c;
+  int st = handoff_config(op, M, N, K, cfg, &c);
+  if (st) return st;
+  return plan_shape_impl(handoff_base(op), M, N, K, c, false, pl, handoff_variant(op));
+}
+
+size_t handoff_workspace(int op, int M, int N, int K, const sk_config* cfg) {
+  Plan pl;
+  if (plan_handoff(op, M, N, K, cfg, &pl)) return 0;
+  return plan_workspace(handoff_base(op), M, N, pl);
+}
+
+struct Handoff {
+  const sk_bf16* r;     // producer: residual in
+  sk_bf16* r_out;       // producer: residual out
+  int64_t ldr;
+  float* sq;            // producer: partial sums out / consumer: in
+  const sk_bf16* w;     // consumer: norm weights
+  float eps;
+};
+
+int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const sk_bf16* W0, const sk_bf16* W1,
+                int64_t ldw, sk_bf16* C, int64_t ldc, int64_t* ids, float* maxv, int M, int N, int K,
+                const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  const int bop = handoff_base(op);
+  const bool resid = handoff_variant(op) == 2;
+  if (M < 0 || N < 1 || K < 32 || M > kMaxM) return SK_ERR_SHAPE;
+  if (M == 0) return SK_OK;
+  if (!A || !W0 || (bop == SK_OP_GATEUP && !W1) || !h.sq) return SK_ERR_NULL;
+  if (resid ? (!h.r || !h.r_out) : !h.w) return SK_ERR_NULL;
+  if (!resid && (bop == SK_OP_LM_ARGMAX ? (!ids || !maxv) : !C)) return SK_ERR_NULL;
+  if ((K & 31) != 0 || lda < K || ldw < K) return SK_ERR_SHAPE;
+  if (!resid && bop != SK_OP_LM_ARGMAX && ldc < N) return SK_ERR_SHAPE;
+  if (resid && h.ldr < N) return SK_ERR_SHAPE;
+  if (!aligned16(A) || !aligned16(W0) || (W1 && !aligned16(W1)) || (lda & 7) || (ldw & 7)) return SK_ERR_ALIGN;
+  if (!resid && (!aligned16(h.w) || (reinterpret_cast<uintptr_t>(h.sq) & 3))) return SK_ERR_ALIGN;
+  if (resid && ((reinterpret_cast<uintptr_t>(h.r) | reinterpret_cast<uintptr_t>(h.r_out)) & 1)) return SK_ERR_ALIGN;
+  const int sq_ld = resid ? (N + 15) / 16 : K / 16;
+  const size_t a_bytes = ((size_t)(M - 1) * lda + K) * sizeof(sk_bf16);
+  const size_t sq_bytes = (size_t)M * sq_ld * sizeof(float);
+  if (resid) {
+    const size_t r_bytes = ((size_t)(M - 1) * h.ldr + N) * sizeof(sk_bf16);
+    // r_out may equal r (each element is read and written by one thread), but
+    // no output may overlap the projection's input or the other output.
+    if (overlaps(h.r_out, r_bytes, A, a_bytes) || overlaps(h.sq, sq_bytes, A, a_bytes) ||
+        overlaps(h.sq, sq_bytes, h.r_out, r_bytes) || overlaps(h.sq, sq_bytes, h.r, r_bytes))
+      return SK_ERR_ALIAS;
+    if (h.r != h.r_out && overlaps(h.r_out, r_bytes, h.r, r_bytes)) return SK_ERR_ALIAS;
+  } else if (bop != SK_OP_LM_ARGMAX) {
+    const size_t c_bytes = ((size_t)(M - 1) * ldc + N) * sizeof(sk_bf16);
+    if (overlaps(C, c_bytes, A, a_bytes) || overlaps(C, c_bytes, h.sq, sq_bytes)) return SK_ERR_ALIAS;
+  }
+  Plan pl;
+  int st = plan_handoff(op, M, N, K, cfg, &pl);
+  if (st) return st;
+  const size_t need = plan_workspace(bop, M, N, pl);
+  if (need > 0 && (!ws || ws_bytes < need)) return SK_ERR_WORKSPACE;
+  int num_cu = 0;
+  if ((st = device_info(&num_cu))) return st;
+  int grid = 0;
+  if ((st = bind_plan(&pl, num_cu, &grid))) return st;
+  sk::Args a;
+  memset(&a, 0, sizeof(a));
+  a.A = A;
+  a.W0 = W0;
+  a.W1 = W1;
+  a.C = C;
+  if (ws) {
+    const size_t tb = ticket_bytes(bop == SK_OP_LM_ARGMAX ? 1 : pl.nrb);
+    a.tickets = static_cast<unsigned*>(ws);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + tb);
+    a.best = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + tb);
+  }
+  if (bop == SK_OP_LM_ARGMAX) {
+    a.C = reinterpret_cast<sk_bf16*>(ids);
+    a.part = maxv;
+  }
+  a.R = h.r;
+  a.RO = h.r_out;
+  a.ldr = h.ldr;
+  a.SQ = h.sq;
+  a.sq_ld = sq_ld;
+  a.NW = h.w;
+  a.eps = h.eps;
+  a.lda = lda;
+  a.ldw = ldw;
+  a.ldc = ldc;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.S = pl.cfg.split;
+  a.slice_units = pl.slice_units;
+  a.ku = pl.cfg.ku;
+  a.nrb = pl.nrb;
+  a.nw = pl.cfg.waves;
+  a.grid = grid;
+  a.rbstep = grid / pl.cfg.split;
+  pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
+  return launch_status();
+}
+
 }  // namespace
 
 extern "C" {
@@ -695,12 +863,17 @@ const char* sk_strerror(int status) {
 
 int sk_default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   if (!out) return SK_ERR_NULL;
+  if (is_handoff_op(op)) return handoff_config(op, M > kMaxM ? kMaxM : M, N, K, nullptr, out);
   if (!is_gemm_family(base_op(op))) return SK_ERR_CONFIG;
   return default_config(op, M, N, K, num_cu, out);
 }
 
 int sk_check_config(int op, int M, int N, int K, const sk_config* cfg) {
   if (!cfg) return SK_ERR_NULL;
+  if (is_handoff_op(op)) {
+    Plan pl;
+    return plan_handoff(op, M, N, K, cfg, &pl);
+  }
   sk_config c;
   int st = resolve_config(op, M > kMaxM ? kMaxM : M, N, K, cfg, &c);
   if (st) return st;
@@ -709,6 +882,7 @@ int sk_check_config(int op, int M, int N, int K, const sk_config* cfg) {
 }
 
 size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg) {
+  if (is_handoff_op(op)) return M < 1 ? 0 : handoff_workspace(op, M, N, K, cfg);
   if (op == SK_OP_ARGMAX) {
     if (M < 1 || N < 1) return 0;
     return ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
@@ -819,6 +993,40 @@ int sk_swiglu_bf16(const sk_bf16* gu, int64_t ld_gu, sk_bf16* out, int64_t ld_ou
   if (g > 8L * num_cu * 8) g = 8L * num_cu * 8;
   sk::swiglu_kernel<<<dim3((unsigned)g), dim3(256), 0, stream>>>(gu, ld_gu, out, ld_out, M, I);
   return launch_status();
+}
+
+
+int sk_gemm_residual_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, const sk_bf16* r,
+                          sk_bf16* r_out, int64_t ldr, float* sq, int M, int N, int K, const sk_config* cfg, void* ws,
+                          size_t ws_bytes, hipStream_t stream) {
+  Handoff h{r, r_out, ldr, sq, nullptr, 0.f};
+  return run_handoff(SK_OP_RESID_GEMM, A, lda, h, W, nullptr, ldw, nullptr, 0, nullptr, nullptr, M, N, K, cfg, ws,
+                     ws_bytes, stream);
+}
+
+int sk_rmsnorm_pre_gemm_bf16(const sk_bf16* x, int64_t ldx, const float* sq, const sk_bf16* w_norm, float eps,
+                             const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc, int M, int N, int K,
+                             const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  Handoff h{nullptr, nullptr, 0, const_cast<float*>(sq), w_norm, eps};
+  return run_handoff(SK_OP_PRE_GEMM, x, ldx, h, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, ws, ws_bytes,
+                     stream);
+}
+
+int sk_rmsnorm_pre_gateup_swiglu_bf16(const sk_bf16* x, int64_t ldx, const float* sq, const sk_bf16* w_norm,
+                                      float eps, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw, sk_bf16* Out,
+                                      int64_t ldo, int M, int I, int K, const sk_config* cfg, void* ws,
+                                      size_t ws_bytes, hipStream_t stream) {
+  Handoff h{nullptr, nullptr, 0, const_cast<float*>(sq), w_norm, eps};
+  return run_handoff(SK_OP_PRE_GATEUP, x, ldx, h, Wg, Wu, ldw, Out, ldo, nullptr, nullptr, M, I, K, cfg, ws,
+                     ws_bytes, stream);
+}
+
+int sk_rmsnorm_pre_lm_argmax_bf16(const sk_bf16* x, int64_t ldx, const float* sq, const sk_bf16* w_norm, float eps,
+                                  const sk_bf16* W, int64_t ldw, int64_t* ids, float* maxv, int M, int V, int K,
+                                  const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+  Handoff h{nullptr, nullptr, 0, const_cast<float*>(sq), w_norm, eps};
+  return run_handoff(SK_OP_PRE_LM_ARGMAX, x, ldx, h, W, nullptr, ldw, nullptr, 0, ids, maxv, M, V, K, cfg, ws,
+                     ws_bytes, stream);
 }
 
 }  // extern "C"

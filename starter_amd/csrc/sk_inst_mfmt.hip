@@ -1,4 +1,4 @@
-// LDS-transposed MFMA kernel instances for one epilogue (-DSK_EPI=<0..4>).
+// LDS-transposed MFMA kernel instances for one epilogue (-DSK_EPI=<0..4, 8..12>).
 #include "sk_registry.hpp"
 
 #ifndef SK_EPI
@@ -22,9 +22,23 @@ mfmt_entry(Args p) {
   SK_C(1, NT, 512) SK_C(2, NT, 512) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(3, NT, 256) SK_C(4, NT, 256) \
   SK_C(1, NT, 1024) SK_C(2, NT, 1024)
 
+// Residual hand-off epilogues exist on the ring path only: the consumers
+// (EPI 8-10) with one 256-column chunk per wave, the producers (EPI 11-12)
+// with one or four.
+#define SK_PRE_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256)
+#define SK_RESID_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(1, NT, 1024) SK_C(2, NT, 1024)
+
 KernelFn SK_CAT(mfmt_for_epi, SK_EPI)(int MT, int NT, int KW) {
   switch (MT * 100000 + NT * 1000 + KW) {
-#if SK_EPI == 1 || SK_EPI == 4   // gate/up: 16 gate rows + 16 up rows
+#if SK_EPI == 9   // gate/up consumer
+    SK_PRE_LIST(2)
+#elif SK_EPI == 8 || SK_EPI == 10
+    SK_PRE_LIST(1)
+    SK_PRE_LIST(2)
+#elif SK_EPI == 11 || SK_EPI == 12
+    SK_RESID_LIST(1)
+    SK_RESID_LIST(2)
+#elif SK_EPI == 1 || SK_EPI == 4   // gate/up: 16 gate rows + 16 up rows
     SK_LIST(2)
 #else
     SK_LIST(1)

@@ -53,7 +53,19 @@ enum Epi : int {
   // the activation rows as they are loaded (one global K split only).
   EPI_STORE_NORM = 5,
   EPI_SWIGLU_NORM = 6,
-  EPI_ARGMAX_NORM = 7
+  EPI_ARGMAX_NORM = 7,
+  // The first three again, consuming activations the producer of the previous
+  // projection already summed (x + y, kept as the residual) and whose per-row
+  // sums of squares it left as partials over 16-column groups: the RMSNorm is
+  // finished here from those partials (LDS-fed MFMA ring path only).
+  EPI_STORE_PRE = 8,
+  EPI_SWIGLU_PRE = 9,
+  EPI_ARGMAX_PRE = 10,
+  // Plain projection (one K split, or split-K partials) whose output y is not
+  // stored: the residual xout = bf16(r + bf16(y)) is, with the sums of
+  // squares of each 16-column group of xout (the next norm's partials).
+  EPI_STORE_RESID = 11,
+  EPI_PART_RESID = 12
 };
 
 // Kernel arguments, passed by value (one struct keeps the launch ABI simple).
@@ -81,6 +93,15 @@ struct Args {
   const uint16_t* NW;
   uint16_t* XO;
   float eps;
+  // Residual hand-off (EPI_*_PRE consume, EPI_*_RESID produce): R residual in,
+  // RO residual out (row stride ldr), SQ per-row partial sums of squares over
+  // 16-column groups of RO, row stride sq_ld floats.  The PRE epilogues read
+  // SQ and the norm weights NW with eps; their K is the producer's N.
+  const uint16_t* R;
+  uint16_t* RO;
+  int64_t ldr;
+  float* SQ;
+  int sq_ld;
 };
 
 // ---------------------------------------------------------------------------
@@ -243,8 +264,14 @@ __device__ __forceinline__ u32x4 norm_bf16x8(u32x4 s, u32x4 w, float rstd) {
 // ---------------------------------------------------------------------------
 template <int EPI>
 struct EpiTraits {
-  static constexpr bool norm = EPI >= EPI_STORE_NORM;
-  static constexpr int base = norm ? EPI - EPI_STORE_NORM : EPI;   // the epilogue proper
+  static constexpr bool norm = EPI >= EPI_STORE_NORM && EPI <= EPI_ARGMAX_NORM;
+  static constexpr bool pre = EPI >= EPI_STORE_PRE && EPI <= EPI_ARGMAX_PRE;
+  static constexpr bool resid = EPI == EPI_STORE_RESID || EPI == EPI_PART_RESID;
+  static constexpr int base = norm  ? EPI - EPI_STORE_NORM   // the epilogue proper
+                              : pre ? EPI - EPI_STORE_PRE
+                              : EPI == EPI_STORE_RESID ? EPI_STORE
+                              : EPI == EPI_PART_RESID  ? EPI_PART
+                                                       : EPI;
   static constexpr bool gateup = (base == EPI_SWIGLU || base == EPI_PART_GU);
   // bytes per staged output element (PART_GU stages gate and up fp32 sums)
   static constexpr int stage_bytes = base == EPI_STORE || base == EPI_SWIGLU ? 2 : (base == EPI_PART ? 4 : 8);
@@ -317,15 +344,39 @@ __device__ __forceinline__ float load_agent(const float* p) {
 
 // Write the staged outputs of this workgroup's tiles (after the stream).
 // Split-K partials are stored device-coherent for the fixup below.
-template <int OUT_ROWS, int EPI>
+// Residual hand-off for output element (m, n) with bf16 projection value yb:
+// xout = bf16(r + y) goes to RO and the sum of xout^2 over each 16-column
+// group (the 16 consecutive lanes that hold it, added in a fixed butterfly
+// order) goes to SQ[m][n / 16].  Every lane of the group must call this;
+// ok = false (a column past N) contributes zero and stores nothing.
+__device__ __forceinline__ void resid_out(const Args& p, int m, int n, bool ok, uint16_t yb) {
+  const float xo = ok ? round_bf(bf2f(p.R[(int64_t)m * p.ldr + n]) + bf2f(yb)) : 0.f;
+  if (ok) p.RO[(int64_t)m * p.ldr + n] = f2bf(xo);
+  float sq = xo * xo;
+  sq += __shfl_xor(sq, 1);
+  sq += __shfl_xor(sq, 2);
+  sq += __shfl_xor(sq, 4);
+  sq += __shfl_xor(sq, 8);
+  if ((n & 15) == 0 && ok) p.SQ[(int64_t)m * p.sq_ld + (n >> 4)] = sq;
+}
+
+template <int OUT_ROWS, int EPI, bool RESID = false>
 __device__ __forceinline__ void flush_stage(const Args& p, const void* stage, int ntiles, int rb0, int slice) {
+  static_assert(!RESID || OUT_ROWS % 16 == 0, "16-column groups of one tile");
   const int M = p.M;
   const int total = ntiles * M * OUT_ROWS;
+  // Consecutive idx hold consecutive columns of one (tile, row): with OUT_ROWS
+  // a multiple of 16, each 16-column group is 16 consecutive lanes of a wave.
   for (int idx = threadIdx.x; idx < total; idx += 64 * p.nw) {
     const int r = idx % OUT_ROWS;
     const int jm = idx / OUT_ROWS;
     const int m = jm % M, j = jm / M;
     const int n = (rb0 + j * p.rbstep) * OUT_ROWS + r;
+    if constexpr (RESID) {
+      static_assert(EPI == EPI_STORE, "the residual follows a finished projection");
+      resid_out(p, m, n, n < p.N, static_cast<const uint16_t*>(stage)[idx]);
+      continue;
+    }
     if (n >= p.N) continue;
     if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
       p.C[(int64_t)m * p.ldc + n] = static_cast<const uint16_t*>(stage)[idx];
@@ -354,7 +405,7 @@ __device__ __forceinline__ bool take_ticket(unsigned* ticket, unsigned expected)
   return last;
 }
 
-template <int OUT_ROWS, int EPI>
+template <int OUT_ROWS, int EPI, bool RESID = false>
 __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0, int* lds_flags) {
   const int M = p.M, S = p.S;
   const int64_t MN = (int64_t)M * p.N;
@@ -374,6 +425,16 @@ __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0,
       for (int idx = threadIdx.x; idx < M * OUT_ROWS; idx += 64 * p.nw) {
         const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
         const int n = rb * OUT_ROWS + r;
+        if constexpr (RESID) {
+          // every lane of a 16-column group takes part in the group sum
+          static_assert(EPI == EPI_PART && OUT_ROWS % 16 == 0, "residual after split-K partials");
+          const bool ok = n < p.N;
+          const int64_t e = (int64_t)m * p.N + (ok ? n : 0);
+          float g = 0.f;
+          for (int s = 0; s < S; ++s) g += ok ? load_agent(&p.part[s * MN + e]) : 0.f;
+          resid_out(p, m, n, ok, f2bf(g));
+          continue;
+        }
         if (n >= p.N) continue;
         const int64_t e = (int64_t)m * p.N + n;
         float g = 0.f, u = 0.f;
@@ -780,6 +841,9 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
   static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
   static_assert(CPW >= 1, "chunks per wave");
+  constexpr bool PRE = EpiTraits<EPI>::pre;       // finish the RMSNorm from the producer's partials
+  constexpr bool RESID = EpiTraits<EPI>::resid;   // hand the residual and its partials on
+  static_assert(!PRE || CPW == 1, "pre-normalised activations are loaded once (one chunk per wave)");
   constexpr int CW = 256;                        // columns per chunk (slab width)
   constexpr int KW = CW * CPW;                   // columns per wave
   constexpr int ROWS = 16 * NT;                  // weight rows per tile
@@ -842,6 +906,20 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
       }
     }
   };
+  // PRE: the producer's partial sums of squares are loaded first (rows
+  // wave + nw*i, groups lane + 64*j; the host guarantees M <= 4*nw and
+  // K <= 4096), so the row-norm reduction below waits for nothing else.
+  constexpr int SQR = PRE ? 4 : 1, SQG = PRE ? 4 : 1;
+  float sqv[SQR][SQG];
+  if constexpr (PRE) {
+    const int ngrp = p.K >> 4;
+#pragma unroll
+    for (int i = 0; i < SQR; ++i) {
+      const float* row = p.SQ + (int64_t)min(wave + nw * i, M - 1) * p.sq_ld;
+#pragma unroll
+      for (int g = 0; g < SQG; ++g) sqv[i][g] = row[min(lane + 64 * g, ngrp - 1)];
+    }
+  }
   load_acts(0);
 
   // Instruction q of slab (rb, c, nt): rows 2q + lane/32 of the 16-row group nt,
@@ -866,6 +944,45 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
 #pragma unroll
     for (int q = 0; q < RING; ++q) ring[q] = ld16_stream(wsrc_col(rb0, col_of(0), 0, q));
   }
+
+  // PRE: norm weights of this wave's columns (after the ring: they are needed
+  // only once the first slab has arrived anyway).  The norm itself is finished
+  // in the first slab, after its refills are issued, so that the weight
+  // stream does not wait for it: rstd of each row from the partial sums
+  // (lane-strided, then a wave butterfly: a fixed order), then
+  // A = bf16(w * bf16(x * rstd)) in place on the fragments (the cast placement
+  // of engine/kernels/gemm.py:28-56).
+  __shared__ float s_rstd[PRE ? 64 : 1];
+  u32x4 wnv[PRE ? UNITS : 1];
+  if constexpr (PRE) {
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      const int k = kw0 + 32 * u + 8 * g4;
+      wnv[u] = ld16((has_unit && k < p.K) ? p.NW + k : zero16);
+    }
+  }
+  if constexpr (PRE) {   // the row norms: the partial sums were the first loads issued
+    const int ngrp = p.K >> 4;
+#pragma unroll
+    for (int i = 0; i < SQR; ++i) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < SQG; ++g) t += lane + 64 * g < ngrp ? sqv[i][g] : 0.f;
+      t = wave_sum(t);
+      const int m = wave + nw * i;
+      if (lane == 0 && m < M) s_rstd[m] = rms_rstd(t, p.K, p.eps);
+    }
+    lds_barrier();
+  }
+  auto pre_normalize = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float rs = s_rstd[min(16 * mt + r16, M - 1)];
+#pragma unroll
+      for (int u = 0; u < UNITS; ++u)
+        af[mt][u] = __builtin_bit_cast(bf16x8, norm_bf16x8(__builtin_bit_cast(u32x4, af[mt][u]), wnv[u], rs));
+    }
+  };
 
   auto tile = [&](int j, auto last) {
     constexpr bool LAST = decltype(last)::value;
@@ -900,6 +1017,9 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
           if (!(LAST && last_slab)) ring[q] = ld16_stream(wsrc_col(rbn, coln, ntn, q));
           __builtin_amdgcn_sched_barrier(0);   // keep each refill next to its staging store
         }
+        if constexpr (PRE) {
+          if (c == 0 && nt == 0 && j == 0) pre_normalize();   // uniform: every wave, first slab only
+        }
 #pragma unroll
         for (int u = 0; u < UNITS; ++u) {
           const bf16x8 wv = *reinterpret_cast<const bf16x8*>(tr + r16 * PITCH + 64 * u + 16 * g4);
@@ -929,10 +1049,11 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   lds_barrier();
   if constexpr (BASE == EPI_ARGMAX) {
     argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
-  } else {
+  } else if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU) {
     flush_stage<OUT_ROWS, BASE>(p, stage, ntiles, rb0, slice);
-    if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU)
-      splitk_fixup<OUT_ROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+    splitk_fixup<OUT_ROWS, BASE, RESID>(p, ntiles, rb0, reinterpret_cast<int*>(parts));
+  } else {
+    flush_stage<OUT_ROWS, BASE, RESID>(p, stage, ntiles, rb0, slice);
   }
 }
 

@@ -104,8 +104,13 @@ class DecodePlan:
     (engine/model.py:215-262).  ``decode()`` touches only preallocated tensors
     and library workspaces, so it can be captured into a HIP graph."""
 
-    def __init__(self, model: SyntheticModel, B: int, T: int, max_new: int):
+    def __init__(self, model: SyntheticModel, B: int, T: int, max_new: int, handoff: bool = True):
+        """``handoff``: run the add + RMSNorm between projections inside the
+        projection kernels (the producer writes the residual and its per-row
+        partial sums of squares, the consumer finishes the norm) instead of as
+        the reference's normed projections (prologue per call)."""
         self.model = model
+        self.handoff = handoff
         cfg = model.cfg
         self.B, self.T, self.max_new = B, T, max_new
         self.cap = ((T + max(max_new, 256) + 2 * 64 + 63) // 64) * 64     # engine/model.py:224
@@ -129,6 +134,20 @@ class DecodePlan:
         self.mm_gu = K.SkinnyGateUp(B, I, H, dev, normed=True)
         self.mm_d = K.SkinnyMatmul(B, H, I, dev)
         self.mm_lm = K.LmArgmax(B, cfg.vocab, H, dev, normed=True)
+        if handoff:
+            # residual hand-off: partial sums of squares of the residual rows
+            # (16-column groups) and one zero-filled workspace per call site
+            self.sq_a = torch.zeros((B, K.sumsq_groups(B, H)), dtype=torch.float32, device=dev)
+            self.sq_b = torch.zeros_like(self.sq_a)
+            self.qkv = torch.empty((B, (HQ + 2 * HKV) * D), dtype=BF16, device=dev)
+            self.act = torch.empty((B, I), dtype=BF16, device=dev)
+            self.ids_out = torch.empty((B,), dtype=torch.int64, device=dev)
+            self.maxv_out = torch.empty((B,), dtype=torch.float32, device=dev)
+            self.ws_o = K._workspace(K.SK_OP_RESID_GEMM, B, H, HQ * D, None, dev)
+            self.ws_d = K._workspace(K.SK_OP_RESID_GEMM, B, H, I, None, dev)
+            self.ws_qkv = K._workspace(K.SK_OP_PRE_GEMM, B, (HQ + 2 * HKV) * D, H, None, dev)
+            self.ws_gu = K._workspace(K.SK_OP_PRE_GATEUP, B, I, H, None, dev)
+            self.ws_lm = K._workspace(K.SK_OP_PRE_LM_ARGMAX, B, cfg.vocab, H, None, dev)
         self.g_decode = None
 
     # -- prefill (torch GEMMs + SDPA, this package's norm/rope/swiglu/argmax) --
@@ -168,6 +187,9 @@ class DecodePlan:
         m, cfg = self.model, self.model.cfg
         B = self.B
         x = F.embedding(self.tok, m.embed)
+        if self.handoff:
+            self._decode_handoff(x)
+            return
         cur, y = x, self.zero
         for i, layer in enumerate(m.layers):
             qkv = self.mm_qkv(cur, layer.wqkv, norm=(y, layer.in_norm, self.xa, cfg.eps))
@@ -180,6 +202,32 @@ class DecodePlan:
             y = self.mm_d(act, layer.wd)
             cur = self.xb
         ids, _ = self.mm_lm(cur, m.lm_head, norm=(y, m.final_norm, self.xa, cfg.eps))
+        self.tok.copy_(ids)
+        self.pos.add_(1)
+
+    def _decode_handoff(self, x: torch.Tensor) -> None:
+        """The decode step with the residual hand-off: xa/xb and their partial
+        sums sq_a/sq_b pass between the projections (layer 0's input norm, on
+        the embedding, keeps the normed projection)."""
+        m, cfg = self.model, self.model.cfg
+        B, I, eps = self.B, cfg.intermediate, cfg.eps
+        for i, layer in enumerate(m.layers):
+            if i == 0:
+                qkv = self.mm_qkv(x, layer.wqkv, norm=(self.zero, layer.in_norm, self.xa, eps))
+            else:
+                qkv = K.rmsnorm_pre_gemm(self.xa, self.sq_a, layer.in_norm, eps, layer.wqkv, out=self.qkv,
+                                         ws=self.ws_qkv)
+            K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.pos, self.q,
+                                 self.k_cache[i], self.v_cache[i], 1, eps)
+            self.attention(self.q, self.k_cache[i], self.v_cache[i], self.pos, self.attn_out)
+            # xb = xa + o (o itself is not stored), then xa = xb + down(act)
+            K.gemm_residual(self.attn_out.view(B, cfg.heads * cfg.head_dim), layer.wo, self.xa, self.xb, self.sq_b,
+                            ws=self.ws_o)
+            act = K.rmsnorm_pre_gateup_swiglu(self.xb, self.sq_b, layer.post_norm, eps, layer.wgu[:I],
+                                              layer.wgu[I:], out=self.act, ws=self.ws_gu)
+            K.gemm_residual(act, layer.wd, self.xb, self.xa, self.sq_a, ws=self.ws_d)
+        ids, _ = K.rmsnorm_pre_lm_argmax(self.xa, self.sq_a, m.final_norm, eps, m.lm_head, ws=self.ws_lm,
+                                         ids=self.ids_out, maxv=self.maxv_out)
         self.tok.copy_(ids)
         self.pos.add_(1)
 

@@ -22,6 +22,9 @@ fast_topk     topk.py:40     fast_topk (sk_topk_bf16, same lane-sweep algorithm)
 qk_norm_rope_cache rope.py   qk_norm_rope_cache (sk_qk_norm_rope_cache_bf16)
 DecodeAttention attention.py DecodeAttention (sk_decode_attention_bf16, chain masks)
 logits.argmax engine.py:207  LmArgmax (sk_lm_argmax_bf16, fused into lm_head)
+(none)                       gemm_residual / rmsnorm_pre_*: the add + RMSNorm
+                             between two projections split across the
+                             producing and consuming kernels (decode step)
 ===========================  ==================================================
 
 All tensors are bf16 and live on one ROCm device; outputs are allocated per
@@ -36,9 +39,9 @@ import math
 import torch
 
 from . import _lib
-from ._lib import (SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_OP_RMSNORM_GATEUP,
-                   SK_OP_RMSNORM_GEMM, SK_OP_RMSNORM_LM_ARGMAX, SK_PATH_GEMV, SK_PATH_MFMA, SkConfig, check, cfg_ptr,
-                   lib)
+from ._lib import (SK_OP_ARGMAX, SK_OP_GATEUP, SK_OP_GEMM, SK_OP_LM_ARGMAX, SK_OP_PRE_GATEUP, SK_OP_PRE_GEMM,
+                   SK_OP_PRE_LM_ARGMAX, SK_OP_RESID_GEMM, SK_OP_RMSNORM_GATEUP, SK_OP_RMSNORM_GEMM,
+                   SK_OP_RMSNORM_LM_ARGMAX, SK_PATH_GEMV, SK_PATH_MFMA, SkConfig, check, cfg_ptr, lib)
 
 BF16 = torch.bfloat16
 
@@ -49,6 +52,7 @@ __all__ = [
     "SK_PATH_MFMA", "SK_PATH_GEMV", "SK_OP_GEMM", "SK_OP_GATEUP", "SK_OP_LM_ARGMAX", "SK_OP_ARGMAX",
     "SK_OP_RMSNORM_GEMM", "SK_OP_RMSNORM_GATEUP", "SK_OP_RMSNORM_LM_ARGMAX",
     "qk_norm_rope_cache", "DecodeAttention", "ancestor_masks", "fast_topk",
+    "gemm_residual", "rmsnorm_pre_gemm", "rmsnorm_pre_gateup_swiglu", "rmsnorm_pre_lm_argmax", "sumsq_groups",
 ]
 
 
@@ -238,6 +242,128 @@ def rmsnorm_lm_argmax(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, ep
                                           xout.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), ids.data_ptr(),
                                           maxv.data_ptr(), M, V, K, cfg_ptr(config), wp, wn, _stream(x)),
           "sk_rmsnorm_lm_argmax_bf16")
+    return ids, maxv
+
+
+# ---------------------------------------------------------------------------
+# Residual hand-off: the add + RMSNorm between two projections of a decoder
+# layer split across the producing and the consuming kernel (no norm kernel
+# in between).  The producer writes the residual xout = bf16(r + bf16(a @ w.T))
+# and per-row sums of squares of xout over 16-column groups; the consumer
+# finishes the norm from those sums.
+# ---------------------------------------------------------------------------
+
+def _f32_vec(t: torch.Tensor, name: str, numel: int) -> None:
+    _need(t.dtype == torch.float32 and t.is_contiguous() and t.numel() >= numel and t.is_cuda,
+          f"{name} must be a contiguous float32 CUDA tensor with >= {numel} elements")
+
+
+def sumsq_groups(M: int, N: int) -> int:
+    """Columns of the partial-sums buffer of an [M, N] residual: ceil(N / 16)."""
+    return (N + 15) // 16
+
+
+def gemm_residual(a: torch.Tensor, w: torch.Tensor, r: torch.Tensor, r_out: torch.Tensor, sq: torch.Tensor,
+                  config: SkConfig | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``r_out = bf16(r + bf16(a @ w.T))`` (the projection itself is not stored) and
+    ``sq[m, g] = sum(r_out[m, 16g:16g+16] ** 2)``; ``sq`` is float32 [M, ceil(N/16)].
+    ``r_out`` may be ``r``.  Returns ``r_out``."""
+    _mat(a, "a")
+    _mat(w, "w")
+    M, K = a.shape
+    N = w.shape[0]
+    _need(w.shape[1] == K, f"K mismatch: a {tuple(a.shape)} vs w {tuple(w.shape)}")
+    _need(r.dtype == BF16 and r_out.dtype == BF16 and r.shape == (M, N) and r_out.shape == (M, N),
+          "r and r_out must be bf16 [M, N]")
+    _need(r.stride(1) == 1 and r_out.stride(1) == 1 and r.stride(0) == r_out.stride(0), "r / r_out row layout")
+    _f32_vec(sq, "sq", M * sumsq_groups(M, N))
+    if ws is None and _lib.workspace_bytes(SK_OP_RESID_GEMM, M, N, K, config):
+        ws = _workspace(SK_OP_RESID_GEMM, M, N, K, config, a.device)
+    _device_guard(a)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_gemm_residual_bf16(a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), r.data_ptr(),
+                                      r_out.data_ptr(), r.stride(0), sq.data_ptr(), M, N, K, cfg_ptr(config), wp, wn,
+                                      _stream(a)), "sk_gemm_residual_bf16")
+    return r_out
+
+
+def _pre_inputs(x: torch.Tensor, sq: torch.Tensor, w_norm: torch.Tensor) -> None:
+    _mat(x, "x")
+    M, K = x.shape
+    _need(K % 16 == 0, "K must be a multiple of 16")
+    _f32_vec(sq, "sq", M * (K // 16))
+    _need(w_norm.dtype == BF16 and w_norm.is_contiguous() and w_norm.numel() == K, "w_norm must be bf16 [K]")
+
+
+def rmsnorm_pre_gemm(x: torch.Tensor, sq: torch.Tensor, w_norm: torch.Tensor, eps: float, w: torch.Tensor,
+                     out: torch.Tensor | None = None, config: SkConfig | None = None,
+                     ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = rms_norm(x, w_norm) @ w.T`` with the row norms taken from a producer's
+    partial sums ``sq`` (float32 [M, K/16], see gemm_residual)."""
+    _pre_inputs(x, sq, w_norm)
+    _mat(w, "w")
+    M, K = x.shape
+    N = w.shape[0]
+    _need(w.shape[1] == K, "K mismatch")
+    if out is None:
+        out = torch.empty((M, N), dtype=BF16, device=x.device)
+    _mat(out, "out")
+    _need(tuple(out.shape) == (M, N), "out shape")
+    if ws is None and _lib.workspace_bytes(SK_OP_PRE_GEMM, M, N, K, config):
+        ws = _workspace(SK_OP_PRE_GEMM, M, N, K, config, x.device)
+    _device_guard(x)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_rmsnorm_pre_gemm_bf16(x.data_ptr(), x.stride(0), sq.data_ptr(), w_norm.data_ptr(), float(eps),
+                                         w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0), M, N, K,
+                                         cfg_ptr(config), wp, wn, _stream(x)), "sk_rmsnorm_pre_gemm_bf16")
+    return out
+
+
+def rmsnorm_pre_gateup_swiglu(x: torch.Tensor, sq: torch.Tensor, w_norm: torch.Tensor, eps: float,
+                              wg: torch.Tensor, wu: torch.Tensor, out: torch.Tensor | None = None,
+                              config: SkConfig | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
+    """``out = swiglu(h @ wg.T, h @ wu.T)``, ``h = rms_norm(x, w_norm)`` from partial sums ``sq``."""
+    _pre_inputs(x, sq, w_norm)
+    _mat(wg, "wg")
+    _mat(wu, "wu")
+    M, K = x.shape
+    I = wg.shape[0]
+    _need(wg.shape == wu.shape and wg.shape[1] == K and wg.stride(0) == wu.stride(0), "gate/up weight shapes")
+    if out is None:
+        out = torch.empty((M, I), dtype=BF16, device=x.device)
+    _mat(out, "out")
+    _need(tuple(out.shape) == (M, I), "out shape")
+    if ws is None and _lib.workspace_bytes(SK_OP_PRE_GATEUP, M, I, K, config):
+        ws = _workspace(SK_OP_PRE_GATEUP, M, I, K, config, x.device)
+    _device_guard(x)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_rmsnorm_pre_gateup_swiglu_bf16(x.data_ptr(), x.stride(0), sq.data_ptr(), w_norm.data_ptr(),
+                                                  float(eps), wg.data_ptr(), wu.data_ptr(), wg.stride(0),
+                                                  out.data_ptr(), out.stride(0), M, I, K, cfg_ptr(config), wp, wn,
+                                                  _stream(x)), "sk_rmsnorm_pre_gateup_swiglu_bf16")
+    return out
+
+
+def rmsnorm_pre_lm_argmax(x: torch.Tensor, sq: torch.Tensor, w_norm: torch.Tensor, eps: float, w: torch.Tensor,
+                          config: SkConfig | None = None, ws: torch.Tensor | None = None,
+                          ids: torch.Tensor | None = None, maxv: torch.Tensor | None = None):
+    """Greedy token per row of ``rms_norm(x, w_norm) @ w.T`` with the norms from ``sq``.
+    Returns ``(ids int64 [M], maxv float32 [M])``."""
+    _pre_inputs(x, sq, w_norm)
+    _mat(w, "w")
+    M, K = x.shape
+    V = w.shape[0]
+    _need(w.shape[1] == K, "K mismatch")
+    ids = torch.empty((M,), dtype=torch.int64, device=x.device) if ids is None else ids
+    maxv = torch.empty((M,), dtype=torch.float32, device=x.device) if maxv is None else maxv
+    if ws is None:
+        ws = _workspace(SK_OP_PRE_LM_ARGMAX, M, V, K, config, x.device)
+    _device_guard(x)
+    wp, wn = _ws_args(ws)
+    check(lib().sk_rmsnorm_pre_lm_argmax_bf16(x.data_ptr(), x.stride(0), sq.data_ptr(), w_norm.data_ptr(),
+                                              float(eps), w.data_ptr(), w.stride(0), ids.data_ptr(), maxv.data_ptr(),
+                                              M, V, K, cfg_ptr(config), wp, wn, _stream(x)),
+          "sk_rmsnorm_pre_lm_argmax_bf16")
     return ids, maxv
 
 

@@ -261,3 +261,77 @@ def test_normed_argument_validation():
     lm = lib.sk_rmsnorm_lm_argmax_bf16(X0, Y0, NW0, 1e-6, XO0, 2560, W0, 2560, C0, C0 + 512, 8, 151936, 2560,
                                        None, None, 0, None)
     assert lm == SK_ERR_WORKSPACE
+
+
+# ---------------------------------------------------------------------------
+# Residual hand-off ops (producer: residual + partial sums; consumers: norm
+# finished from those sums)
+# ---------------------------------------------------------------------------
+
+from starter_amd._lib import (SK_OP_PRE_GATEUP, SK_OP_PRE_GEMM, SK_OP_PRE_LM_ARGMAX,  # noqa: E402
+                              SK_OP_RESID_GEMM, SK_PATH_MFMA_LDS as _LDS)
+
+HANDOFF = {  # decode-step call sites at Qwen3-4B shapes
+    "o_resid": (SK_OP_RESID_GEMM, 2560, 4096, SK_OP_GEMM), "d_resid": (SK_OP_RESID_GEMM, 2560, 9728, SK_OP_GEMM),
+    "qkv_pre": (SK_OP_PRE_GEMM, 6144, 2560, SK_OP_GEMM), "gu_pre": (SK_OP_PRE_GATEUP, 9728, 2560, SK_OP_GATEUP),
+    "lm_pre": (SK_OP_PRE_LM_ARGMAX, 151936, 2560, SK_OP_LM_ARGMAX),
+}
+
+
+@pytest.mark.parametrize("name", list(HANDOFF))
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+def test_handoff_default_config_is_a_ring_config(name, M):
+    """Hand-off ops run on the ring-streamed LDS-fed MFMA path: the tuned
+    projection configuration where it is one (M >= 2 at these shapes), else
+    a ring configuration; the workspace is the projection's own."""
+    op, N, K, base = HANDOFF[name]
+    cfg = _lib.default_config(op, M, N, K)
+    assert cfg.path == _LDS and cfg.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,))
+    assert _lib.check_config(op, M, N, K, cfg) == SK_OK
+    b = _lib.default_config(base, M, N, K)
+    if b.path == _LDS and b.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,)):
+        assert cfg.as_dict() == b.as_dict()
+    assert _lib.workspace_bytes(op, M, N, K, cfg) == _lib.workspace_bytes(base, M, N, K, cfg)
+
+
+def test_handoff_rejects_unsupported_configs():
+    gemv = SkConfig.make(SK_PATH_GEMV, 2, 5, 2)
+    tile512 = SkConfig.make(_LDS, 5, 16, 16)
+    split_pre = SkConfig.make(_LDS, 5, 8, 16, 2)
+    assert _lib.check_config(SK_OP_PRE_GEMM, 8, 6144, 2560, gemv) == SK_ERR_CONFIG
+    assert _lib.check_config(SK_OP_PRE_GEMM, 8, 6144, 2560, tile512) == SK_ERR_CONFIG
+    assert _lib.check_config(SK_OP_PRE_GEMM, 8, 6144, 2560, split_pre) == SK_ERR_CONFIG   # consumers: one K split
+    assert _lib.check_config(SK_OP_RESID_GEMM, 8, 2560, 9728, SkConfig.make(_LDS, 13, 8, 16, 3)) == SK_OK
+    assert _lib.check_config(SK_OP_RESID_GEMM, 8, 2560, 9728, SkConfig.make(_LDS, 10, 32, 16, 1)) == SK_OK
+
+
+R0, RO0, SQ0 = FAKE + (1 << 29), FAKE + (1 << 29) + (1 << 22), FAKE + (1 << 29) + (2 << 22)
+
+
+def _resid(lib, A=A0, W=W0, r=R0, ro=RO0, ldr=2560, sq=SQ0, M=8, N=2560, K=4096, cfg=None, ws=None, wsb=0):
+    return lib.sk_gemm_residual_bf16(A, K, W, K, r, ro, ldr, sq, M, N, K, _lib.cfg_ptr(cfg), ws, wsb, None)
+
+
+def _pre(lib, x=X0, sq=SQ0, nw=NW0, W=W0, C=C0, M=8, N=6144, K=2560, cfg=None, ws=None, wsb=0):
+    return lib.sk_rmsnorm_pre_gemm_bf16(x, K, sq, nw, 1e-6, W, K, C, N, M, N, K, _lib.cfg_ptr(cfg), ws, wsb, None)
+
+
+def test_handoff_argument_validation_precedes_any_device_work():
+    lib = _lib.lib()
+    assert _resid(lib, r=None) == SK_ERR_NULL
+    assert _resid(lib, sq=None) == SK_ERR_NULL
+    assert _resid(lib, ro=A0 + 512) == SK_ERR_ALIAS     # residual out overlaps the projection's input
+    assert _resid(lib, sq=RO0 + 64) == SK_ERR_ALIAS     # partial sums overlap the residual
+    assert _resid(lib, ro=R0 + 2) == SK_ERR_ALIAS       # partially overlapping residuals
+    assert _resid(lib, ldr=100) == SK_ERR_SHAPE
+    assert _resid(lib, M=65) == SK_ERR_SHAPE
+    assert _resid(lib, M=0, A=None, r=None, ro=None, sq=None) == SK_OK
+    assert _resid(lib, K=9728, cfg=SkConfig.make(_LDS, 13, 8, 16, 3)) == SK_ERR_WORKSPACE
+    assert _pre(lib, nw=None) == SK_ERR_NULL
+    assert _pre(lib, nw=NW0 + 2) == SK_ERR_ALIGN
+    assert _pre(lib, sq=SQ0 + 2) == SK_ERR_ALIGN
+    assert _pre(lib, C=X0) == SK_ERR_ALIAS              # output overlaps the activations
+    assert _pre(lib, C=SQ0) == SK_ERR_ALIAS             # output overlaps the partial sums
+    lm = lib.sk_rmsnorm_pre_lm_argmax_bf16(X0, 2560, SQ0, NW0, 1e-6, W0, 2560, C0, C0 + 512, 8, 151936, 2560,
+                                           None, None, 0, None)
+    assert lm == SK_ERR_WORKSPACE

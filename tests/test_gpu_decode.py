@@ -75,13 +75,14 @@ def _reference_logits(model: SyntheticModel, ids: torch.Tensor, cos, sin) -> tor
     return _bf(hf @ model.lm_head.float().t())
 
 
-def test_graph_replay_matches_eager_decode():
+@pytest.mark.parametrize("handoff", [True, False])
+def test_graph_replay_matches_eager_decode(handoff):
     torch.manual_seed(0)
     model = SyntheticModel(CFG, DEV, seed=1, norm_noise=0.1)
     B, T, N = 3, 40, 6
     ids = torch.randint(0, CFG.vocab, (B, T), device=DEV)
-    eager = DecodePlan(model, B, T, N).generate(ids, N)
-    plan = DecodePlan(model, B, T, N)
+    eager = DecodePlan(model, B, T, N, handoff=handoff).generate(ids, N)
+    plan = DecodePlan(model, B, T, N, handoff=handoff)
     plan.ids.copy_(ids)
     plan.prefill()
     plan.capture()
@@ -93,12 +94,15 @@ def test_graph_replay_matches_eager_decode():
     assert torch.equal(torch.stack(toks, 1), eager)
 
 
-def test_decode_tokens_match_torch_reference():
+@pytest.mark.parametrize("handoff", [True, False])
+def test_decode_tokens_match_torch_reference(handoff):
+    """Both decode steps: the reference's normed projections, and the residual
+    hand-off (norms finished inside the projection kernels)."""
     torch.backends.cuda.matmul.allow_tf32 = False
     model = SyntheticModel(CFG, DEV, seed=2, norm_noise=0.1)
     B, T, N = 2, 33, 8
     ids = torch.randint(0, CFG.vocab, (B, T), device=DEV, generator=torch.Generator(device=DEV).manual_seed(3))
-    plan = DecodePlan(model, B, T, N)
+    plan = DecodePlan(model, B, T, N, handoff=handoff)
     out = plan.generate(ids, N)                           # [B, N]: token after position T-1, T, ...
     seq = torch.cat([ids, out[:, :-1]], dim=1)            # the sequence the engine actually consumed
     logits = _reference_logits(model, seq, plan.cos, plan.sin)[:, T - 1:]      # [B, N, V]
