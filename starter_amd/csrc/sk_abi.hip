@@ -208,7 +208,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tn = gateup ? 2 : c.rows / 16;
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
-    if (c.waves > sk::mfmt_max_waves(pl->tm, pl->tn, KW)) return SK_ERR_CONFIG;
+    if (c.waves > sk::mfmt_max_waves(pl->tm, pl->tn, KW, variant == 1)) return SK_ERR_CONFIG;
     pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;

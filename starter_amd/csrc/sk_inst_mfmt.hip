@@ -11,7 +11,7 @@
 namespace sk {
 
 template <int MT, int NT, int KW, int EPI>
-__global__ void __launch_bounds__(64 * mfmt_max_waves(MT, NT, KW))
+__global__ void __launch_bounds__(64 * mfmt_max_waves(MT, NT, KW, EpiTraits<EPI>::pre))
 mfmt_entry(Args p) {
   mfmt_body<MT, NT, KW, EPI>(p);
 }

@@ -35,7 +35,11 @@ constexpr int gemv_regs(int MR, int RR, int KU, bool norm = false) {
 // Otherwise (ring, KW = 256 * chunks per wave): one 256-column chunk's
 // activation units plus an 8-instruction ring.
 constexpr int mfmt_regs(int MT, int NT, int KW) {
-  return KW == 512 ? 4 * 16 * MT + 4 * 16 * NT + 4 * NT * MT + 32 : 4 * 8 * MT + 4 * 8 + 4 * NT * MT + 32;
+  // tile body: weight tile + fragments + accumulators; ring body: fragments +
+  // ring + accumulators, plus, with several chunks, the next chunk's
+  // activations and their addresses (measured: about twice the data alone)
+  return KW == 512 ? 4 * 16 * MT + 4 * 16 * NT + 4 * NT * MT + 32
+                   : 4 * 8 * MT + 4 * 8 + 4 * NT * MT + 32 + (KW > 256 ? 8 * 8 * MT : 0);
 }
 
 // Waves per workgroup an instance is compiled for (its __launch_bounds__):
@@ -44,8 +48,12 @@ constexpr int mfmt_regs(int MT, int NT, int KW) {
 constexpr int max_waves_for_regs(int regs, bool norm = false) {
   return regs <= 128 ? 16 : (norm && regs <= 168 ? 12 : (regs <= 256 ? 8 : 4));
 }
-// Waves per workgroup an LDS-fed MFMA instance is compiled for.
-constexpr int mfmt_max_waves(int MT, int NT, int KW) { return max_waves_for_regs(mfmt_regs(MT, NT, KW)); }
+// Waves per workgroup an LDS-fed MFMA instance is compiled for.  The residual
+// hand-off consumers (pre) also hold the norm weights of their chunk and the
+// producer's partial sums (48 more registers) and use the 12-wave tier.
+constexpr int mfmt_max_waves(int MT, int NT, int KW, bool pre = false) {
+  return pre ? max_waves_for_regs(mfmt_regs(MT, NT, KW) + 48, true) : max_waves_for_regs(mfmt_regs(MT, NT, KW));
+}
 
 KernelFn mfma_for_epi0(int MT, int NT, int KU);
 KernelFn mfma_for_epi1(int MT, int NT, int KU);

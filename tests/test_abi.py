@@ -302,7 +302,7 @@ def test_handoff_rejects_unsupported_configs():
     assert _lib.check_config(SK_OP_PRE_GEMM, 8, 6144, 2560, tile512) == SK_ERR_CONFIG
     assert _lib.check_config(SK_OP_PRE_GEMM, 8, 6144, 2560, split_pre) == SK_ERR_CONFIG   # consumers: one K split
     assert _lib.check_config(SK_OP_RESID_GEMM, 8, 2560, 9728, SkConfig.make(_LDS, 13, 8, 16, 3)) == SK_OK
-    assert _lib.check_config(SK_OP_RESID_GEMM, 8, 2560, 9728, SkConfig.make(_LDS, 10, 32, 16, 1)) == SK_OK
+    assert _lib.check_config(SK_OP_RESID_GEMM, 8, 2560, 9728, SkConfig.make(_LDS, 4, 32, 32, 3)) == SK_OK
 
 
 R0, RO0, SQ0 = FAKE + (1 << 29), FAKE + (1 << 29) + (1 << 22), FAKE + (1 << 29) + (2 << 22)

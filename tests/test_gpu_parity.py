@@ -425,13 +425,17 @@ MFMT_CASES = {  # shape, 32-column units per wave (8: 256, 16: 512, 32: 1024), r
 
 def mfmt_config(Kd: int, ku: int, rows: int, split: int, M: int) -> SkConfig:
     """One K chunk per wave; above 32 rows use 256-column chunks and enough
-    splits that at most 8 waves share a tile."""
+    splits that at most 8 waves share a tile.  Four chunks per wave (ku=32)
+    allow 8 waves per workgroup up to 16 rows and 4 above (registers)."""
     if M > 32:
         ku, rows = 8, 16
         split = max(split, 1)
         while -(-(Kd // 256) // split) > 8:
             split += 1
     chunks = -(-Kd // (32 * ku))
+    if ku == 32:
+        while -(-chunks // split) > (8 if M <= 16 else 4):
+            split += 1
     return SkConfig.make(SK_PATH_MFMA_LDS, waves=-(-chunks // split), ku=ku, rows=rows, split=split)
 
 
