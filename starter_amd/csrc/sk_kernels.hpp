@@ -41,6 +41,7 @@ namespace sk {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum Epi : int {
@@ -250,6 +251,28 @@ __device__ __forceinline__ u32x4 norm_bf16x8(u32x4 s, u32x4 w, float rstd) {
     const uint16_t lo = f2bf(bf2f(w[q] & 0xFFFFu) * round_bf(bf2f(s[q] & 0xFFFFu) * rstd));
     const uint16_t hi = f2bf(bf2f(w[q] >> 16) * round_bf(bf2f(s[q] >> 16) * rstd));
     r[q] = (uint32_t)lo | ((uint32_t)hi << 16);
+  }
+  return r;
+}
+
+// The same for 8 columns of one row, with the weights given as bf16 pairs with
+// one half zeroed (wlo[q] = (w[2q], 0), whi[q] = (0, w[2q+1])): after the
+// first rounding the product w * y comes from v_dot2_f32_bf16 straight off the
+// packed bf16 pair; one bf16 x bf16 product plus a zero product is exact in
+// fp32, so the result equals the fp32 product rounded once, as above.
+__device__ __forceinline__ u32x4 norm_line_bf16x8(u32x4 x, const u32x4& wlo, const u32x4& whi, float rstd) {
+  // The pairs are taken as .s01/.s23/.. of a bf16x8 view (see dot8).
+  const bf16x8 wl = __builtin_bit_cast(bf16x8, wlo), wh = __builtin_bit_cast(bf16x8, whi);
+  const bf16x2 wlp[4] = {wl.s01, wl.s23, wl.s45, wl.s67};
+  const bf16x2 whp[4] = {wh.s01, wh.s23, wh.s45, wh.s67};
+  u32x4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const f32x2 t = {bf2f(x[q] & 0xFFFFu) * rstd, bf2f(x[q] >> 16) * rstd};
+    const bf16x2 yb = __builtin_convertvector(t, bf16x2);   // one v_cvt_pk_bf16_f32 (RNE)
+    const f32x2 h = {__builtin_amdgcn_fdot2_f32_bf16(yb, wlp[q], 0.0f, false),
+                     __builtin_amdgcn_fdot2_f32_bf16(yb, whp[q], 0.0f, false)};
+    r[q] = __builtin_bit_cast(uint32_t, __builtin_convertvector(h, bf16x2));
   }
   return r;
 }
@@ -936,6 +959,18 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
     }
   }
   issue_acts(0);
+  // PRE: the norm weights of this lane's 8 columns (the same for every row
+  // in the row-contiguous layout), as (w, 0) and (0, w) bf16 pairs.
+  u32x4 wlo, whi;
+  if constexpr (PRE) {
+    const int k = kw0 + 8 * (lane & 31);
+    const u32x4 w = ld16((has_unit && k < p.K) ? p.NW + k : zero16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wlo[q] = w[q] & 0xFFFFu;
+      whi[q] = w[q] & 0xFFFF0000u;
+    }
+  }
 
   // Instruction q of slab (rb, c, nt): rows 2q + lane/32 of the 16-row group nt,
   // 8 columns at kw0 + 256c + 8*(lane%32) (rows clamped in bounds).
@@ -954,35 +989,21 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   };
   char* const wdst = tr + lrow * PITCH + 16 * (lane & 31);
 
+  // Issued even by a workgroup without tiles (rows are clamped, so the loads
+  // stay in bounds): with a branch here the compiler could no longer count
+  // the ring loads behind the activation loads and would wait for all of
+  // them before staging the activations.
   u32x4 ring[RING];
-  if (ntiles > 0) {
 #pragma unroll
-    for (int q = 0; q < RING; ++q) ring[q] = ld16_stream(wsrc_col(rb0, col_of(0), 0, q));
-  }
-  // The first chunk's activations into fragments (their loads were issued
-  // before the ring, so this waits for them alone); with several chunks per
-  // wave, the next chunk's loads go out at once and are staged when that
-  // chunk starts, one chunk later.
-  stage_acts();
-  if constexpr (CPW > 1) issue_acts(1);
-
-  // PRE: norm weights of this wave's columns (after the ring: they are needed
-  // only once the first slab has arrived anyway).  The norm itself is finished
-  // in the first slab, after its refills are issued, so that the weight
-  // stream does not wait for it: rstd of each row from the partial sums
-  // (lane-strided, then a wave butterfly: a fixed order), then
-  // A = bf16(w * bf16(x * rstd)) in place on the fragments (the cast placement
-  // of engine/kernels/gemm.py:28-56).
-  __shared__ float s_rstd[PRE ? 64 : 1];
-  u32x4 wnv[PRE ? UNITS : 1];
+  for (int q = 0; q < RING; ++q) ring[q] = ld16_stream(wsrc_col(rb0, col_of(0), 0, q));
+  // PRE: the row norms (the partial sums were the first loads issued), then
+  // the first chunk's activations normalised in the row-contiguous layout,
+  // A = bf16(w * bf16(x * rstd)) (the cast placement of
+  // engine/kernels/gemm.py:28-56), while the first slab is still in flight.
+  // rstd of a row: its partial sums lane-strided, then a wave butterfly (a
+  // fixed order).
   if constexpr (PRE) {
-#pragma unroll
-    for (int u = 0; u < UNITS; ++u) {
-      const int k = kw0 + 32 * u + 8 * g4;
-      wnv[u] = ld16((has_unit && k < p.K) ? p.NW + k : zero16);
-    }
-  }
-  if constexpr (PRE) {   // the row norms: the partial sums were the first loads issued
+    __shared__ float s_rstd[64];
     const int ngrp = p.K >> 4;
 #pragma unroll
     for (int i = 0; i < SQR; ++i) {
@@ -994,16 +1015,20 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
       if (lane == 0 && m < M) s_rstd[m] = rms_rstd(t, p.K, p.eps);
     }
     lds_barrier();
-  }
-  auto pre_normalize = [&]() {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const float rs = s_rstd[min(16 * mt + r16, M - 1)];
-#pragma unroll
-      for (int u = 0; u < UNITS; ++u)
-        af[mt][u] = __builtin_bit_cast(bf16x8, norm_bf16x8(__builtin_bit_cast(u32x4, af[mt][u]), wnv[u], rs));
+    for (int q = 0; q < 8 * MT; ++q) {
+      if (2 * q < M) {   // uniform: row pairs past M hold zeros
+        const float rs = s_rstd[min(2 * q + (lane >> 5), M - 1)];
+        araw[q] = norm_line_bf16x8(araw[q], wlo, whi, rs);
+      }
     }
-  };
+  }
+  // The first chunk's activations into fragments (their loads were issued
+  // before the ring, so this waits for them alone); with several chunks per
+  // wave, the next chunk's loads go out at once and are staged when that
+  // chunk starts, one chunk later.
+  stage_acts();
+  if constexpr (CPW > 1) issue_acts(1);
 
   auto tile = [&](int j, auto last) {
     constexpr bool LAST = decltype(last)::value;
@@ -1040,9 +1065,6 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
           *reinterpret_cast<u32x4*>(wdst + 2 * q * PITCH) = ring[q];
           if (!(LAST && last_slab)) ring[q] = ld16_stream(wsrc_col(rbn, coln, ntn, q));
           __builtin_amdgcn_sched_barrier(0);   // keep each refill next to its staging store
-        }
-        if constexpr (PRE) {
-          if (c == 0 && nt == 0 && j == 0) pre_normalize();   // uniform: every wave, first slab only
         }
 #pragma unroll
         for (int u = 0; u < UNITS; ++u) {
