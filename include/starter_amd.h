@@ -293,6 +293,27 @@ int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_
                              const int64_t* tree, sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap,
                              int max_len, float scale, int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/*
+ * sk_decode_attention_rope_bf16: sk_qk_norm_rope_cache_bf16 followed by
+ * sk_decode_attention_bf16 (chain mask) in one launch, for the consecutive
+ * calls qk_norm_rope_cache(...) and self.attention(q, k_cache, v_cache, pos,
+ * out) of engine/model.py's decode layer.  No single reference counterpart.
+ * Arguments as in those two calls (qkv rows (b, t), t < R; the query rows go
+ * straight to the attention instead of a q buffer).  Each workgroup
+ * normalises and rotates its own query rows with the same arithmetic as
+ * sk_qk_norm_rope_cache_bf16 (same bits), and each workgroup whose key range
+ * holds slot pos[b] + t writes that slot's K and V rows before it reads the
+ * cache, so the outputs and the caches equal those of the two calls.  A query
+ * row whose slot is outside the rotary table attends with a zero query.
+ * Same workspace as sk_decode_attention_bf16 (same plan arguments).  out must
+ * not overlap qkv or the caches.
+ */
+int sk_decode_attention_rope_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w,
+                                  const sk_bf16* k_norm_w, const sk_bf16* cos, const sk_bf16* sin, int rope_rows,
+                                  float eps, sk_bf16* k_cache, sk_bf16* v_cache, const int32_t* pos, sk_bf16* out,
+                                  int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                                  int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Exact argmax plus approximate top-k over bf16 logits L[N, V] (row stride
  * ld) in one pass.  Replaces fast_topk (engine/kernels/topk.py:17-46) with
  * the same algorithm and results: 2048 lanes sweep each row with stride 2048,

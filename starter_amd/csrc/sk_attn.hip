@@ -44,6 +44,22 @@ struct RopeArgs {
   float eps;
 };
 
+// One wave, one head row src[0..127]: lane i returns the normalised and
+// rotated pair (o1, o2) = output dims (i, i + 64).  Shared by the standalone
+// kernel and the attention prologue, so both produce the same bits.
+__device__ __forceinline__ void rope_head(const uint16_t* src, const uint16_t* w, const uint16_t* cs,
+                                          const uint16_t* sn, float eps, int lane, uint16_t& o1, uint16_t& o2) {
+  const float x1 = bf2f(src[lane]), x2 = bf2f(src[lane + 64]);
+  const float ss = wave_sum(x1 * x1 + x2 * x2);
+  const float r = 1.0f / sqrtf(ss / (float)HEAD_D + eps);
+  const float y1 = round_bf(bf2f(w[lane]) * round_bf(x1 * r));
+  const float y2 = round_bf(bf2f(w[lane + 64]) * round_bf(x2 * r));
+  const float c1 = bf2f(cs[lane]), c2 = bf2f(cs[lane + 64]);
+  const float s1 = bf2f(sn[lane]), s2 = bf2f(sn[lane + 64]);
+  o1 = f2bf(round_bf(y1 * c1) + round_bf(-y2 * s1));
+  o2 = f2bf(round_bf(y2 * c2) + round_bf(y1 * s2));
+}
+
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(RopeArgs a) {
   const int row = blockIdx.x;                       // (b, t)
   const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
@@ -55,18 +71,9 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(RopeArgs a) {
   const bool is_q = head < a.HQ;
   if (!is_q && slot >= a.cap) return;
   const uint16_t* src = a.qkv + (int64_t)row * a.ld_qkv + (int64_t)head * HEAD_D;
-  const float x1 = bf2f(src[lane]), x2 = bf2f(src[lane + 64]);
-  const float ss = wave_sum(x1 * x1 + x2 * x2);
-  const float r = 1.0f / sqrtf(ss / (float)HEAD_D + a.eps);
-  const uint16_t* w = is_q ? a.qw : a.kw;
-  const float y1 = round_bf(bf2f(w[lane]) * round_bf(x1 * r));
-  const float y2 = round_bf(bf2f(w[lane + 64]) * round_bf(x2 * r));
-  const uint16_t* cs = a.cos + (int64_t)slot * HEAD_D;
-  const uint16_t* sn = a.sin + (int64_t)slot * HEAD_D;
-  const float c1 = bf2f(cs[lane]), c2 = bf2f(cs[lane + 64]);
-  const float s1 = bf2f(sn[lane]), s2 = bf2f(sn[lane + 64]);
-  const uint16_t o1 = f2bf(round_bf(y1 * c1) + round_bf(-y2 * s1));
-  const uint16_t o2 = f2bf(round_bf(y2 * c2) + round_bf(y1 * s2));
+  uint16_t o1, o2;
+  rope_head(src, is_q ? a.qw : a.kw, a.cos + (int64_t)slot * HEAD_D, a.sin + (int64_t)slot * HEAD_D, a.eps, lane,
+            o1, o2);
   if (is_q) {
     uint16_t* dst = a.q_out + ((int64_t)(b * a.HQ + head) * a.T + t) * HEAD_D;
     dst[lane] = o1;
@@ -111,6 +118,18 @@ struct AttnArgs {
   unsigned* tickets;        // [B*HKV, NRB]
   int HQ, HKV, R, G, cap, S, split_len, NRB;
   float scale;
+  // ROPE instances: q rows and the new K/V rows come from the projection
+  // buffer (rows (b, t)) through the per-head norm + rotary step.
+  const uint16_t* qkv;
+  int64_t ld_qkv;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  uint16_t* k_out;          // writable views of k / v
+  uint16_t* v_out;
+  int rope_rows;
+  float eps;
 };
 
 
@@ -132,8 +151,9 @@ __device__ __forceinline__ float row_bcast(float v, int src) {
   return __int_as_float(o);
 }
 
-template <int QR, int ATTN_WAVES, bool TREE>
+template <int QR, int ATTN_WAVES, bool TREE, bool ROPE = false>
 __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a) {
+  static_assert(!(ROPE && TREE), "the fused rotary prologue uses chain positions pos + t");
   __shared__ float s_m[ATTN_WAVES][QR], s_l[ATTN_WAVES][QR];
   __shared__ __attribute__((aligned(16))) float s_acc[ATTN_WAVES][QR][HEAD_D];
   __shared__ int s_last;
@@ -158,7 +178,53 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   // for K step s (rows >= QR are zero columns).
   const int r16 = lane & 15;
   bf16x8 qb[HEAD_D / 32];
-  {
+  if constexpr (ROPE) {
+    // Query rows through the norm + rotary step (one wave per row), into LDS.
+    // A row whose slot is outside the rotary table stays zero.
+    __shared__ __attribute__((aligned(16))) uint16_t s_q[QR][HEAD_D];
+    const int T = a.R;
+    for (int r = wave; r < QR; r += ATTN_WAVES) {   // wave-uniform
+      const int gr = rbk * QR + r;
+      const int t = gr / a.G, g = gr - (gr / a.G) * a.G;
+      const int slot = pos + t;
+      uint16_t o1 = 0, o2 = 0;
+      if (gr < rows && slot >= 0 && slot < a.rope_rows)
+        rope_head(a.qkv + (int64_t)(b * T + t) * a.ld_qkv + (int64_t)(kh * a.G + g) * HEAD_D, a.qw,
+                  a.cos + (int64_t)slot * HEAD_D, a.sin + (int64_t)slot * HEAD_D, a.eps, lane, o1, o2);
+      s_q[r][lane] = o1;
+      s_q[r][lane + 64] = o2;
+    }
+    // The new K/V rows of this (b, kv head) are written by every workgroup
+    // whose key range holds their slot (the last split also takes slots past
+    // the planned length), before any of its K/V loads: the stores are
+    // complete (vmcnt 0) before the barrier.  Only those workgroups read
+    // these slots, and each reads them after its own stores; several row
+    // blocks write the same values, so a read never sees an older row.
+    for (int t = wave; t < T; t += ATTN_WAVES) {   // wave-uniform
+      const int slot = pos + t;
+      const bool mine = slot >= start && (slot < start + a.split_len || s == S - 1);
+      if (mine && slot < a.cap && slot < a.rope_rows) {
+        const uint16_t* row = a.qkv + (int64_t)(b * T + t) * a.ld_qkv;
+        uint16_t o1, o2;
+        rope_head(row + (int64_t)(a.HQ + kh) * HEAD_D, a.kw, a.cos + (int64_t)slot * HEAD_D,
+                  a.sin + (int64_t)slot * HEAD_D, a.eps, lane, o1, o2);
+        const int64_t cs = ((int64_t)bk * a.cap + slot) * HEAD_D;
+        a.k_out[cs + lane] = o1;
+        a.k_out[cs + lane + 64] = o2;
+        const uint16_t* vsrc = row + (int64_t)(a.HQ + a.HKV + kh) * HEAD_D;
+        a.v_out[cs + lane] = vsrc[lane];
+        a.v_out[cs + lane + 64] = vsrc[lane + 64];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const bool real = r16 < QR;
+#pragma unroll
+    for (int st = 0; st < HEAD_D / 32; ++st) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&s_q[min(r16, QR - 1)][32 * st + 8 * kr]);
+      qb[st] = __builtin_bit_cast(bf16x8, real ? v : u32x4{0u, 0u, 0u, 0u});
+    }
+  } else {
     const int gr = rbk * QR + r16;
     const int t = gr / a.G, g = gr - (gr / a.G) * a.G;
     const bool real = r16 < QR && gr < rows;
@@ -490,6 +556,53 @@ size_t sk_decode_attention_workspace_bytes(int B, int HQ, int HKV, int D, int R,
   return p.need;
 }
 
+}  // extern "C"
+
+namespace {
+
+// Fills the plan-dependent fields of a and launches the instance for
+// (QR, tree, rope).
+int attn_run(const AttnPlan& p, sk::AttnArgs& a, int B, int HQ, int HKV, int R, int cap, float scale, void* ws,
+             bool rope, hipStream_t stream) {
+  if (p.need > 0) {
+    char* w = static_cast<char*>(ws);
+    a.tickets = reinterpret_cast<unsigned*>(w);
+    a.part_o = reinterpret_cast<float*>(w + p.tickets);
+    a.part_ml = reinterpret_cast<float*>(w + p.tickets + align256(p.part_o));
+  }
+  a.HQ = HQ;
+  a.HKV = HKV;
+  a.R = R;
+  a.G = HQ / HKV;
+  a.cap = cap;
+  a.S = p.S;
+  a.split_len = p.split_len;
+  a.NRB = p.NRB;
+  a.scale = scale;
+  const dim3 grid((unsigned)(B * HKV * p.NRB * p.S));
+  const dim3 block(64 * kAttnWaves);
+  if (rope) {
+    if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<8, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
+  } else if (a.tree) {
+    if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<8, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
+  } else {
+    if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<8, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
+  }
+  return attn_launch_status();
+}
+
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + nb && y < x + na;
+}
+
+}  // namespace
+
+extern "C" {
+
 int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_bf16* v_cache, const int32_t* pos,
                              const int64_t* tree, sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap,
                              int max_len, float scale, int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
@@ -511,31 +624,49 @@ int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_
   a.pos = pos;
   a.tree = tree;
   a.out = out;
-  if (p.need > 0) {
-    char* w = static_cast<char*>(ws);
-    a.tickets = reinterpret_cast<unsigned*>(w);
-    a.part_o = reinterpret_cast<float*>(w + p.tickets);
-    a.part_ml = reinterpret_cast<float*>(w + p.tickets + align256(p.part_o));
-  }
-  a.HQ = HQ;
-  a.HKV = HKV;
-  a.R = R;
-  a.G = HQ / HKV;
-  a.cap = cap;
-  a.S = p.S;
-  a.split_len = p.split_len;
-  a.NRB = p.NRB;
-  a.scale = scale;
-  const dim3 grid((unsigned)(B * HKV * p.NRB * p.S));
-  const dim3 block(64 * kAttnWaves);
-  if (tree) {
-    if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
-    else sk::decode_attn_kernel<8, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
-  } else {
-    if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
-    else sk::decode_attn_kernel<8, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
-  }
-  return attn_launch_status();
+  return attn_run(p, a, B, HQ, HKV, R, cap, scale, ws, false, stream);
+}
+
+int sk_decode_attention_rope_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w,
+                                  const sk_bf16* k_norm_w, const sk_bf16* cos, const sk_bf16* sin, int rope_rows,
+                                  float eps, sk_bf16* k_cache, sk_bf16* v_cache, const int32_t* pos, sk_bf16* out,
+                                  int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                                  int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (B < 0) return SK_ERR_SHAPE;
+  if (B == 0) return SK_OK;
+  AttnPlan p;
+  int st = attn_plan(B, HQ, HKV, D, R, cap, max_len, nsplit, &p);
+  if (st) return st;
+  if (rope_rows < 1 || ld_qkv < (int64_t)(HQ + 2 * HKV) * D || (long)B * R > 0x7FFFFFFFL) return SK_ERR_SHAPE;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos || !sin || !k_cache || !v_cache || !pos || !out) return SK_ERR_NULL;
+  if (!aligned16(k_cache) || !aligned16(v_cache)) return SK_ERR_ALIGN;
+  if (p.need > 0 && (!ws || ws_bytes < p.need)) return SK_ERR_WORKSPACE;
+  // The output is written while the projection rows and the caches are read.
+  const size_t out_bytes = (size_t)B * R * HQ * D * 2, cache_bytes = (size_t)B * HKV * cap * D * 2;
+  const size_t qkv_bytes = ((size_t)(B * R - 1) * ld_qkv + (size_t)(HQ + 2 * HKV) * D) * 2;
+  if (overlaps(out, out_bytes, qkv, qkv_bytes) || overlaps(out, out_bytes, k_cache, cache_bytes) ||
+      overlaps(out, out_bytes, v_cache, cache_bytes) || overlaps(k_cache, cache_bytes, v_cache, cache_bytes) ||
+      overlaps(k_cache, cache_bytes, qkv, qkv_bytes) || overlaps(v_cache, cache_bytes, qkv, qkv_bytes))
+    return SK_ERR_ALIAS;
+  st = attn_device_ok();
+  if (st) return st;
+  sk::AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.k = k_cache;
+  a.v = v_cache;
+  a.pos = pos;
+  a.out = out;
+  a.qkv = qkv;
+  a.ld_qkv = ld_qkv;
+  a.qw = q_norm_w;
+  a.kw = k_norm_w;
+  a.cos = cos;
+  a.sin = sin;
+  a.k_out = k_cache;
+  a.v_out = v_cache;
+  a.rope_rows = rope_rows;
+  a.eps = eps;
+  return attn_run(p, a, B, HQ, HKV, R, cap, scale, ws, true, stream);
 }
 
 }  // extern "C"

@@ -208,7 +208,8 @@ class DecodePlan:
     def _decode_handoff(self, x: torch.Tensor) -> None:
         """The decode step with the residual hand-off: xa/xb and their partial
         sums sq_a/sq_b pass between the projections (layer 0's input norm, on
-        the embedding, keeps the normed projection)."""
+        the embedding, keeps the normed projection), and the q/k norm, rotary
+        step and cache write run inside the attention launch."""
         m, cfg = self.model, self.model.cfg
         B, I, eps = self.B, cfg.intermediate, cfg.eps
         for i, layer in enumerate(m.layers):
@@ -217,9 +218,9 @@ class DecodePlan:
             else:
                 qkv = K.rmsnorm_pre_gemm(self.xa, self.sq_a, layer.in_norm, eps, layer.wqkv, out=self.qkv,
                                          ws=self.ws_qkv)
-            K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.pos, self.q,
-                                 self.k_cache[i], self.v_cache[i], 1, eps)
-            self.attention(self.q, self.k_cache[i], self.v_cache[i], self.pos, self.attn_out)
+            # q/k norm + rotary + cache write inside the attention launch
+            self.attention.rope_attend(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.pos,
+                                       self.k_cache[i], self.v_cache[i], self.attn_out, eps)
             # xb = xa + o (o itself is not stored), then xa = xb + down(act)
             K.gemm_residual(self.attn_out.view(B, cfg.heads * cfg.head_dim), layer.wo, self.xa, self.xb, self.sq_b,
                             ws=self.ws_o)

@@ -510,6 +510,31 @@ class DecodeAttention:
                                              HKV, D, R, cap, self.maxlen, float(self.scale), self.nsplit, wp, wn,
                                              _stream(q)), "sk_decode_attention_bf16")
 
+    def rope_attend(self, qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
+                    sin: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                    out: torch.Tensor, eps: float) -> None:
+        """``qk_norm_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, q, k_cache, v_cache, R, eps)``
+        followed by ``self(q, k_cache, v_cache, pos, out)`` in one launch
+        (sk_decode_attention_rope_bf16): same outputs and cache contents, no q
+        buffer.  Chain mask only (an instance built with tree=True refuses)."""
+        B, HQ, HKV, D, R, cap = self.B, self.HQ, self.HKV, self.D, self.R, self.cap
+        _need(not self.tree, "the fused rotary path uses chain positions (no tree masks)")
+        _mat(qkv, "qkv")
+        _need(qkv.shape[0] == B * R and qkv.shape[1] >= (HQ + 2 * HKV) * D, "qkv must be [B*R, (HQ+2*HKV)*D]")
+        _need(k_cache.shape == (B, HKV, cap, D) and v_cache.shape == k_cache.shape, "cache shapes")
+        _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous caches")
+        _need(out.shape == (B, R, HQ, D) and out.is_contiguous(), "out must be [B, R, HQ, D]")
+        _need(cos.shape == sin.shape and cos.shape[1] == D and cos.is_contiguous() and sin.is_contiguous(), "rope tables")
+        _i32_dev(pos, "pos")
+        _device_guard(qkv)
+        wp, wn = _ws_args(self.ws)
+        check(lib().sk_decode_attention_rope_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(),
+                                                  k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
+                                                  float(eps), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(),
+                                                  out.data_ptr(), B, HQ, HKV, D, R, cap, self.maxlen,
+                                                  float(self.scale), self.nsplit, wp, wn, _stream(qkv)),
+              "sk_decode_attention_rope_bf16")
+
 
 def ancestor_masks(parent: list[int]) -> list[int]:
     """Per-node int64 bit mask of the node and its ancestors (engine/kernels/attention.py:245-254)."""
