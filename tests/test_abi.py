@@ -335,3 +335,30 @@ def test_handoff_argument_validation_precedes_any_device_work():
     lm = lib.sk_rmsnorm_pre_lm_argmax_bf16(X0, 2560, SQ0, NW0, 1e-6, W0, 2560, C0, C0 + 512, 8, 151936, 2560,
                                            None, None, 0, None)
     assert lm == SK_ERR_WORKSPACE
+
+
+Q0, KC0, VC0, O0 = FAKE + (1 << 30), FAKE + (1 << 30) + (1 << 26), FAKE + (1 << 30) + (2 << 26), FAKE + (1 << 30) + (3 << 26)
+
+
+def _attn_rope(lib, qkv=Q0, ld=6144, kc=KC0, vc=VC0, out=O0, B=16, R=1, cap=1408, ws=None, wsb=0):
+    return lib.sk_decode_attention_rope_bf16(qkv, ld, FAKE, FAKE, FAKE, FAKE, 1408, 1e-6, kc, vc, FAKE, out,
+                                             B, 32, 8, 128, R, cap, 1152, 0.088, 0, ws, wsb, None)
+
+
+def test_fused_attention_argument_validation_precedes_any_device_work():
+    """sk_decode_attention_rope_bf16 rejects bad arguments before it touches the
+    device (fake, never dereferenced addresses); the workspace is the one
+    sk_decode_attention_workspace_bytes() reports for the same plan."""
+    lib = _lib.lib()
+    need = lib.sk_decode_attention_workspace_bytes(16, 32, 8, 128, 1, 1408, 1152, 0)
+    assert need > 0                                              # the default plan splits the keys
+    assert _attn_rope(lib) == SK_ERR_WORKSPACE
+    assert _attn_rope(lib, ws=FAKE, wsb=need - 1) == SK_ERR_WORKSPACE
+    assert _attn_rope(lib, qkv=None, ws=FAKE, wsb=need) == SK_ERR_NULL
+    assert _attn_rope(lib, kc=None, ws=FAKE, wsb=need) == SK_ERR_NULL
+    assert _attn_rope(lib, ld=6143, ws=FAKE, wsb=need) == SK_ERR_SHAPE      # row shorter than HQ + 2*HKV heads
+    assert _attn_rope(lib, kc=KC0 + 2, ws=FAKE, wsb=need) == SK_ERR_ALIGN
+    assert _attn_rope(lib, out=KC0 + 4096, ws=FAKE, wsb=need) == SK_ERR_ALIAS  # output inside the key cache
+    assert _attn_rope(lib, out=Q0 + 64, ws=FAKE, wsb=need) == SK_ERR_ALIAS     # output inside the projection rows
+    assert _attn_rope(lib, vc=KC0 + 128, ws=FAKE, wsb=need) == SK_ERR_ALIAS    # overlapping caches
+    assert _attn_rope(lib, B=0, qkv=None, kc=None, vc=None, out=None) == SK_OK
