@@ -230,8 +230,9 @@ int sk_rmsnorm_lm_argmax_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16*
  * path 3 and ku 8, or ku 8 / 32 with any split for the producer); cfg NULL or
  * path AUTO picks the tuned configuration when it is such a path, else the
  * first ring configuration that fits.  M <= 64; a consumer holds all of K in
- * one workgroup (16 waves of 256 columns at M <= 16, 8 above), so shapes with
- * no such configuration return SK_ERR_CONFIG. */
+ * one workgroup (12 waves of 256 columns, K <= 3072, at M <= 16; 8 waves,
+ * K <= 2048, above), so shapes with no such configuration return
+ * SK_ERR_CONFIG (Qwen3-4B's consumers, K = 2560: M <= 16). */
 int sk_gemm_residual_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, const sk_bf16* r,
                           sk_bf16* r_out, int64_t ldr, float* sq, int M, int N, int K, const sk_config* cfg, void* ws,
                           size_t ws_bytes, hipStream_t stream);

@@ -300,6 +300,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 6144, 2560, 4, {3, 10, 8, 32, 1, 0}},  // qkv        7.84 us  4022 GB/s
     {SK_OP_GEMM, 6144, 2560, 8, {3, 10, 8, 32, 1, 192}},  // qkv        7.99 us  3955 GB/s
     {SK_OP_GEMM, 6144, 2560, 16, {3, 10, 8, 32, 1, 192}},  // qkv        8.43 us  3764 GB/s
+    {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
+    {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 3, 32, 32, 1, 0}},  // qkv       12.84 us  2494 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {1, 16, 5, 16, 1, 0}},  // qkv       17.01 us  1890 GB/s
     {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
@@ -710,6 +712,13 @@ int handoff_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
   if (cfg && cfg->path != SK_PATH_AUTO) {
     *out = *cfg;
     return SK_OK;
+  }
+  // The hand-off op's own table entry, then its projection's.
+  if (const Tuned* t = tuned_lookup(op, M, N, K)) {
+    if (plan_shape_impl(bop, M, N, K, t->cfg, false, &pl, variant) == SK_OK) {
+      *out = t->cfg;
+      return SK_OK;
+    }
   }
   sk_config d;
   if (default_config(bop, M, N, K, 0, &d) == SK_OK && plan_shape_impl(bop, M, N, K, d, false, &pl, variant) == SK_OK) {

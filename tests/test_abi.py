@@ -278,18 +278,25 @@ HANDOFF = {  # decode-step call sites at Qwen3-4B shapes
 }
 
 
+OWN_ENTRY = {"qkv_pre"}   # hand-off ops with table entries of their own (M <= 16)
+
+
 @pytest.mark.parametrize("name", list(HANDOFF))
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_handoff_default_config_is_a_ring_config(name, M):
-    """Hand-off ops run on the ring-streamed LDS-fed MFMA path: the tuned
-    projection configuration where it is one (M >= 2 at these shapes), else
-    a ring configuration; the workspace is the projection's own."""
+    """Hand-off ops run on the ring-streamed LDS-fed MFMA path: their own
+    tuned entry where the table has one (the qkv consumer: 16-row tiles), else
+    the tuned projection configuration where it is a ring configuration (M >= 2
+    at these shapes), else a ring configuration; the workspace is the
+    projection's own."""
     op, N, K, base = HANDOFF[name]
     cfg = _lib.default_config(op, M, N, K)
     assert cfg.path == _LDS and cfg.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,))
     assert _lib.check_config(op, M, N, K, cfg) == SK_OK
     b = _lib.default_config(base, M, N, K)
-    if b.path == _LDS and b.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,)):
+    if name in OWN_ENTRY:
+        assert cfg.rows == 16
+    elif b.path == _LDS and b.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,)):
         assert cfg.as_dict() == b.as_dict()
     assert _lib.workspace_bytes(op, M, N, K, cfg) == _lib.workspace_bytes(base, M, N, K, cfg)
 
