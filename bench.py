@@ -188,11 +188,24 @@ def _cpu_model() -> str:
     return cpu
 
 
-def cpu_baseline(M: int, samples: int) -> dict:
+def _timed_steps(step, seconds: float, min_steps: int = 5) -> tuple[list[float], float]:
+    """Per-step times of `step` run back to back until `seconds` of work (and
+    at least `min_steps` steps) are done; returns (times, total seconds)."""
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < min_steps or time.perf_counter() - t_start < seconds:
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    return ts, time.perf_counter() - t_start
+
+
+def cpu_baseline(M: int, seconds: float) -> dict:
     """The reference's own CPU path for one step: torch F.linear (bf16 in,
     fp32 accumulate, bf16 out; engine/kernels/gemm.py:527 `a @ w.t()`) for QKV,
     o_proj and down, F.silu(g) * u over the gate/up projection (gemm.py:569),
-    on the host cores of this box.  Median of `samples` steps after 3 warmups."""
+    on the host cores of this box.  Median step of a sample of about `seconds`
+    of CPU work after 3 warmups."""
     import torch
     import torch.nn.functional as F
 
@@ -215,25 +228,22 @@ def cpu_baseline(M: int, samples: int) -> dict:
 
     for _ in range(3):
         step()
-    ts = []
-    for _ in range(samples):
-        t0 = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t0)
+    ts, total = _timed_steps(step, seconds)
     t = statistics.median(ts)
     step_bytes = sum(alg_bytes(n, M) for n in ("qkv", "o_proj", "gate_up", "down"))
     cpu = _cpu_model()
     return {"value": round(step_bytes / t / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "reference",
-            "sample": f"{samples} steps (median) of the M={M} layer workload via torch F.linear/F.silu on CPU "
-                      f"(the reference's a @ w.t() baseline path), {t * 1e3:.2f} ms/step, {cpu}"}
+            "sample": f"{len(ts)} steps ({total:.1f} s of CPU work; median step) of the M={M} layer workload via "
+                      f"torch F.linear/F.silu on CPU (the reference's a @ w.t() baseline path), "
+                      f"{t * 1e3:.2f} ms/step, {cpu}"}
 
 
-def cpu_port(M: int, samples: int) -> dict:
+def cpu_port(M: int, seconds: float) -> dict:
     """The CPU restatement of the hot path (oracle/, kind "port": plain C,
     fp32 accumulation, OpenMP over output rows) timed on this box's host
     cores for the same layer step: QKV, o_proj, gate_up+SwiGLU and down at
-    M rows.  Median of `samples` steps after one warmup.  The reference's
+    M rows.  Median step of about `seconds` of CPU work after one warmup.  The reference's
     own path is Triton on a GPU and has no CPU build to time."""
     import numpy as np
 
@@ -255,18 +265,15 @@ def cpu_port(M: int, samples: int) -> dict:
         oracle.gemm(act, w["down"])
 
     step()
-    ts = []
-    for _ in range(samples):
-        t0 = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t0)
+    ts, total = _timed_steps(step, seconds, min_steps=3)
     t = statistics.median(ts)
     step_bytes = sum(alg_bytes(n, M) for n in ("qkv", "o_proj", "gate_up", "down"))
     cpu = _cpu_model()
     return {"value": round(step_bytes / t / 1e9, 2), "unit": "GB/s", "cores": oracle.threads(),
             "kind": "port",
-            "sample": f"{samples} steps (median) of the M={M} layer workload (qkv, o_proj, gate_up+swiglu, down) "
-                      f"through the C oracle, {t * 1e3:.2f} ms/step, {oracle.threads()} OpenMP threads, {cpu}"}
+            "sample": f"{len(ts)} steps ({total:.1f} s of CPU work; median step) of the M={M} layer workload "
+                      f"(qkv, o_proj, gate_up+swiglu, down) through the C oracle, {t * 1e3:.2f} ms/step, "
+                      f"{oracle.threads()} OpenMP threads, {cpu}"}
 
 
 PROBE_LAUNCHES = 24
@@ -377,7 +384,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--sweep", action="store_true", help="also time all five shapes at M in 1..64 (BASELINE config 4)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-samples", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="CPU work in the reference baseline's sample (the oracle port gets half)")
     ap.add_argument("--decode-steps", type=int, default=127,
                     help="C5: greedy decode steps timed after a B=16, T=1024 prefill (0 skips it)")
     ap.add_argument("--decode-only", action="store_true",
@@ -489,9 +497,9 @@ def main() -> int:
     cpu = port = None
     if not args.no_cpu:
         log("timing the CPU baseline")
-        cpu = cpu_baseline(args.M, args.cpu_samples)
+        cpu = cpu_baseline(args.M, args.cpu_seconds)
         log("timing the C oracle on the CPU")
-        port = cpu_port(args.M, max(3, args.cpu_samples // 4))
+        port = cpu_port(args.M, args.cpu_seconds / 2)
 
     line = {
         "metric": METRIC,
