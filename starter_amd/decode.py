@@ -82,8 +82,11 @@ class SyntheticModel:
         H, I, D = cfg.hidden, cfg.intermediate, cfg.head_dim
         HQ, HKV = cfg.heads, cfg.kv_heads
 
+        # Drawn in place in bf16: an fp32 draw + cast makes the caching allocator
+        # release device segments, and on this platform every kernel of the
+        # process runs ~7% slower after a large device free.
         def w(*shape):
-            return (torch.randn(*shape, generator=g, device=self.device) * 0.02).to(BF16)
+            return torch.empty(*shape, dtype=BF16, device=self.device).normal_(0.0, 0.02, generator=g)
 
         def gain(n):
             if norm_noise == 0.0:
