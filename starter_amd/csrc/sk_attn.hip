@@ -288,7 +288,11 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   // for the prefetched loads at the end of every iteration).  Blocks past
   // `end` in the last iteration are fully masked; their loads read the last
   // valid row (one cached line).
-  auto process = [&](int n0, const u32x4* kf, const u32x4* vv) {
+  // MASKED: the block may hold keys a row must not see; blocks wholly below
+  // min(end, pos) need no masks (every real row sees every key below pos, and
+  // padding rows are never written out).
+  auto process = [&](int n0, const u32x4* kf, const u32x4* vv, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < HEAD_D / 32; ++st)
@@ -310,15 +314,19 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float dot = row_bcast(sacc[j], r) * a.scale;
-        const int key = key0 + j;
-        bool vis;
-        if constexpr (TREE) {
-          const int rel = key - pos;
-          vis = row_lim[r] >= 0 && (rel < 0 || (rel < a.R && ((row_tree[r] >> rel) & 1ll)));
+        if constexpr (MASKED) {
+          const int key = key0 + j;
+          bool vis;
+          if constexpr (TREE) {
+            const int rel = key - pos;
+            vis = row_lim[r] >= 0 && (rel < 0 || (rel < a.R && ((row_tree[r] >> rel) & 1ll)));
+          } else {
+            vis = key <= row_lim[r];
+          }
+          sc[j] = (key < end && vis) ? dot : -INFINITY;
         } else {
-          vis = key <= row_lim[r];
+          sc[j] = dot;
         }
-        sc[j] = (key < end && vis) ? dot : -INFINITY;
         mx = fmaxf(mx, sc[j]);
       }
       const float msafe = mx == -INFINITY ? 0.f : mx;
@@ -349,19 +357,24 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     load_block(start, kA, vA);
     load_block(start + step, kB, vB);
   }
+  const int unmasked_end = min(end, pos);   // blocks wholly below it skip the masks
+  auto run = [&](int nb, const u32x4* kf, const u32x4* vv) {
+    if (nb + step <= unmasked_end) process(nb, kf, vv, std::false_type{});   // uniform
+    else process(nb, kf, vv, std::true_type{});
+  };
   // The scheduling fences keep every prefetch ahead of the block it overlaps.
   for (int n0 = start; n0 < end; n0 += 3 * step) {
     load_block(n0 + 2 * step, kC, vC);
     __builtin_amdgcn_sched_barrier(0);
-    process(n0, kA, vA);
+    run(n0, kA, vA);
     __builtin_amdgcn_sched_barrier(0);
     load_block(n0 + 3 * step, kA, vA);
     __builtin_amdgcn_sched_barrier(0);
-    process(n0 + step, kB, vB);
+    run(n0 + step, kB, vB);
     __builtin_amdgcn_sched_barrier(0);
     load_block(n0 + 4 * step, kB, vB);
     __builtin_amdgcn_sched_barrier(0);
-    process(n0 + 2 * step, kC, vC);
+    run(n0 + 2 * step, kC, vC);
     __builtin_amdgcn_sched_barrier(0);
   }
 
