@@ -135,20 +135,19 @@ struct AttnArgs {
 
 // Value of lane `src` (0..15) of each 16-lane DPP row, in every lane of that
 // row (DPP row_newbcast; src is a compile-time constant after unrolling).
-__device__ __forceinline__ float row_bcast(float v, int src) {
-  const int iv = __float_as_int(v);
-  int o;
-  switch (src) {
-    case 0: o = __builtin_amdgcn_mov_dpp(iv, 0x150, 0xF, 0xF, false); break;
-    case 1: o = __builtin_amdgcn_mov_dpp(iv, 0x151, 0xF, 0xF, false); break;
-    case 2: o = __builtin_amdgcn_mov_dpp(iv, 0x152, 0xF, 0xF, false); break;
-    case 3: o = __builtin_amdgcn_mov_dpp(iv, 0x153, 0xF, 0xF, false); break;
-    case 4: o = __builtin_amdgcn_mov_dpp(iv, 0x154, 0xF, 0xF, false); break;
-    case 5: o = __builtin_amdgcn_mov_dpp(iv, 0x155, 0xF, 0xF, false); break;
-    case 6: o = __builtin_amdgcn_mov_dpp(iv, 0x156, 0xF, 0xF, false); break;
-    default: o = __builtin_amdgcn_mov_dpp(iv, 0x157, 0xF, 0xF, false); break;
-  }
-  return __int_as_float(o);
+// Reductions over lanes l, l^16, l^32, l^48 (the four 16-lane rows), by
+// row swaps: every lane ends with the same value.
+__device__ __forceinline__ float rows4_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 template <int QR, int ATTN_WAVES, bool TREE, bool ROPE = false>
@@ -236,27 +235,22 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
       qb[st] = __builtin_bit_cast(bf16x8, real ? v : u32x4{0u, 0u, 0u, 0u});
     }
   }
-  // Visibility of key n to local row r: keys before pos always; key pos + j
+  // Lane l owns query row l%16 (its MFMA column) and, in each 16-key block,
+  // keys 4*(l/16) .. +3 of that row; the 4 lanes of a row share its running
+  // max and keep partial sums.  acc[c][k] = O[row l%16][dim 8*(4*(l/16)+k) + c].
+  // Visibility of key n to the row: keys before pos always; key pos + j
   // (j < R) iff j <= t (chain) or bit j of tree[t] is set (draft tree).
-  int row_lim[QR];
-  long long row_tree[TREE ? QR : 1];
-#pragma unroll
-  for (int r = 0; r < QR; ++r) {
-    const int gr = rbk * QR + r;
-    const int t = gr / a.G;
-    const bool real = gr < rows;
-    row_lim[r] = real ? pos + t : -1;   // last visible key of the row (chain)
-    if constexpr (TREE) row_tree[r] = real ? (long long)a.tree[min(t, a.R - 1)] : 0ll;
-  }
+  const int my_gr = rbk * QR + r16;
+  const bool my_real = r16 < QR && my_gr < rows;
+  const int my_t = my_gr / a.G;
+  const int row_lim = my_real ? pos + my_t : -1;   // last visible key of the row (chain)
+  long long row_tree = 0ll;
+  if constexpr (TREE) row_tree = my_real ? (long long)a.tree[min(my_t, a.R - 1)] : 0ll;
 
-  float m[QR], l[QR], acc[QR][8];
+  float m = -INFINITY, l = 0.f;
+  f32x4 acc[8];
 #pragma unroll
-  for (int r = 0; r < QR; ++r) {
-    m[r] = -INFINITY;
-    l[r] = 0.f;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) acc[r][d] = 0.f;
-  }
+  for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Wave w processes keys n0 + 16w .. n0 + 16w + 15 of each 64-key block.
   //  * Scores: S^T[key][row] = K[16 keys, 128] . Q^T by four MFMAs; K is the A
@@ -298,59 +292,55 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     for (int st = 0; st < HEAD_D / 32; ++st)
       sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[st]), qb[st], sacc, 0, 0, 0);
     const int key0 = n0 + 16 * wave + 4 * kr;   // keys key0 .. key0+3 of this lane's row
-    // V of key pairs (j, j+1) per dim, packed as bf16 pairs for v_dot2.
-    uint32_t vp[2][4][2];
+    float sc[4];
+    float mx = m;
 #pragma unroll
-    for (int jp = 0; jp < 2; ++jp)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        vp[jp][c][0] = __builtin_amdgcn_perm(vv[2 * jp + 1][c], vv[2 * jp][c], 0x05040100u);
-        vp[jp][c][1] = __builtin_amdgcn_perm(vv[2 * jp + 1][c], vv[2 * jp][c], 0x07060302u);
-      }
-#pragma unroll
-    for (int r = 0; r < QR; ++r) {
-      float sc[4];
-      float mx = m[r];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float dot = row_bcast(sacc[j], r) * a.scale;
-        if constexpr (MASKED) {
-          const int key = key0 + j;
-          bool vis;
-          if constexpr (TREE) {
-            const int rel = key - pos;
-            vis = row_lim[r] >= 0 && (rel < 0 || (rel < a.R && ((row_tree[r] >> rel) & 1ll)));
-          } else {
-            vis = key <= row_lim[r];
-          }
-          sc[j] = (key < end && vis) ? dot : -INFINITY;
+    for (int j = 0; j < 4; ++j) {
+      const float dot = sacc[j] * a.scale;
+      if constexpr (MASKED) {
+        const int key = key0 + j;
+        bool vis;
+        if constexpr (TREE) {
+          const int rel = key - pos;
+          vis = row_lim >= 0 && (rel < 0 || (rel < a.R && ((row_tree >> rel) & 1ll)));
         } else {
-          sc[j] = dot;
+          vis = key <= row_lim;
         }
-        mx = fmaxf(mx, sc[j]);
+        sc[j] = (key < end && vis) ? dot : -INFINITY;
+      } else {
+        sc[j] = dot;
       }
-      const float msafe = mx == -INFINITY ? 0.f : mx;
-      const float alpha = __expf(m[r] - msafe);
-      float lsum = l[r] * alpha;
-#pragma unroll
-      for (int d = 0; d < 8; ++d) acc[r][d] *= alpha;
-#pragma unroll
-      for (int jp = 0; jp < 2; ++jp) {
-        const float p0 = __expf(sc[2 * jp] - msafe), p1 = __expf(sc[2 * jp + 1] - msafe);
-        lsum += p0;
-        lsum += p1;
-        const bf16x2 pp = {(__bf16)p0, (__bf16)p1};   // probabilities rounded to bf16 (RNE)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          acc[r][2 * c] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vp[jp][c][0]),
-                                                          acc[r][2 * c], false);
-          acc[r][2 * c + 1] = __builtin_amdgcn_fdot2_f32_bf16(pp, __builtin_bit_cast(bf16x2, vp[jp][c][1]),
-                                                              acc[r][2 * c + 1], false);
-        }
-      }
-      l[r] = lsum;
-      m[r] = mx;
+      mx = fmaxf(mx, sc[j]);
     }
+    mx = rows4_max(mx);
+    const float msafe = mx == -INFINITY ? 0.f : mx;
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = __expf(sc[j] - msafe);
+    // Rescale only when some row's max moved (alpha == 1 elsewhere, so the
+    // skipped multiplications are exact).
+    if (__builtin_amdgcn_ballot_w64(mx != m)) {   // wave-uniform
+      const float alpha = __expf(m - msafe);
+      l *= alpha;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] *= alpha;
+    }
+    l += (p[0] + p[1]) + (p[2] + p[3]);
+    m = mx;
+    // P.V on MFMA: O^T[dims][rows] += V^T[dims][16 keys] . P^T[16 keys][rows].
+    // B = the probabilities as they sit (lane l: row l%16, keys 4*(l/16)+j),
+    // rounded to bf16 (RNE) as the reference's tl.dot does; A for dim offset
+    // c = V[keys 4*(l/16)+j][8*(l%16) + c], key pairs packed by v_perm.
+    const bf16x2 p01 = {(__bf16)p[0], (__bf16)p[1]}, p23 = {(__bf16)p[2], (__bf16)p[3]};
+    const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{__builtin_bit_cast(uint32_t, p01), __builtin_bit_cast(uint32_t, p23)});
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t sel = h ? 0x07060302u : 0x05040100u;
+        const u32x2 vt = {__builtin_amdgcn_perm(vv[1][c4], vv[0][c4], sel), __builtin_amdgcn_perm(vv[3][c4], vv[2][c4], sel)};
+        acc[2 * c4 + h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vt), pb, acc[2 * c4 + h], 0, 0, 0);
+      }
   };
   u32x4 kA[HEAD_D / 32], vA[4], kB[HEAD_D / 32], vB[4], kC[HEAD_D / 32], vC[4];
   if (start < end) {
@@ -378,30 +368,19 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // Merge the 4 lane-group streams of each wave (lanes l, l^16, l^32, l^48
-  // hold the same dims), then the waves' results in LDS in wave order.
-#pragma unroll
-  for (int r = 0; r < QR; ++r) {
-    float M = fmaxf(m[r], __shfl_xor(m[r], 16));
-    M = fmaxf(M, __shfl_xor(M, 32));
-    const float w = m[r] == -INFINITY ? 0.f : __expf(m[r] - M);
-    float lw = l[r] * w;
-    lw += __shfl_xor(lw, 16);
-    lw += __shfl_xor(lw, 32);
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      float o = acc[r][d] * w;
-      o += __shfl_xor(o, 16);
-      o += __shfl_xor(o, 32);
-      acc[r][d] = o;
-    }
-    if (lane == 0) {
-      s_m[wave][r] = M;
-      s_l[wave][r] = lw;
-    }
+  // Per wave: the row sums of the 4 lanes of each row, then the waves'
+  // results merge in LDS in wave order.
+  const float lw = rows4_sum(l);
+  if (r16 < QR) {
     if (kr == 0) {
+      s_m[wave][r16] = m;
+      s_l[wave][r16] = lw;
+    }
 #pragma unroll
-      for (int d = 0; d < 8; ++d) s_acc[wave][r][8 * dg + d] = acc[r][d];
+    for (int k = 0; k < 4; ++k) {
+      float* dst = &s_acc[wave][r16][8 * (4 * kr + k)];
+      *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0][k], acc[1][k], acc[2][k], acc[3][k]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][k], acc[5][k], acc[6][k], acc[7][k]};
     }
   }
   __syncthreads();
