@@ -252,24 +252,30 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Wave w processes keys n0 + 16w .. n0 + 16w + 15 of each 64-key block.
-  //  * Scores: S^T[key][row] = K[16 keys, 128] . Q^T by four MFMAs; K is the A
-  //    operand (lane l: key l%16, dims 32s + 8*(l/16): 64 contiguous bytes of
-  //    one key row per load).  Lane l then holds keys 4*(l/16) + i (i < 4) of
-  //    query row l%16.
-  //  * P.V: lane l holds dims 8*(l%16) .. +7 of keys 4*(l/16) + j (j < 4),
-  //    i.e. the same four keys as its 16-lane DPP row in the score layout, so
-  //    each row's scores reach the lanes that need them by row broadcasts
-  //    (DPP row_newbcast) - no LDS.
-  // The next block's rows are loaded while the current one is processed
+  // Wave w processes keys n0 + 16w .. n0 + 16w + 15 of each block of
+  // 16 * ATTN_WAVES keys.  K and V are loaded row-contiguously: load j of a
+  // lane holds dims 8*(l%16) .. +7 of key 4j + l/16 (one load = 4 whole
+  // 256-byte rows per wave).
+  //  * Scores: S^T[key][row] = K[16 keys, 128] . Q^T by four MFMAs with K as
+  //    the A operand (lane l: key l%16, dims 32s + 8*(l/16)); the wave's K rows
+  //    pass through its own LDS tile (rows padded to 272 bytes, so neither the
+  //    row writes nor the column reads conflict) into that layout.  Lane l then
+  //    holds keys 4*(l/16) + i (i < 4) of query row l%16.
+  //  * P.V: lane l's V loads hold keys 4*(l/16) + j, the keys of its scores.
+  // The next blocks' rows are loaded while the current one is processed
   // (keys past `end` reload the last valid row and are masked).
+  constexpr int KPITCH = 2 * HEAD_D + 16;
+  __shared__ __attribute__((aligned(16))) char s_k[ATTN_WAVES][16 * KPITCH];
+  char* const ktile = s_k[wave];
   const int64_t kv_row0 = (int64_t)bk * a.cap;
   const int step = 16 * ATTN_WAVES;
   auto load_block = [&](int n0, u32x4* kf, u32x4* vv) {
     const int base = n0 + 16 * wave;
-    const int kk = max(min(base + r16, end - 1), 0);
 #pragma unroll
-    for (int st = 0; st < HEAD_D / 32; ++st) kf[st] = ld16(a.k + (kv_row0 + kk) * HEAD_D + 32 * st + 8 * kr);
+    for (int j = 0; j < 4; ++j) {
+      const int kk = max(min(base + 4 * j + kr, end - 1), 0);
+      kf[j] = ld16(a.k + (kv_row0 + kk) * HEAD_D + 8 * dg);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kv = max(min(base + 4 * kr + j, end - 1), 0);
@@ -287,10 +293,17 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   // padding rows are never written out).
   auto process = [&](int n0, const u32x4* kf, const u32x4* vv, auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
+    // K rows into the wave's tile and back in the A-operand layout (LDS
+    // operations of one wave execute in order; the compiler keeps these
+    // accesses in program order since their addresses may alias).
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(ktile + (4 * j + kr) * KPITCH + 16 * dg) = kf[j];
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < HEAD_D / 32; ++st)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kf[st]), qb[st], sacc, 0, 0, 0);
+    for (int st = 0; st < HEAD_D / 32; ++st) {
+      const u32x4 ka = *reinterpret_cast<const u32x4*>(ktile + r16 * KPITCH + 64 * st + 16 * kr);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka), qb[st], sacc, 0, 0, 0);
+    }
     const int key0 = n0 + 16 * wave + 4 * kr;   // keys key0 .. key0+3 of this lane's row
     float sc[4];
     float mx = m;
@@ -446,9 +459,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int cdiv(int a, int b) { return (a + b - 1) / b; }
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Waves per workgroup, 16 keys each per block (8 waves measured slower at the
-// Qwen3-4B decode shape: 19.6 vs 18.4 us at B = 16, ~1.1k keys).
-constexpr int kAttnWaves = 4;
+// Waves per workgroup, 16 keys each per block (at B = 16, ~1.1k keys, one
+// split: 8 waves 15.4 us, 4 waves 15.9 us).
+constexpr int kAttnWaves = 8;
 
 struct AttnPlan {
   int QR = 0, NRB = 0, S = 0, split_len = 0;
@@ -473,11 +486,11 @@ int attn_plan(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int ns
   const int blocks = cdiv(work, block);
   int S = nsplit;
   if (S <= 0) {
-    // About one workgroup per CU of an MI355X: longer key ranges per
-    // workgroup amortise its merge better than more workgroups per CU help
-    // (measured at B = 16, 8 KV heads, ~1.1k keys: 2 splits 19 us, 8 splits 24 us).
+    // About one workgroup per two CUs of an MI355X: the cross-workgroup merge
+    // of the splits costs more than the compute units left idle (B = 16,
+    // 8 KV heads, ~1.1k keys: one split 15.4 us, two 16.3 us, eight 24 us).
     const long pairs = (long)B * HKV;
-    S = (int)((256 + pairs - 1) / pairs);
+    S = (int)((128 + pairs - 1) / pairs);
     if (S > 32) S = 32;
   }
   if (S > blocks) S = blocks;

@@ -347,7 +347,7 @@ def test_handoff_argument_validation_precedes_any_device_work():
 Q0, KC0, VC0, O0 = FAKE + (1 << 30), FAKE + (1 << 30) + (1 << 26), FAKE + (1 << 30) + (2 << 26), FAKE + (1 << 30) + (3 << 26)
 
 
-def _attn_rope(lib, qkv=Q0, ld=6144, kc=KC0, vc=VC0, out=O0, B=16, R=1, cap=1408, ws=None, wsb=0):
+def _attn_rope(lib, qkv=Q0, ld=6144, kc=KC0, vc=VC0, out=O0, B=8, R=1, cap=1408, ws=None, wsb=0):
     return lib.sk_decode_attention_rope_bf16(qkv, ld, FAKE, FAKE, FAKE, FAKE, 1408, 1e-6, kc, vc, FAKE, out,
                                              B, 32, 8, 128, R, cap, 1152, 0.088, 0, ws, wsb, None)
 
@@ -357,8 +357,8 @@ def test_fused_attention_argument_validation_precedes_any_device_work():
     device (fake, never dereferenced addresses); the workspace is the one
     sk_decode_attention_workspace_bytes() reports for the same plan."""
     lib = _lib.lib()
-    need = lib.sk_decode_attention_workspace_bytes(16, 32, 8, 128, 1, 1408, 1152, 0)
-    assert need > 0                                              # the default plan splits the keys
+    need = lib.sk_decode_attention_workspace_bytes(8, 32, 8, 128, 1, 1408, 1152, 0)
+    assert need > 0                                              # the default plan splits the keys at B = 8
     assert _attn_rope(lib) == SK_ERR_WORKSPACE
     assert _attn_rope(lib, ws=FAKE, wsb=need - 1) == SK_ERR_WORKSPACE
     assert _attn_rope(lib, qkv=None, ws=FAKE, wsb=need) == SK_ERR_NULL
