@@ -94,14 +94,15 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(RopeArgs a) {
 // softmax statistics in fp32, probabilities rounded to bf16 before the PV
 // product, fp32 accumulation, one normalisation at the end).
 //
-// Workgroup (b, kv head, split s): 4 waves stream keys [s*split_len, ...)
-// clipped to the row's valid length pos[b] + t + 1, 16 keys per wave and
-// block.  The scores of the KV head's query rows (QR = G*R of them) come from
-// v_mfma_f32_16x16x32_bf16 with the key rows as the A operand; P.V runs on
-// v_dot2_f32_bf16 with the probabilities of two keys paired against their
-// value rows (v_perm_b32).  Each 16-lane row keeps an online-softmax stream
-// (m, l, acc[8 dims]) over its 4 keys per block; the 4 streams of a wave are
-// merged with lane exchanges, the 4 waves in LDS, both in a fixed order.
+// Workgroup (b, kv head, split s): ATTN_WAVES waves stream keys
+// [s*split_len, ...) clipped to the row's valid length pos[b] + t + 1, 16 keys
+// per wave and block.  The scores of the KV head's query rows (QR = G*R of
+// them, the columns of a 16-wide MFMA) come from v_mfma_f32_16x16x32_bf16 with
+// the key rows as the A operand; each lane runs the online softmax of its own
+// score column (4 keys of one row per block, the row max shared by the row's
+// 4 lanes through permlane row swaps), and P.V runs on
+// v_mfma_f32_16x16x16_bf16 with the probabilities as they sit in the score
+// layout.  The waves' (m, l, acc) are merged in LDS in wave order.
 // With several splits, the partial (m, l, acc) goes to the workspace and the
 // last workgroup of the (b, kv head) to arrive merges the splits in split
 // order (no second kernel).
@@ -133,8 +134,6 @@ struct AttnArgs {
 };
 
 
-// Value of lane `src` (0..15) of each 16-lane DPP row, in every lane of that
-// row (DPP row_newbcast; src is a compile-time constant after unrolling).
 // Reductions over lanes l, l^16, l^32, l^48 (the four 16-lane rows), by
 // row swaps: every lane ends with the same value.
 __device__ __forceinline__ float rows4_max(float x) {
@@ -397,27 +396,43 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     }
   }
   __syncthreads();
-  const bool single = (S == 1);
-  for (int idx = threadIdx.x; idx < QR * HEAD_D; idx += 64 * ATTN_WAVES) {
-    const int r = idx / HEAD_D, d = idx - (idx / HEAD_D) * HEAD_D;
+  // Per row: the merged max, each wave's weight and the merged sum (waves in
+  // order); then every output of the real rows combines the waves' partial
+  // accumulators with those weights.
+  __shared__ float s_w[ATTN_WAVES][QR], s_rowM[QR], s_rowL[QR];
+  if (threadIdx.x < QR) {
+    const int r = threadIdx.x;
     float M = -INFINITY;
+#pragma unroll
     for (int wv = 0; wv < ATTN_WAVES; ++wv) M = fmaxf(M, s_m[wv][r]);
-    float L = 0.f, O = 0.f;
+    float L = 0.f;
+#pragma unroll
     for (int wv = 0; wv < ATTN_WAVES; ++wv) {
       const float w = s_m[wv][r] == -INFINITY ? 0.f : __expf(s_m[wv][r] - M);
+      s_w[wv][r] = w;
       L += w * s_l[wv][r];
-      O += w * s_acc[wv][r][d];
     }
+    s_rowM[r] = M;
+    s_rowL[r] = L;
+  }
+  __syncthreads();
+  const bool single = (S == 1);
+  const int nreal = min(QR, rows - rbk * QR);   // rows of this block that exist
+  for (int idx = threadIdx.x; idx < nreal * HEAD_D; idx += 64 * ATTN_WAVES) {
+    const int r = idx / HEAD_D, d = idx - (idx / HEAD_D) * HEAD_D;
+    float O = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < ATTN_WAVES; ++wv) O += s_w[wv][r] * s_acc[wv][r][d];
+    const float L = s_rowL[r];
     const int gr = rbk * QR + r;
     const int t = gr / a.G, g = gr - (gr / a.G) * a.G;
     if (single) {
-      if (gr < rows)
-        a.out[((int64_t)(b * a.R + t) * a.HQ + kh * a.G + g) * HEAD_D + d] = f2bf(L > 0.f ? O / L : 0.f);
+      a.out[((int64_t)(b * a.R + t) * a.HQ + kh * a.G + g) * HEAD_D + d] = f2bf(L > 0.f ? O / L : 0.f);
     } else {
       const int64_t pr = ((int64_t)bq * S + s) * QR + r;
       store_agent(&a.part_o[pr * HEAD_D + d], O);
       if (d == 0) {
-        store_agent(&a.part_ml[2 * pr], M);
+        store_agent(&a.part_ml[2 * pr], s_rowM[r]);
         store_agent(&a.part_ml[2 * pr + 1], L);
       }
     }
@@ -468,18 +483,20 @@ struct AttnPlan {
   size_t tickets = 0, part_o = 0, part_ml = 0, need = 0;
 };
 
-// Splits: enough workgroups to give every compute unit several (the keys of
-// one (b, kv head) pair are split when B*HKV alone cannot fill the chip), each
-// split a whole number of 64-key workgroup blocks of the longest sequence the
-// plan will see.
+// Splits: the keys of one (b, kv head) pair are split when B*HKV alone
+// leaves most compute units idle, each split a whole number of workgroup
+// blocks (16 keys per wave) of the longest sequence the plan will see.
 int attn_plan(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int nsplit, AttnPlan* p) {
   if (B < 1 || HKV < 1 || HQ < HKV || HQ % HKV != 0 || R < 1 || cap < 1 || D != sk::HEAD_D) return SK_ERR_SHAPE;
   const int G = HQ / HKV;
   const int rows = G * R;
   if (rows > kAttnMaxRows) return SK_ERR_SHAPE;
-  // Query rows per workgroup: up to 8 (the accumulators are per lane); more
-  // rows take several row blocks, each streaming the keys once more.
-  p->QR = rows <= 4 ? 4 : 8;
+  // Query rows per workgroup: up to 16, the columns of the MFMA tiles (the
+  // per-lane state does not grow with them); more rows take several row
+  // blocks, each streaming the keys once more.  The smaller instances keep
+  // less LDS and epilogue work (B = 16, 1088 keys, R = 2: 17.1 us with 8
+  // rows, 17.8 us with 16).
+  p->QR = rows <= 4 ? 4 : rows <= 8 ? 8 : 16;
   p->NRB = cdiv(rows, p->QR);
   const int work = max_len > 0 && max_len < cap ? max_len : cap;
   const int block = 16 * kAttnWaves;   // keys per workgroup block
@@ -588,13 +605,16 @@ int attn_run(const AttnPlan& p, sk::AttnArgs& a, int B, int HQ, int HKV, int R, 
   const dim3 block(64 * kAttnWaves);
   if (rope) {
     if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
-    else sk::decode_attn_kernel<8, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
+    else if (p.QR == 8) sk::decode_attn_kernel<8, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<16, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
   } else if (a.tree) {
     if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
-    else sk::decode_attn_kernel<8, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
+    else if (p.QR == 8) sk::decode_attn_kernel<8, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<16, kAttnWaves, true><<<grid, block, 0, stream>>>(a);
   } else {
     if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
-    else sk::decode_attn_kernel<8, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
+    else if (p.QR == 8) sk::decode_attn_kernel<8, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<16, kAttnWaves, false><<<grid, block, 0, stream>>>(a);
   }
   return attn_launch_status();
 }

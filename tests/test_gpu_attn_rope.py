@@ -5,7 +5,7 @@ The fused launch must equal the two launches it replaces,
 sk_qk_norm_rope_cache_bf16 then sk_decode_attention_bf16 (each pinned against
 the oracle in test_gpu_attn.py), bit for bit: the attention output and both
 caches.  Cases: the Qwen3-4B decode shape at several split counts, verify rows
-(8 query rows per workgroup, and two row blocks), a slot past the planned
+(up to 16 query rows per workgroup, and two row blocks), a slot past the planned
 length, graph replays with a growing length, and argument checks.
 """
 
@@ -62,7 +62,8 @@ def _assert_same(a: torch.Tensor, b: torch.Tensor, what: str) -> None:
     (16, 32, 8, 1, 1100, tuple(range(1000, 1016)), 1100, 3),
     (4, 32, 8, 1, 300, (0, 1, 63, 64), 300, 2),                   # first positions, split boundary
     (2, 8, 2, 2, 200, (50, 127), 200, 2),                         # verify rows: 8 rows per workgroup
-    (2, 8, 2, 3, 200, (50, 126), 200, 3),                         # 12 rows: two row blocks
+    (2, 8, 2, 3, 200, (50, 126), 200, 3),                         # 12 rows in one row block of 16
+    (2, 8, 2, 5, 200, (50, 124), 200, 2),                         # 20 rows: two row blocks of 16
     (3, 8, 2, 1, 300, (10, 150, 250), 128, None),                 # slots past the planned length
 ])
 def test_fused_equals_rope_then_attention(B, HQ, HKV, R, cap, starts, maxlen, nsplit):
