@@ -280,8 +280,8 @@ int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16
  *   out    [B, R, HQ, D] bf16 (rows (b, t) of [B*R, HQ*D])
  *   max_len: the longest sequence the caller will attend over (bounds the
  *            splits; 0 = cap); nsplit: key splits per (b, kv head), 0 = default
- * (HQ/HKV) * R must be at most 64; query rows are processed 8 per workgroup
- * (more rows stream the keys once per block of 8).  Scores and softmax
+ * (HQ/HKV) * R must be at most 64; query rows are processed up to 16 per
+ * workgroup (more rows stream the keys once per block of 16).  Scores and softmax
  * statistics in fp32, probabilities rounded to bf16 before the PV product,
  * fp32 accumulation (attention.py:9-11).  Needs a zero-filled workspace of
  * sk_decode_attention_workspace_bytes() bytes when it splits the keys; the
