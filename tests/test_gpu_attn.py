@@ -195,10 +195,11 @@ def test_decode_attention_visible_key_boundary(nsplit):
             assert torch.allclose(o, vc[b, kh, pos[b]].float(), atol=0.05), (b, kh)
 
 
-@pytest.mark.parametrize("R,nsplit", [(5, None), (8, 3), (3, 1)])
+@pytest.mark.parametrize("R,nsplit", [(5, None), (8, 3), (3, 1), (2, None), (4, 2)])
 def test_decode_attention_verify_rows_chain(R, nsplit):
-    """Speculative verify: R query rows per sequence (G*R up to 32 here, so
-    several 8-row blocks), chain mask (row t sees keys <= pos + t)."""
+    """Speculative verify: R query rows per sequence (G*R = 8 .. 32 here: the
+    8-row instance, one full or partial 16-row block, or two blocks), chain
+    mask (row t sees keys <= pos + t)."""
     B, HQ, HKV, CAP = 4, 32, 8, 700
     g = torch.Generator().manual_seed(R * 10 + (nsplit or 0))
     q = randn_bf16((B, HQ, R, D), 1.0, g)
