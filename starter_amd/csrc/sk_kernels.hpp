@@ -1017,12 +1017,19 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
       if (lane == 0 && m < M) s_rstd[m] = rms_rstd(t, p.K, p.eps);
     }
     lds_barrier();
+    // All row norms are read before any is used (one LDS wait, not one per
+    // row pair); row pairs past M hold zeros and are skipped, and when every
+    // pair holds a real row the loop carries no per-pair branch.
+    float rsv[8 * MT];
 #pragma unroll
-    for (int q = 0; q < 8 * MT; ++q) {
-      if (2 * q < M) {   // uniform: row pairs past M hold zeros
-        const float rs = s_rstd[min(2 * q + (lane >> 5), M - 1)];
-        araw[q] = norm_line_bf16x8(araw[q], wlo, whi, rs);
-      }
+    for (int q = 0; q < 8 * MT; ++q) rsv[q] = s_rstd[min(2 * q + (lane >> 5), M - 1)];
+    if (M > 2 * (8 * MT - 1)) {   // uniform
+#pragma unroll
+      for (int q = 0; q < 8 * MT; ++q) araw[q] = norm_line_bf16x8(araw[q], wlo, whi, rsv[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8 * MT; ++q)
+        if (2 * q < M) araw[q] = norm_line_bf16x8(araw[q], wlo, whi, rsv[q]);   // uniform
     }
   }
   // The first chunk's activations into fragments (their loads were issued
