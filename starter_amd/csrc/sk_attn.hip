@@ -198,7 +198,10 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     // complete (vmcnt 0) before the barrier.  Only those workgroups read
     // these slots, and each reads them after its own stores; several row
     // blocks write the same values, so a read never sees an older row.
-    for (int t = wave; t < T; t += ATTN_WAVES) {   // wave-uniform
+    // Row t goes to wave (QR + t) mod ATTN_WAVES, so with fewer query rows
+    // than waves the K/V rows run beside the query rows, not after them.
+    constexpr int KV_WAVE0 = QR % ATTN_WAVES;
+    for (int t = (wave - KV_WAVE0 + ATTN_WAVES) % ATTN_WAVES; t < T; t += ATTN_WAVES) {   // wave-uniform
       const int slot = pos + t;
       const bool mine = slot >= start && (slot < start + a.split_len || s == S - 1);
       if (mine && slot < a.cap && slot < a.rope_rows) {
