@@ -255,9 +255,9 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   for (int c = 0; c < 8; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Wave w processes keys n0 + 16w .. n0 + 16w + 15 of each block of
-  // 16 * ATTN_WAVES keys.  K and V are loaded row-contiguously: load j of a
-  // lane holds dims 8*(l%16) .. +7 of key 4j + l/16 (one load = 4 whole
-  // 256-byte rows per wave).
+  // 16 * ATTN_WAVES keys.  K and V are loaded row-contiguously (one load = 4
+  // whole 256-byte rows per wave): load j of lane l holds dims 8*(l%16) .. +7
+  // of key 4j + l/16 for K and of key 4*(l/16) + j for V.
   //  * Scores: S^T[key][row] = K[16 keys, 128] . Q^T by four MFMAs with K as
   //    the A operand (lane l: key l%16, dims 32s + 8*(l/16)); the wave's K rows
   //    pass through its own LDS tile (rows padded to 272 bytes, so neither the
