@@ -357,7 +357,7 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
         acc[2 * c4 + h] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, vt), pb, acc[2 * c4 + h], 0, 0, 0);
       }
   };
-  u32x4 kA[HEAD_D / 32], vA[4], kB[HEAD_D / 32], vB[4], kC[HEAD_D / 32], vC[4];
+  u32x4 kA[4], vA[4], kB[4], vB[4], kC[4], vC[4];   // the 4 K and 4 V loads of a block
   if (start < end) {
     load_block(start, kA, vA);
     load_block(start + step, kB, vB);
