@@ -25,10 +25,12 @@ The ``decode`` object of the JSON line is BASELINE configuration 5: a
 synthetic Qwen3-4B (36 layers, random bf16 weights) decoding greedily at
 batch 16 after a 1024-token prompt, one HIP graph per decode step, reported as
 decode tok/s = 16 * steps / decode time (and end-to-end tok/s including the
-prefill).
+prefill).  The ``attention`` object times the decode step's attention launch
+(q/k norm + rotary + KV write + GQA attention) alone at batch 16, position 1088,
+with its achieved HBM bandwidth (the K and V rows read per launch).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
-                       [--decode-steps S] [--decode-only]
+                       [--decode-steps S] [--decode-only] [--attention-only]
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 
@@ -376,6 +378,75 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int = 128)
     return out
 
 
+_KEEP: list = []   # attention workloads stay allocated until the process ends (no device frees)
+
+
+def attention_benchmark(launches: int = 64, B: int = 16, pos: int = 1088, cap: int = 1408, ncache: int = 8) -> dict:
+    """Decode attention with the rotary step (sk_decode_attention_rope_bf16, the
+    launch the decode step makes per layer) at the Qwen3-4B decode shape: B
+    sequences at position ``pos``, 32/8 heads of 128, plan length 1152 (one key
+    split per (sequence, KV head) at B = 16).  ``ncache`` K/V cache pairs of
+    92 MB rotate so that a launch does not find its rows in the 256 MB Infinity
+    Cache.  One graph of ``launches`` launches, HIP events on its stream; HBM
+    bytes per launch = the K and V rows read, B x 8 x (pos + 1) x 128 x 2 x 2."""
+    import statistics
+
+    import torch
+
+    from starter_amd import kernels as K
+    from starter_amd.decode import Qwen3Config, rope_tables
+
+    dev = "cuda:0"
+    cfg = Qwen3Config()
+    HQ, HKV, D = cfg.heads, cfg.kv_heads, cfg.head_dim
+    g = torch.Generator(device=dev).manual_seed(13)
+
+    def rnd(*shape):
+        return torch.empty(*shape, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+
+    ks = [rnd(B, HKV, cap, D) for _ in range(ncache)]
+    vs = [rnd(B, HKV, cap, D) for _ in range(ncache)]
+    qkv = rnd(B, (HQ + 2 * HKV) * D)
+    qw = torch.ones(D, dtype=torch.bfloat16, device=dev)
+    cos, sin = rope_tables(cfg, cap, dev)
+    posv = torch.full((B,), pos, dtype=torch.int32, device=dev)
+    out = torch.empty(B, 1, HQ, D, dtype=torch.bfloat16, device=dev)
+    attn = K.DecodeAttention(B, HQ, HKV, D, cap, dev, maxlen=1152)
+    _KEEP.extend([ks, vs, qkv, qw, cos, sin, posv, out, attn])
+
+    def call(i):
+        attn.rope_attend(qkv, qw, qw, cos, sin, posv, ks[i % ncache], vs[i % ncache], out, cfg.eps)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(2):
+            call(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(launches):
+            call(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(5):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b) * 1e3 / launches)
+    us = statistics.median(ts)
+    byts = B * HKV * (pos + 1) * D * 2 * 2
+    log(f"attention: {us:.2f} us per launch, {byts / us / 1e3:.0f} GB/s")
+    return {"us": round(us, 3), "GB/s": round(byts / us / 1e3, 1), "frac_peak": round(byts / us / 1e3 / PEAK_HBM_GBS, 4),
+            "bytes": byts, "launches": launches,
+            "workload": f"q/k norm + rotary + KV write + GQA decode attention, B={B}, 32/8 heads x 128, "
+                        f"position {pos}, {ncache} rotating caches of cap {cap}"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -389,6 +460,8 @@ def main() -> int:
                     help="CPU work in the reference baseline's sample (the oracle port gets half)")
     ap.add_argument("--decode-steps", type=int, default=127,
                     help="C5: greedy decode steps timed after a B=16, T=1024 prefill (0 skips it)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the decode-attention measurement and print its JSON object")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the C5 decode measurement and print its JSON object")
     ap.add_argument("--probe", action="store_true",
@@ -421,6 +494,9 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.probe:
         return probe(args.M)
+    if args.attention_only:
+        print(json.dumps({"attention": attention_benchmark()}), flush=True)
+        return 0
     if args.decode_only:
         print(json.dumps({"decode": decode_benchmark(max(1, args.decode_steps))}), flush=True)
         return 0
@@ -493,6 +569,7 @@ def main() -> int:
     decode = None
     if args.decode_steps > 0:
         decode = decode_benchmark(args.decode_steps)
+    attention = attention_benchmark()
 
     cpu = port = None
     if not args.no_cpu:
@@ -521,6 +598,7 @@ def main() -> int:
                    "frac_peak_hbm": round(value / PEAK_HBM_GBS, 4)},
         "roofline": roofline,
         "decode": decode,
+        "attention": attention,
         "cpu_baseline": cpu,
         "cpu_port": port,
         "per_gemm": per_gemm,
