@@ -84,9 +84,21 @@ class SyntheticModel:
 
         # Drawn in place in bf16: an fp32 draw + cast makes the caching allocator
         # release device segments, and on this platform every kernel of the
-        # process runs ~7% slower after a large device free.
+        # process runs ~7% slower after a large device free.  All projection
+        # matrices are views into one allocation (256-byte aligned): a decode
+        # step over them measured 0.3-0.4% faster than over one allocation per
+        # matrix (5727-5729 vs 5701-5715 tok/s, alternating runs on one box).
+        mats = [(cfg.vocab, H)] + [((HQ + 2 * HKV) * D, H), (H, HQ * D), (2 * I, H), (H, I)] * cfg.layers
+        align = lambda n: (n + 127) // 128 * 128
+        pool = torch.empty(sum(align(a * b) for a, b in mats), dtype=BF16, device=self.device)
+        used = 0
+
         def w(*shape):
-            return torch.empty(*shape, dtype=BF16, device=self.device).normal_(0.0, 0.02, generator=g)
+            nonlocal used
+            n = shape[0] * shape[1]
+            view = pool[used:used + n].view(*shape)
+            used += align(n)
+            return view.normal_(0.0, 0.02, generator=g)
 
         def gain(n):
             if norm_noise == 0.0:
