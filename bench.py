@@ -181,6 +181,37 @@ class Workload:
         del g
         return statistics.median(t) * 1000.0 / launches
 
+    def launch_library(self, name: str, layer: int) -> None:
+        """The vendor-library yardstick of the reference's pickers: ``a @ w.t()``
+        through torch (hipBLASLt on ROCm; engine/kernels/gemm.py:527-528,
+        569-570) on the same weights.  Only the GEMM is timed: gate_up's
+        SwiGLU and lm_head's argmax would come on top (the library writes the
+        full [M, 2I] / [M, V] output instead)."""
+        mm = self.torch.mm
+        if name == "qkv":
+            mm(self.x, self.wqkv[layer].t(), out=self.lib_out["qkv"])
+        elif name == "o_proj":
+            mm(self.attn, self.wo[layer].t(), out=self.lib_out["o_proj"])
+        elif name == "gate_up":
+            mm(self.x, self.wgu[layer].t(), out=self.lib_out["gate_up"])
+        elif name == "down":
+            mm(self.act, self.wd[layer].t(), out=self.lib_out["down"])
+        elif name == "lm_head":
+            mm(self.x, self.wlm[layer % 2].t(), out=self.lib_out["lm_head"])
+
+    def library_us(self, name: str, launches: int, reps: int = 5) -> float:
+        """kernel_us for launch_library: graph replay of back-to-back calls."""
+        nl = 2 if name == "lm_head" else self.L
+        if not hasattr(self, "lib_out"):
+            torch, M, bf16 = self.torch, self.M, self.torch.bfloat16
+            self.lib_out = {n: torch.empty(M, (2 * N if k == "gateup" else N), dtype=bf16, device=self.dev)
+                            for n, (N, K, k) in SHAPES.items()}
+        g = self.capture(lambda i: self.launch_library(name, i % nl), launches)
+        g.replay()
+        t = self.time_graph(g, reps)
+        del g
+        return statistics.median(t) * 1000.0 / launches
+
 
 def _cpu_model() -> str:
     cpu = platform.processor() or platform.machine()
@@ -242,6 +273,30 @@ def cpu_baseline(M: int, seconds: float) -> dict:
             "sample": f"{len(ts)} steps ({total:.1f} s of CPU work; median step) of the M={M} layer workload via "
                       f"torch F.linear/F.silu on CPU (the reference's a @ w.t() baseline path), "
                       f"{t * 1e3:.2f} ms/step, {cpu}"}
+
+
+def cpu_config1(seconds: float) -> dict:
+    """BASELINE configs[0], the reference's own CPU-runnable case: one decode
+    QKV projection on the CPU path, torch F.linear (bf16 in, fp32 accumulate,
+    bf16 out), x [1, 2560] ~N(0, 1) then W [6144, 2560] ~N(0, 0.02) drawn from
+    one generator seeded 0.  Median call of about `seconds` of CPU work (at
+    least 20 calls) after 3 warmups, on this box's host cores."""
+    import torch
+    import torch.nn.functional as F
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 2560, generator=g).to(torch.bfloat16)
+    w = (torch.randn(6144, 2560, generator=g) * 0.02).to(torch.bfloat16)
+    for _ in range(3):
+        F.linear(x, w)
+    ts, total = _timed_steps(lambda: F.linear(x, w), seconds, min_steps=20)
+    t = statistics.median(ts)
+    return {"value": round(alg_bytes("qkv", 1) / t / 1e9, 2), "unit": "GB/s", "us": round(t * 1e6, 1),
+            "cores": torch.get_num_threads(), "kind": "reference",
+            "sample": f"{len(ts)} calls ({total:.1f} s of CPU work; median call) of F.linear(x [1,2560], "
+                      f"W [6144,2560]) bf16, seed 0, {_cpu_model()}"}
 
 
 def cpu_port(M: int, seconds: float) -> dict:
@@ -354,7 +409,7 @@ def traffic_summary(fetch_dir: str, write_dir: str, M: int) -> int:
     return 0
 
 
-def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int = 128) -> dict:
+def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None = None) -> dict:
     """synthetic Qwen3-4B (36 layers, random bf16
     weights ~N(0, 0.02)), B prompts of T uniform-random token ids, prefill, then
     ``steps`` greedy decode steps replayed from one captured HIP graph.
@@ -366,6 +421,9 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int = 128)
 
     log(f"decode: building the synthetic Qwen3-4B (B={B}, prompt {T}, {steps} steps)")
     model = SyntheticModel(Qwen3Config(), "cuda:0", seed=7)
+    # the plan (attention length, cache) covers every timed step: 128 new
+    # tokens (the prefill's and 127 steps) unless more steps are asked for
+    max_new = max(128, steps + 1) if max_new is None else max_new
     plan = DecodePlan(model, B, T, max_new)
     g = torch.Generator(device="cuda:0").manual_seed(11)
     plan.ids.copy_(torch.randint(0, model.cfg.vocab, (B, T), device="cuda:0", generator=g))
@@ -534,11 +592,14 @@ def main() -> int:
         for name in SHAPES:
             n = 8 if name == "lm_head" else 72
             us = wlM.kernel_us(name, n)
+            lib_us = wlM.library_us(name, n)
             gbs = alg_bytes(name, M) / (us * 1e-6) / 1e9
             per_gemm.setdefault(name, {})[f"M{M}"] = {
                 "us": round(us, 3), "GB/s": round(gbs, 1), "frac_peak": round(gbs / PEAK_HBM_GBS, 4),
-                "TFLOP/s": round(alg_flops(name, M) / (us * 1e-6) / 1e12, 3)}
-            log(f"{name:8s} M={M:2d}: {us:8.2f} us  {gbs:7.1f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s)")
+                "TFLOP/s": round(alg_flops(name, M) / (us * 1e-6) / 1e12, 3),
+                "hipblaslt_us": round(lib_us, 3), "vs_hipblaslt": round(lib_us / us, 3)}
+            log(f"{name:8s} M={M:2d}: {us:8.2f} us  {gbs:7.1f} GB/s  ({100 * gbs / PEAK_HBM_GBS:.1f}% of 8 TB/s); "
+                f"hipBLASLt GEMM alone {lib_us:8.2f} us")
 
     sweep = None
     if args.sweep:
@@ -546,11 +607,15 @@ def main() -> int:
         for M in (1, 2, 4, 8, 16, 32, 40, 64):
             wlM = Workload(min(args.layers, 12), M, seed=2)
             for name in SHAPES:
-                us = wlM.kernel_us(name, 8 if name == "lm_head" else 36)
+                n = 8 if name == "lm_head" else 36
+                us = wlM.kernel_us(name, n)
+                lib_us = wlM.library_us(name, n)
                 gbs = alg_bytes(name, M) / (us * 1e-6) / 1e9
                 sweep.setdefault(name, {})[f"M{M}"] = {"us": round(us, 3), "GB/s": round(gbs, 1),
-                                                       "TFLOP/s": round(alg_flops(name, M) / (us * 1e-6) / 1e12, 3)}
-                log(f"sweep {name:8s} M={M:2d}: {us:8.2f} us {gbs:7.1f} GB/s")
+                                                       "TFLOP/s": round(alg_flops(name, M) / (us * 1e-6) / 1e12, 3),
+                                                       "hipblaslt_us": round(lib_us, 3),
+                                                       "vs_hipblaslt": round(lib_us / us, 3)}
+                log(f"sweep {name:8s} M={M:2d}: {us:8.2f} us {gbs:7.1f} GB/s; hipBLASLt {lib_us:8.2f} us")
             keep.append(wlM)
 
     dom = per_gemm["gate_up"][f"M{args.M}"]
@@ -573,12 +638,14 @@ def main() -> int:
     if args.decode_steps > 0:
         decode = decode_benchmark(args.decode_steps)
 
-    cpu = port = None
+    cpu = port = cpu1 = None
     if not args.no_cpu:
         log("timing the CPU baseline")
         cpu = cpu_baseline(args.M, args.cpu_seconds)
         log("timing the C oracle on the CPU")
         port = cpu_port(args.M, args.cpu_seconds / 2)
+        log("timing BASELINE config 1 (QKV, M = 1) on the CPU reference path")
+        cpu1 = cpu_config1(args.cpu_seconds / 4)
 
     line = {
         "metric": METRIC,
@@ -603,6 +670,7 @@ def main() -> int:
         "attention": attention,
         "cpu_baseline": cpu,
         "cpu_port": port,
+        "cpu_config1": cpu1,
         "per_gemm": per_gemm,
     }
     if sweep is not None:

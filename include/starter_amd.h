@@ -259,14 +259,19 @@ int sk_rmsnorm_pre_lm_argmax_bf16(const sk_bf16* x, int64_t ldx, const float* sq
  *   qkv     [B*T, ld_qkv] bf16, rows (b, t): HQ query heads | HKV key heads | HKV value heads
  *   q_norm_w, k_norm_w [D]; cos, sin [rope_rows, D] bf16 (model.py:85-100 tables)
  *   pos     [B] int32 device array: row (b, t) goes to slot pos[b] + t
+ *   depth   NULL: row (b, t) rotates by position pos[b] + t (a chain); else
+ *           [T] int32 device array: it rotates by pos[b] + depth[t] (draft-tree
+ *           rows, siblings sharing a position; rope.py:94-122, the `depth=`
+ *           argument of engine/model.py:204, 369-370)
  *   q_out   [B, HQ, T, D]; k_cache, v_cache [B, HKV, cap, D] (one layer)
- * Slots outside [0, cap) or outside the table are skipped (pos is device data,
- * so the host cannot check it).  No workspace.
+ * Rows whose rotary position is outside the table, and key/value rows whose
+ * slot is outside [0, cap), are skipped (pos and depth are device data, so the
+ * host cannot check them).  No workspace.
  */
 int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w, const sk_bf16* k_norm_w,
                                const sk_bf16* cos, const sk_bf16* sin, int rope_rows, const int32_t* pos,
-                               sk_bf16* q_out, sk_bf16* k_cache, sk_bf16* v_cache, int B, int T, int HQ, int HKV,
-                               int D, int cap, float eps, hipStream_t stream);
+                               const int32_t* depth, sk_bf16* q_out, sk_bf16* k_cache, sk_bf16* v_cache, int B, int T,
+                               int HQ, int HKV, int D, int cap, float eps, hipStream_t stream);
 
 /*
  * sk_decode_attention_bf16: split-K grouped-query flash-decoding with a

@@ -59,7 +59,8 @@ def lib() -> ctypes.CDLL:
         h.oracle_swiglu_scalar.restype = ctypes.c_uint16
         _i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
         h.oracle_qk_norm_rope_cache_bf16.argtypes = [_u16p, _i64, _u16p, _u16p, _u16p, _u16p, _i32p, _u16p, _u16p,
-                                                     _u16p, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float]
+                                                     _u16p, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float,
+                                                     ctypes.c_void_p]
         h.oracle_topk_bf16.argtypes = [_u16p, _i64, _i32, _i32, _i32, _f32p, _i32p]
         h.oracle_decode_attention.argtypes = [_u16p, _u16p, _u16p, _i32p, ctypes.c_void_p, _f32p, _f32p, _i32, _i32,
                                               _i32, _i32, _i32, _i32, ctypes.c_float, _i32]
@@ -172,9 +173,11 @@ def f32_to_bf16_c(f: float) -> int:
 
 def qk_norm_rope_cache(qkv: np.ndarray, qw: np.ndarray, kw: np.ndarray, cos: np.ndarray, sin: np.ndarray,
                        pos: np.ndarray, q_out: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, T: int,
-                       eps: float) -> None:
+                       eps: float, depth: np.ndarray | None = None) -> None:
     """In place: q_out [B, HQ, T, D], k/v_cache [B, HKV, cap, D] at slots pos[b] + t
-    (engine/kernels/rope.py:140-188).  qkv [B*T, (HQ + 2*HKV)*D] bits."""
+    (engine/kernels/rope.py:140-188).  qkv [B*T, (HQ + 2*HKV)*D] bits.  The
+    rotary angle of row (b, t) is that of position pos[b] + t, or with
+    ``depth`` [T] int32 (a draft tree) pos[b] + depth[t] (rope.py:108-111)."""
     qkv = _u16(qkv)
     B, HQ, _, D = q_out.shape
     HKV, cap = k_cache.shape[1], k_cache.shape[2]
@@ -182,10 +185,21 @@ def qk_norm_rope_cache(qkv: np.ndarray, qw: np.ndarray, kw: np.ndarray, cos: np.
         if a.dtype != np.uint16 or not a.flags["C_CONTIGUOUS"]:
             raise TypeError("outputs must be contiguous uint16 arrays")
     pos = np.ascontiguousarray(pos, dtype=np.int32)
-    if pos.min() < 0 or pos.max() + T > min(cap, cos.shape[0]):
-        raise ValueError("slots outside the cache or the rotary table")
+    if pos.min() < 0 or pos.max() + T > cap:
+        raise ValueError("slots outside the cache")
+    dp = None
+    if depth is not None:
+        depth = np.ascontiguousarray(depth, dtype=np.int32)
+        if depth.shape != (T,):
+            raise ValueError("depth must hold one position offset per row t")
+        angles = pos[:, None] + depth[None, :]
+        dp = depth.ctypes.data
+    else:
+        angles = pos[:, None] + np.arange(T, dtype=np.int32)[None, :]
+    if angles.min() < 0 or angles.max() >= cos.shape[0]:
+        raise ValueError("rotary positions outside the table")
     lib().oracle_qk_norm_rope_cache_bf16(qkv, qkv.shape[1], _u16(qw), _u16(kw), _u16(cos), _u16(sin), pos, q_out,
-                                         k_cache, v_cache, B, T, HQ, HKV, D, cap, eps)
+                                         k_cache, v_cache, B, T, HQ, HKV, D, cap, eps, dp)
 
 
 def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, pos: np.ndarray,

@@ -239,7 +239,9 @@ void oracle_lm_argmax_bf16(const uint16_t* A, int64_t lda, const uint16_t* W, in
  * qkv [B*T, ld] rows (b, t) hold HQ query heads, HKV key heads, HKV value
  * heads of width D; query heads go to q_out [B, HQ, T, D]; key heads
  * (normalised, rotated) and value heads (raw) to the caches [B, HKV, cap, D]
- * at slot pos[b] + t, which is also the rotary table row. */
+ * at slot pos[b] + t.  The rotary table row is that slot for a chain
+ * (depth == NULL), or pos[b] + depth[t] for a draft tree, whose siblings
+ * share one absolute position (rope.py:94-122, the DEPTH branch at 108-111). */
 static void norm_rope_head(const uint16_t* x, const uint16_t* w, const uint16_t* c, const uint16_t* s, int D,
                            float eps, uint16_t* o) {
   double sq = 0.0;
@@ -260,13 +262,14 @@ static void norm_rope_head(const uint16_t* x, const uint16_t* w, const uint16_t*
 void oracle_qk_norm_rope_cache_bf16(const uint16_t* qkv, int64_t ld, const uint16_t* qw, const uint16_t* kw,
                                     const uint16_t* cosT, const uint16_t* sinT, const int32_t* pos, uint16_t* q_out,
                                     uint16_t* k_cache, uint16_t* v_cache, int B, int T, int HQ, int HKV, int D,
-                                    int cap, float eps) {
+                                    int cap, float eps, const int32_t* depth) {
   for (int b = 0; b < B; ++b)
     for (int t = 0; t < T; ++t) {
       const uint16_t* row = qkv + (int64_t)(b * T + t) * ld;
       const int slot = pos[b] + t;
-      const uint16_t* c = cosT + (int64_t)slot * D;
-      const uint16_t* s = sinT + (int64_t)slot * D;
+      const int angle = depth ? pos[b] + depth[t] : slot;
+      const uint16_t* c = cosT + (int64_t)angle * D;
+      const uint16_t* s = sinT + (int64_t)angle * D;
       for (int h = 0; h < HQ; ++h)
         norm_rope_head(row + (int64_t)h * D, qw, c, s, D, eps, q_out + ((int64_t)(b * HQ + h) * T + t) * D);
       for (int h = 0; h < HKV; ++h) {

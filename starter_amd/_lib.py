@@ -121,7 +121,7 @@ _SIGNATURES = {
                                                  _i32, _i32, _cfgp, _p, _sz, _p]),
     "sk_rmsnorm_pre_lm_argmax_bf16": (_i32, [_p, _i64, _p, _p, ctypes.c_float, _p, _i64, _p, _p, _i32, _i32, _i32,
                                              _cfgp, _p, _sz, _p]),
-    "sk_qk_norm_rope_cache_bf16": (_i32, [_p, _i64, _p, _p, _p, _p, _i32, _p, _p, _p, _p,
+    "sk_qk_norm_rope_cache_bf16": (_i32, [_p, _i64, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _p,
                                           _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p]),
     "sk_decode_attention_workspace_bytes": (_sz, [_i32] * 8),
     "sk_topk_bf16": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _p, _p]),

@@ -77,17 +77,28 @@ def _run(cmd: list[str]) -> list[tuple[str, int]]:
     return spills
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
-    """Compile every HIP translation unit and link the shared library."""
+def build(jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile every HIP translation unit and link the shared library.
+    ``incremental``: recompile only the units whose object is older than their
+    source or any header (a development shortcut; the default rebuilds all)."""
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found; the library needs ROCm's hipcc to build")
     BUILD.mkdir(parents=True, exist_ok=True)
     LIB.parent.mkdir(parents=True, exist_ok=True)
     jobs = jobs or min(16, os.cpu_count() or 4)
     units = _units()
+    headers = max(p.stat().st_mtime for p in [*CSRC.glob("*.hpp"), *(ROOT / "include").glob("*.h")])
+    spill_file = BUILD / "spills_by_unit.txt"
+    old_spills: dict[str, list[tuple[str, int]]] = {}
+    if incremental and spill_file.exists():
+        for line in spill_file.read_text().splitlines():
+            unit, name, n = line.split("\t")
+            old_spills.setdefault(unit, []).append((name, int(n)))
 
     def compile_one(u):
         src, defs, obj = u
+        if incremental and obj.exists() and obj.stat().st_mtime > max(src.stat().st_mtime, headers):
+            return obj, old_spills.get(obj.name, [])
         cmd = [HIPCC, *COMMON, *defs, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -97,6 +108,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         done = list(ex.map(compile_one, units))
     objs = [o for o, _ in done]
     spilled = [s for _, sp in done for s in sp]
+    spill_file.write_text("".join(f"{o.name}\t{n}\t{c}\n" for o, sp in done for n, c in sp))
     (BUILD / "spills.txt").write_text("".join(f"{n}\t{c}\n" for n, c in spilled))
     if spilled:
         print(f"note: {len(spilled)} kernel instances spill VGPRs (list in {BUILD / 'spills.txt'})", file=sys.stderr)
@@ -110,5 +122,5 @@ if __name__ == "__main__":
     import time
 
     t0 = time.time()
-    out = build(verbose="-v" in sys.argv)
+    out = build(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
     print(f"built {out} in {time.time() - t0:.1f}s")

@@ -242,6 +242,9 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   const int tiles_per = c.grid > 0 ? cdiv(pl->nrb, c.grid / c.split) : 1;
   pl->lds = plan_lds(*pl, M, tiles_per);
   if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
+  // A derived grid holds at most kMaxGrid workgroups per K split, so every
+  // workgroup may have to stage cdiv(nrb, kMaxGrid) tiles.
+  if (c.grid == 0 && plan_lds(*pl, M, cdiv(pl->nrb, kMaxGrid)) > kMaxLds) return SK_ERR_CONFIG;
   return SK_OK;
 }
 
@@ -512,8 +515,13 @@ int bind_plan(Plan* pl, int num_cu, int* grid) {
     if (per_split > kMaxGrid) per_split = kMaxGrid;
     int tiles_per = cdiv(pl->nrb, per_split);
     if (epi_base(pl->epi) != sk::EPI_ARGMAX) {
-      const size_t budget = pl->pre_lds + pl->parts_lds > kPrefLds ? kMaxLds : kPrefLds;
-      while (tiles_per > 1 && plan_lds(*pl, 0, tiles_per) > budget) --tiles_per;
+      // Never below the tiles per workgroup that keep the grid within
+      // kMaxGrid (lm_head logits: 9496 tiles); past the preferred budget the
+      // staging may use the whole LDS.
+      const int min_tiles = cdiv(pl->nrb, kMaxGrid);
+      const size_t budget = pl->pre_lds + pl->parts_lds + (size_t)min_tiles * pl->stage_elem > kPrefLds ? kMaxLds
+                                                                                                      : kPrefLds;
+      while (tiles_per > min_tiles && plan_lds(*pl, 0, tiles_per) > budget) --tiles_per;
     }
     per_split = cdiv(pl->nrb, tiles_per);
     if (per_split > kMaxGrid) return SK_ERR_CONFIG;

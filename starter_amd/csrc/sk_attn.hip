@@ -26,7 +26,11 @@ constexpr int HEAD_D = 128;   // head width of Qwen3 (the only one compiled)
 // (row, head group): 4 waves, heads 4*hg .. 4*hg+3 of projection row (b, t);
 // heads < HQ are query heads (to q_out), then HKV key heads (normalised and
 // rotated into k_cache at slot pos[b] + t, their value heads copied raw to
-// v_cache).  A slot outside [0, cap) or outside the rotary table is skipped.
+// v_cache).  The rotary angle is that of position pos[b] + t (a chain), or of
+// pos[b] + depth[t] when depth is given (draft-tree rows, whose siblings share
+// one absolute position: rope.py:94-122).  A row whose rotary position is
+// outside the table, or a key/value row whose slot is outside [0, cap), is
+// skipped.
 // ---------------------------------------------------------------------------
 struct RopeArgs {
   const uint16_t* qkv;
@@ -37,6 +41,7 @@ struct RopeArgs {
   const uint16_t* sin;
   int rope_rows;
   const int32_t* pos;
+  const int32_t* depth;   // [T] rotary position offsets, or nullptr (chain: t)
   uint16_t* q_out;
   uint16_t* k_cache;
   uint16_t* v_cache;
@@ -66,13 +71,15 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(RopeArgs a) {
   const int lane = threadIdx.x & 63;
   if (head >= a.HQ + a.HKV) return;                 // wave-uniform
   const int b = row / a.T, t = row - (row / a.T) * a.T;
-  const int slot = a.pos[b] + t;
-  if (slot < 0 || slot >= a.rope_rows) return;
+  const int p0 = a.pos[b];
+  const int slot = p0 + t;
+  const int angle = a.depth ? p0 + a.depth[t] : slot;
+  if (angle < 0 || angle >= a.rope_rows) return;
   const bool is_q = head < a.HQ;
-  if (!is_q && slot >= a.cap) return;
+  if (!is_q && (slot < 0 || slot >= a.cap)) return;
   const uint16_t* src = a.qkv + (int64_t)row * a.ld_qkv + (int64_t)head * HEAD_D;
   uint16_t o1, o2;
-  rope_head(src, is_q ? a.qw : a.kw, a.cos + (int64_t)slot * HEAD_D, a.sin + (int64_t)slot * HEAD_D, a.eps, lane,
+  rope_head(src, is_q ? a.qw : a.kw, a.cos + (int64_t)angle * HEAD_D, a.sin + (int64_t)angle * HEAD_D, a.eps, lane,
             o1, o2);
   if (is_q) {
     uint16_t* dst = a.q_out + ((int64_t)(b * a.HQ + head) * a.T + t) * HEAD_D;
@@ -544,8 +551,8 @@ extern "C" {
 
 int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w, const sk_bf16* k_norm_w,
                                const sk_bf16* cos, const sk_bf16* sin, int rope_rows, const int32_t* pos,
-                               sk_bf16* q_out, sk_bf16* k_cache, sk_bf16* v_cache, int B, int T, int HQ, int HKV,
-                               int D, int cap, float eps, hipStream_t stream) {
+                               const int32_t* depth, sk_bf16* q_out, sk_bf16* k_cache, sk_bf16* v_cache, int B, int T,
+                               int HQ, int HKV, int D, int cap, float eps, hipStream_t stream) {
   if (B < 0 || T < 0 || HQ < 1 || HKV < 1 || cap < 1 || rope_rows < 1 || D != sk::HEAD_D) return SK_ERR_SHAPE;
   if (ld_qkv < (int64_t)(HQ + 2 * HKV) * D) return SK_ERR_SHAPE;
   if ((long)B * T > 0x7FFFFFFFL) return SK_ERR_SHAPE;
@@ -562,6 +569,7 @@ int sk_qk_norm_rope_cache_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16
   a.sin = sin;
   a.rope_rows = rope_rows;
   a.pos = pos;
+  a.depth = depth;
   a.q_out = q_out;
   a.k_cache = k_cache;
   a.v_cache = v_cache;

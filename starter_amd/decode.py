@@ -163,6 +163,7 @@ class DecodePlan:
             self.ws_gu = K._workspace(K.SK_OP_PRE_GATEUP, B, I, H, None, dev)
             self.ws_lm = K._workspace(K.SK_OP_PRE_LM_ARGMAX, B, cfg.vocab, H, None, dev)
         self.g_decode = None
+        self.steps_done = 0   # decode steps since the last prefill (host-side count)
 
     # -- prefill (torch GEMMs + SDPA, this package's norm/rope/swiglu/argmax) --
     @torch.inference_mode()
@@ -193,6 +194,7 @@ class DecodePlan:
         ids, _ = K.argmax(logits)
         self.tok.copy_(ids)
         self.pos.fill_(T)
+        self.steps_done = 0
 
     # -- one decode step: run_layers (engine/model.py:182-210) + greedy token --
     def decode(self) -> None:
@@ -270,10 +272,18 @@ class DecodePlan:
         self.g_decode = g
 
     def step(self) -> None:
+        """One decode step (the captured graph when there is one).  Step s after
+        the prefill attends over T + s keys; the attention and the cache were
+        planned for T + max_new, so a step past max_new raises instead of
+        silently dropping keys."""
+        if self.steps_done >= self.max_new:
+            raise RuntimeError(f"decode step {self.steps_done + 1} exceeds the planned max_new = {self.max_new} "
+                               f"(attention planned for {self.T + self.max_new} keys)")
         if self.g_decode is None:
             self.decode()
         else:
             self.g_decode.replay()
+        self.steps_done += 1
 
     @torch.inference_mode()
     def generate(self, ids: torch.Tensor, max_new: int | None = None) -> torch.Tensor:
@@ -301,10 +311,12 @@ def time_decode(plan: DecodePlan, steps: int) -> dict:
     prefill_s = time.perf_counter() - t0
     if plan.g_decode is None:
         plan.capture()
+    if steps > plan.max_new:
+        raise ValueError(f"{steps} decode steps exceed the plan's max_new = {plan.max_new}")
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(steps):
-        plan.g_decode.replay()
+        plan.step()
     b.record()
     b.synchronize()
     ms = a.elapsed_time(b)

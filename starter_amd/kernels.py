@@ -87,6 +87,33 @@ def _ws_args(ws: torch.Tensor | None):
     return (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
 
 
+def _argmax_outputs(ids: torch.Tensor | None, maxv: torch.Tensor | None, M: int, device):
+    """The (ids, maxv) outputs of an argmax call: allocated when not given, else
+    checked to be what the kernel writes (int64 / float32, >= M contiguous
+    elements on the call's device), so a caller-supplied buffer can never be
+    written past its end."""
+    if ids is None:
+        ids = torch.empty((M,), dtype=torch.int64, device=device)
+    if maxv is None:
+        maxv = torch.empty((M,), dtype=torch.float32, device=device)
+    _need(ids.dtype == torch.int64, f"ids must be int64, got {ids.dtype}")
+    _need(maxv.dtype == torch.float32, f"maxv must be float32, got {maxv.dtype}")
+    _need(ids.is_contiguous() and maxv.is_contiguous(), "ids and maxv must be contiguous")
+    _need(ids.numel() >= M and maxv.numel() >= M, f"ids and maxv need at least M = {M} elements")
+    _need(ids.device == torch.device(device) and maxv.device == torch.device(device),
+          "ids and maxv must be on the device of the activations")
+    return ids, maxv
+
+
+def _vec(t: torch.Tensor, name: str, dtype: torch.dtype, numel: int, exact: bool = True) -> None:
+    """A contiguous 1-D parameter vector (norm gains, positions) of the right dtype and length."""
+    _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+    _need(t.numel() == numel if exact else t.numel() >= numel,
+          f"{name} must have {'' if exact else 'at least '}{numel} elements, got {t.numel()}")
+    _need(t.is_cuda, f"{name} must be a ROCm device tensor")
+
+
 def _config(config: SkConfig | None, kw: dict) -> SkConfig | None:
     if config is not None and kw:
         raise ValueError("pass either config= or individual config fields, not both")
@@ -152,8 +179,7 @@ def lm_argmax(a: torch.Tensor, w: torch.Tensor, config: SkConfig | None = None, 
     M, K = a.shape
     V = w.shape[0]
     _need(w.shape[1] == K, "K mismatch")
-    ids = torch.empty((M,), dtype=torch.int64, device=a.device) if ids is None else ids
-    maxv = torch.empty((M,), dtype=torch.float32, device=a.device) if maxv is None else maxv
+    ids, maxv = _argmax_outputs(ids, maxv, M, a.device)
     if ws is None:
         ws = _workspace(SK_OP_LM_ARGMAX, M, V, K, config, a.device)
     _device_guard(a)
@@ -232,8 +258,7 @@ def rmsnorm_lm_argmax(x: torch.Tensor, y: torch.Tensor, w_norm: torch.Tensor, ep
     M, K = x.shape
     V = w.shape[0]
     _need(w.shape[1] == K, "K mismatch")
-    ids = torch.empty((M,), dtype=torch.int64, device=x.device) if ids is None else ids
-    maxv = torch.empty((M,), dtype=torch.float32, device=x.device) if maxv is None else maxv
+    ids, maxv = _argmax_outputs(ids, maxv, M, x.device)
     if ws is None:
         ws = _workspace(SK_OP_RMSNORM_LM_ARGMAX, M, V, K, config, x.device)
     _device_guard(x)
@@ -354,8 +379,7 @@ def rmsnorm_pre_lm_argmax(x: torch.Tensor, sq: torch.Tensor, w_norm: torch.Tenso
     M, K = x.shape
     V = w.shape[0]
     _need(w.shape[1] == K, "K mismatch")
-    ids = torch.empty((M,), dtype=torch.int64, device=x.device) if ids is None else ids
-    maxv = torch.empty((M,), dtype=torch.float32, device=x.device) if maxv is None else maxv
+    ids, maxv = _argmax_outputs(ids, maxv, M, x.device)
     if ws is None:
         ws = _workspace(SK_OP_PRE_LM_ARGMAX, M, V, K, config, x.device)
     _device_guard(x)
@@ -433,8 +457,15 @@ def swiglu(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 # Attention side of the decode step
 # ---------------------------------------------------------------------------
 
-def _i32_dev(t: torch.Tensor, name: str) -> None:
-    _need(t.is_cuda and t.dtype == torch.int32 and t.is_contiguous(), f"{name} must be a contiguous int32 device tensor")
+def _rope_params(q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                 D: int) -> None:
+    """Per-head norm gains bf16 [D]; rotary tables bf16 [rows, D], contiguous."""
+    _vec(q_norm_w, "q_norm_w", BF16, D)
+    _vec(k_norm_w, "k_norm_w", BF16, D)
+    _need(cos.dtype == BF16 and sin.dtype == BF16, "rope tables must be bf16")
+    _need(cos.dim() == 2 and cos.shape == sin.shape and cos.shape[1] == D, "rope tables must be [rows, D]")
+    _need(cos.is_contiguous() and sin.is_contiguous() and cos.is_cuda and sin.is_cuda,
+          "rope tables must be contiguous device tensors")
 
 
 def qk_norm_rope_cache(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
@@ -445,24 +476,28 @@ def qk_norm_rope_cache(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torc
 
     qkv [B*T, (HQ + 2*HKV)*D] rows (b, t); pos [B] int32 (row (b, t) -> slot
     pos[b] + t); q_out [B, HQ, T, D]; k_cache / v_cache [B, HKV, cap, D] (one
-    layer).  ``fused`` is accepted for signature compatibility (there is one
-    launch either way); draft-tree depths are not supported."""
-    if depth is not None:
-        raise NotImplementedError("draft-tree rotary positions (depth=) are not supported")
+    layer).  ``depth`` [T] int32 (draft-tree rows): row (b, t) still goes to
+    slot pos[b] + t but rotates by position pos[b] + depth[t]
+    (rope.py:94-122; engine/model.py:369-370).  ``fused`` is accepted for
+    signature compatibility (there is one launch either way)."""
     _mat(qkv, "qkv")
     B, HQ, T_, D = q_out.shape
     _need(T_ == T, "q_out must be [B, HQ, T, D]")
     HKV, cap = k_cache.shape[1], k_cache.shape[2]
     _need(q_out.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous outputs")
+    _need(q_out.dtype == BF16 and k_cache.dtype == BF16 and v_cache.dtype == BF16, "q_out and caches must be bf16")
     _need(k_cache.shape == v_cache.shape and k_cache.shape[0] == B and k_cache.shape[3] == D, "cache shapes")
     _need(qkv.shape[0] == B * T and qkv.shape[1] >= (HQ + 2 * HKV) * D, "qkv shape")
-    _need(cos.shape == sin.shape and cos.shape[1] == D and cos.is_contiguous() and sin.is_contiguous(), "rope tables")
-    _i32_dev(pos, "pos")
+    _rope_params(q_norm_w, k_norm_w, cos, sin, D)
+    _vec(pos, "pos", torch.int32, B, exact=False)
+    if depth is not None:
+        _vec(depth, "depth", torch.int32, T)
     _device_guard(qkv)
     check(lib().sk_qk_norm_rope_cache_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
                                            cos.data_ptr(), sin.data_ptr(), cos.shape[0], pos.data_ptr(),
-                                           q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), B, T, HQ, HKV,
-                                           D, cap, float(eps), _stream(qkv)), "sk_qk_norm_rope_cache_bf16")
+                                           depth.data_ptr() if depth is not None else None, q_out.data_ptr(),
+                                           k_cache.data_ptr(), v_cache.data_ptr(), B, T, HQ, HKV, D, cap, float(eps),
+                                           _stream(qkv)), "sk_qk_norm_rope_cache_bf16")
 
 
 class DecodeAttention:
@@ -496,8 +531,9 @@ class DecodeAttention:
         _need(q.shape == (B, HQ, R, D) and q.is_contiguous() and q.dtype == BF16, "q must be [B, HQ, R, D] bf16")
         _need(k_cache.shape == (B, HKV, cap, D) and v_cache.shape == k_cache.shape, "cache shapes")
         _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous caches")
-        _need(out.shape == (B, R, HQ, D) and out.is_contiguous(), "out must be [B, R, HQ, D]")
-        _i32_dev(pos, "pos")
+        _need(out.shape == (B, R, HQ, D) and out.is_contiguous() and out.dtype == BF16, "out must be [B, R, HQ, D] bf16")
+        _need(k_cache.dtype == BF16 and v_cache.dtype == BF16, "caches must be bf16")
+        _vec(pos, "pos", torch.int32, B, exact=False)
         if self.tree:
             _need(tree is not None and tree.is_cuda and tree.dtype == torch.int64 and tree.numel() == R,
                   "tree=True needs tree [R] int64 on the device")
@@ -523,9 +559,10 @@ class DecodeAttention:
         _need(qkv.shape[0] == B * R and qkv.shape[1] >= (HQ + 2 * HKV) * D, "qkv must be [B*R, (HQ+2*HKV)*D]")
         _need(k_cache.shape == (B, HKV, cap, D) and v_cache.shape == k_cache.shape, "cache shapes")
         _need(k_cache.is_contiguous() and v_cache.is_contiguous(), "contiguous caches")
-        _need(out.shape == (B, R, HQ, D) and out.is_contiguous(), "out must be [B, R, HQ, D]")
-        _need(cos.shape == sin.shape and cos.shape[1] == D and cos.is_contiguous() and sin.is_contiguous(), "rope tables")
-        _i32_dev(pos, "pos")
+        _need(out.shape == (B, R, HQ, D) and out.is_contiguous() and out.dtype == BF16, "out must be [B, R, HQ, D] bf16")
+        _need(k_cache.dtype == BF16 and v_cache.dtype == BF16, "caches must be bf16")
+        _rope_params(q_norm_w, k_norm_w, cos, sin, D)
+        _vec(pos, "pos", torch.int32, B, exact=False)
         _device_guard(qkv)
         wp, wn = _ws_args(self.ws)
         check(lib().sk_decode_attention_rope_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(),

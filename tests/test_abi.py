@@ -369,3 +369,53 @@ def test_fused_attention_argument_validation_precedes_any_device_work():
     assert _attn_rope(lib, out=Q0 + 64, ws=FAKE, wsb=need) == SK_ERR_ALIAS     # output inside the projection rows
     assert _attn_rope(lib, vc=KC0 + 128, ws=FAKE, wsb=need) == SK_ERR_ALIAS    # overlapping caches
     assert _attn_rope(lib, B=0, qkv=None, kc=None, vc=None, out=None) == SK_OK
+
+
+def test_argmax_outputs_are_checked_before_launch():
+    """Caller-supplied ids / maxv buffers of the argmax entry points must be
+    what the kernel writes (int64 / float32, >= M contiguous elements on the
+    activations' device), else the call raises before reaching the library."""
+    import torch
+
+    from starter_amd import kernels as K
+
+    M = 4
+    ids, maxv = K._argmax_outputs(None, None, M, "cpu")
+    assert ids.dtype == torch.int64 and maxv.dtype == torch.float32 and ids.numel() == maxv.numel() == M
+    good_i, good_v = torch.empty(M, dtype=torch.int64), torch.empty(M, dtype=torch.float32)
+    assert K._argmax_outputs(good_i, good_v, M, "cpu")[0] is good_i
+    bad = [
+        (torch.empty(M, dtype=torch.int32), good_v),            # ids int32: 8-byte stores would overrun
+        (good_i, torch.empty(M, dtype=torch.float16)),          # maxv not float32
+        (torch.empty(M - 1, dtype=torch.int64), good_v),        # too short
+        (good_i, torch.empty(M - 1, dtype=torch.float32)),
+        (torch.empty(2 * M, dtype=torch.int64)[::2], good_v),   # not contiguous
+    ]
+    for i, v in bad:
+        with pytest.raises(ValueError):
+            K._argmax_outputs(i, v, M, "cpu")
+    with pytest.raises(ValueError):
+        K._argmax_outputs(good_i, good_v, M, "meta")             # not on the activations' device
+
+
+def test_rope_and_attention_parameters_are_checked_before_launch():
+    """Norm gains bf16 [D], rotary tables bf16 [rows, D], positions int32 with at
+    least B entries and depths int32 [T]: anything else raises before launch
+    (the kernels read w[0..D-1], pos[b] and depth[t] unconditionally)."""
+    import torch
+
+    from starter_amd import kernels as K
+
+    D = 128
+    w = torch.ones(D, dtype=torch.bfloat16)
+    tab = torch.zeros(16, D, dtype=torch.bfloat16)
+    for args in [(w.float(), w, tab, tab), (w, w[:64], tab, tab), (w, w, tab.float(), tab.float()),
+                 (w, w, tab, tab[:, :64].contiguous()), (w, w, tab[:, :64], tab[:, :64])]:
+        with pytest.raises(ValueError):
+            K._rope_params(*args, D)
+    for t, n, exact in [(torch.zeros(3, dtype=torch.int32), 4, False), (torch.zeros(4, dtype=torch.int64), 4, False),
+                        (torch.zeros(5, dtype=torch.int32), 4, True), (torch.zeros(8, dtype=torch.int32)[::2], 4, True)]:
+        with pytest.raises(ValueError):
+            K._vec(t, "pos", torch.int32, n, exact=exact)
+    with pytest.raises(ValueError, match="device"):
+        K._vec(torch.zeros(4, dtype=torch.int32), "pos", torch.int32, 4, exact=False)   # right shape, host memory

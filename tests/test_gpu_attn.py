@@ -72,6 +72,85 @@ def test_qk_norm_rope_cache_matches_oracle(B, T, HQ, HKV, starts):
     assert np.array_equal(bits(vc), vc_o), "value rows are copied raw; untouched slots stay zero"
 
 
+@pytest.mark.parametrize("B,depth", [
+    (4, (0, 1, 1, 2, 2)),                 # root, two children, two grandchildren (draft tree, R = 5)
+    (16, (0, 1, 2, 3)),                   # a chain given as depths: equals the chain call
+    (3, (0, 1, 1, 1, 2, 3, 2, 4)),        # R = 8 rows, siblings at several depths
+])
+def test_qk_norm_rope_cache_tree_depth_matches_oracle(B, depth):
+    """Draft-tree rows (engine/kernels/rope.py:94-122, the depth= argument of
+    engine/model.py:204, 369-370): row t goes to cache slot pos + t and rotates
+    by position pos + depth[t]; Qwen3-4B heads, per-sequence positions."""
+    T, HQ, HKV, eps = len(depth), 32, 8, 1e-6
+    starts = np.array([700 + 37 * b for b in range(B)], np.int32)
+    CAP = int(starts.max()) + T + 3
+    g = torch.Generator().manual_seed(B * 7 + T)
+    cos, sin = rope_tables_cpu(D, 1e6, CAP)
+    qkv = randn_bf16((B * T, (HQ + 2 * HKV) * D), 1.0, g)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    dep = np.array(depth, np.int32)
+    q_o = np.zeros((B, HQ, T, D), np.uint16)
+    kc_o = np.zeros((B, HKV, CAP, D), np.uint16)
+    vc_o = np.zeros_like(kc_o)
+    oracle.qk_norm_rope_cache(bits(qkv), bits(qw), bits(kw), bits(cos), bits(sin), starts, q_o, kc_o, vc_o, T, eps,
+                              depth=dep)
+    q_out = torch.empty(B, HQ, T, D, dtype=BF16, device=DEV)
+    kc = torch.zeros(B, HKV, CAP, D, dtype=BF16, device=DEV)
+    vc = torch.zeros_like(kc)
+    args = (qkv.to(DEV), qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), torch.from_numpy(starts).to(DEV))
+    K.qk_norm_rope_cache(*args, q_out, kc, vc, T, eps, depth=torch.from_numpy(dep).to(DEV))
+    torch.cuda.synchronize()
+    _check_rope(q_out, q_o, "q (tree depth)")
+    _check_rope(kc, kc_o, "k (tree depth)")
+    assert np.array_equal(bits(vc), vc_o), "value rows go to slots pos + t"
+    if tuple(depth) == tuple(range(T)):   # the chain given as depths: bit for bit the chain call
+        q2, kc2, vc2 = torch.empty_like(q_out), torch.zeros_like(kc), torch.zeros_like(vc)
+        K.qk_norm_rope_cache(*args, q2, kc2, vc2, T, eps)
+        torch.cuda.synchronize()
+        assert torch.equal(q2, q_out) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
+
+
+def test_tree_verify_rope_then_tree_attention_matches_oracle():
+    """The reference's draft-tree verify pair (engine/model.py:203-205 with
+    depth= and tree masks): rotary step with per-row depths, then attention
+    with the ancestor masks of the same tree, against the oracle's pair."""
+    B, HQ, HKV, eps = 4, 32, 8, 1e-6
+    parent = [-1, 0, 0, 1, 2]
+    depth = np.array([0, 1, 1, 2, 2], np.int32)
+    R = len(parent)
+    starts = np.array([500, 517, 640, 901], np.int32)
+    CAP = 1024
+    g = torch.Generator().manual_seed(77)
+    cos, sin = rope_tables_cpu(D, 1e6, CAP)
+    qkv = randn_bf16((B * R, (HQ + 2 * HKV) * D), 1.0, g)
+    qw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    kw = (1 + 0.1 * torch.randn(D, generator=g)).to(BF16)
+    k0 = randn_bf16((B, HKV, CAP, D), 1.0, g)
+    v0 = randn_bf16((B, HKV, CAP, D), 1.0, g)
+    tree = np.array(K.ancestor_masks(parent), np.int64)
+    q_o = np.zeros((B, HQ, R, D), np.uint16)
+    kc_o, vc_o = bits(k0).copy(), bits(v0).copy()
+    oracle.qk_norm_rope_cache(bits(qkv), bits(qw), bits(kw), bits(cos), bits(sin), starts, q_o, kc_o, vc_o, R, eps,
+                              depth=depth)
+    ref = oracle.decode_attention(q_o, kc_o, vc_o, starts, 1.0 / np.sqrt(D), with_abs=True, tree=tree)
+
+    q = torch.empty(B, HQ, R, D, dtype=BF16, device=DEV)
+    kc, vc = k0.to(DEV), v0.to(DEV)
+    posd = torch.from_numpy(starts).to(DEV)
+    K.qk_norm_rope_cache(qkv.to(DEV), qw.to(DEV), kw.to(DEV), cos.to(DEV), sin.to(DEV), posd, q, kc, vc, R, eps,
+                         depth=torch.from_numpy(depth).to(DEV))
+    attn = K.DecodeAttention(B, HQ, HKV, D, CAP, DEV, R=R, tree=True)
+    out = torch.empty(B, R, HQ, D, dtype=BF16, device=DEV)
+    attn(q, kc, vc, posd, out, torch.from_numpy(tree).to(DEV))
+    torch.cuda.synchronize()
+    _check_rope(q, q_o, "tree q")
+    _check_rope(kc, kc_o, "tree k cache")
+    # attention against the oracle's attention over the oracle's own rotated rows
+    # (at most 0.2% of q/k elements may differ by one bf16 ulp, see _check_rope)
+    _check_attention(out, ref, "tree verify attention")
+
+
 def test_qk_norm_rope_cache_skips_slots_outside_the_cache():
     """pos is device data: a slot beyond the cache or the rotary table is
     skipped (no write, no fault), the in-range rows are still written."""

@@ -24,7 +24,7 @@ import torch
 import oracle
 from starter_amd import kernels as K
 from starter_amd._lib import SK_ERR_ALIAS, SK_ERR_SHAPE, SK_OP_RESID_GEMM, SkError, default_config
-from tests._util import BF16, assert_parity, bits, check_argmax_rows, from_bits, randn_bf16
+from tests._util import BF16, assert_gateup_parity, assert_parity, bits, check_argmax_rows, from_bits, randn_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -169,9 +169,23 @@ def test_rmsnorm_pre_gemm_random_against_oracle(M):
     assert_parity(got, from_bits(oracle.gemm(h, bits(w))), f"pre gemm M={M}")
 
 
-def test_rmsnorm_pre_lm_argmax_random_against_oracle():
-    M, V = 8, 151936
-    x, wn, w = _rand((M, H), 60), _gain(61), _rand((V, H), 62, 0.02)
+@pytest.mark.parametrize("M", [1, 5, 16])
+def test_rmsnorm_pre_gateup_random_against_oracle(M):
+    """The gate/up consumer on random residual rows (M = 16 is the decode
+    step's batch) against the oracle's add_rmsnorm + gate/up + SwiGLU."""
+    I = 9728
+    x, wn, wgu = _rand((M, H), 55 + M), _gain(155), _rand((2 * I, H), 56, 0.02)
+    wgud = wgu.to(DEV)
+    got = K.rmsnorm_pre_gateup_swiglu(x.to(DEV), _sq_of(x), wn.to(DEV), EPS, wgud[:I], wgud[I:])
+    torch.cuda.synchronize()
+    _, h = oracle.add_rmsnorm(bits(x), np.zeros_like(bits(x)), bits(wn), EPS)
+    assert_gateup_parity(got, h, bits(wgu[:I]), bits(wgu[I:]), f"pre gateup M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_rmsnorm_pre_lm_argmax_random_against_oracle(M):
+    V = 151936
+    x, wn, w = _rand((M, H), 60 + M), _gain(61), _rand((V, H), 62, 0.02)
     ids, mv = K.rmsnorm_pre_lm_argmax(x.to(DEV), _sq_of(x), wn.to(DEV), EPS, w.to(DEV))
     _, h = oracle.add_rmsnorm(bits(x), np.zeros_like(bits(x)), bits(wn), EPS)
     o_ids, o_max = oracle.lm_argmax(h, bits(w))

@@ -324,8 +324,9 @@ def rope_tables_cpu(D: int, theta: float, max_pos: int):
     return emb.cos().to(BF16).contiguous(), emb.sin().to(BF16).contiguous()
 
 
-def _torch_rope_reference(qkv, qw, kw, cos, sin, start, B, T, HQ, HKV, D, eps):
-    """The reference test's composition (tests/test_kernels.py:11-19, 45-53) on the CPU."""
+def _torch_rope_reference(qkv, qw, kw, cos, sin, start, B, T, HQ, HKV, D, eps, positions=None):
+    """The reference test's composition (tests/test_kernels.py:11-19, 45-53) on the CPU.
+    ``positions`` [T]: the rotary position of each row (default start + t)."""
     def ref_rmsnorm(x, w):
         h = x.float()
         h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
@@ -338,8 +339,10 @@ def _torch_rope_reference(qkv, qw, kw, cos, sin, start, B, T, HQ, HKV, D, eps):
     q = qkv[:, : HQ * D].view(B, T, HQ, D)
     k = qkv[:, HQ * D:(HQ + HKV) * D].view(B, T, HKV, D)
     v = qkv[:, (HQ + HKV) * D:].view(B, T, HKV, D)
-    c = cos[start:start + T][None, :, None, :]
-    s = sin[start:start + T][None, :, None, :]
+    if positions is None:
+        positions = torch.arange(start, start + T)
+    c = cos[positions][None, :, None, :]
+    s = sin[positions][None, :, None, :]
     qn, kn = ref_rmsnorm(q, qw), ref_rmsnorm(k, kw)
     q_ref = ((qn * c) + (rotate_half(qn) * s)).transpose(1, 2)
     k_ref = ((kn * c) + (rotate_half(kn) * s)).transpose(1, 2)
@@ -390,6 +393,78 @@ def test_oracle_rope_position_zero_is_norm_only():
     r = 1.0 / torch.sqrt((x * x).mean() + eps)
     y = (qw.float() * (x * r).float().to(BF16).float()).to(BF16)
     assert np.array_equal(q_out[0, 0, 0], bits(y))
+
+
+def _rope_inputs(B, T, HQ, HKV, cap, seed, theta=1e6):
+    g = torch.Generator().manual_seed(seed)
+    cos, sin = rope_tables_cpu(128, theta, cap)
+    qkv = randn_bf16((B * T, (HQ + 2 * HKV) * 128), 1.0, g)
+    qw = (1 + 0.1 * torch.randn(128, generator=g)).to(BF16)
+    kw = (1 + 0.1 * torch.randn(128, generator=g)).to(BF16)
+    return qkv, qw, kw, cos, sin
+
+
+def _oracle_rope(qkv, qw, kw, cos, sin, pos, B, T, HQ, HKV, cap, eps=1e-6, depth=None):
+    q_out = np.zeros((B, HQ, T, 128), np.uint16)
+    kc = np.zeros((B, HKV, cap, 128), np.uint16)
+    vc = np.zeros((B, HKV, cap, 128), np.uint16)
+    oracle.qk_norm_rope_cache(bits(qkv), bits(qw), bits(kw), bits(cos), bits(sin), np.asarray(pos, np.int32), q_out,
+                              kc, vc, T, eps, depth=depth)
+    return q_out, kc, vc
+
+
+def test_oracle_rope_tree_depth_matches_reference_composition():
+    """Draft-tree rows (engine/kernels/rope.py:94-122, DEPTH): row t goes to
+    cache slot pos + t but rotates by position pos + depth[t]; siblings share a
+    depth.  Against the reference test's composition with per-row positions."""
+    B, T, HQ, HKV, start, eps = 2, 6, 8, 2, 40, 1e-6
+    depth = np.array([0, 1, 1, 2, 2, 3], np.int32)   # root, two children, two grandchildren, ...
+    cap = start + T + 4
+    qkv, qw, kw, cos, sin = _rope_inputs(B, T, HQ, HKV, cap, seed=21)
+    q_out, kc, vc = _oracle_rope(qkv, qw, kw, cos, sin, [start] * B, B, T, HQ, HKV, cap, eps, depth)
+    q_ref, k_ref, v_ref = _torch_rope_reference(qkv, qw, kw, cos, sin, start, B, T, HQ, HKV, 128, eps,
+                                                positions=torch.from_numpy(start + depth).long())
+    qd = np.abs(q_out.astype(np.int32) - bits(q_ref).astype(np.int32))
+    kd = np.abs(kc[:, :, start:start + T].astype(np.int32) - bits(k_ref).astype(np.int32))
+    assert qd.max() <= 2 and (qd != 0).mean() < 2e-3, (qd.max(), (qd != 0).mean())
+    assert kd.max() <= 2 and (kd != 0).mean() < 2e-3
+    assert np.array_equal(vc[:, :, start:start + T], bits(v_ref))   # slots pos + t, raw values
+    # the chain angles (pos + t) would give a different result for the rows whose depth != t
+    q_chain, _, _ = _oracle_rope(qkv, qw, kw, cos, sin, [start] * B, B, T, HQ, HKV, cap, eps)
+    assert not np.array_equal(q_chain[:, :, 2], q_out[:, :, 2])
+
+
+def test_oracle_rope_depth_identities():
+    """depth = 0..T-1 is the chain, bit for bit; a row rotated at depth d equals
+    the same row alone in a chain at position pos + d; depth = -pos rotates by
+    position 0, i.e. the per-head RMSNorm alone."""
+    B, T, HQ, HKV, start = 1, 5, 4, 2, 9
+    cap = start + T + 2
+    qkv, qw, kw, cos, sin = _rope_inputs(B, T, HQ, HKV, cap, seed=22)
+    chain = _oracle_rope(qkv, qw, kw, cos, sin, [start], B, T, HQ, HKV, cap)
+    same = _oracle_rope(qkv, qw, kw, cos, sin, [start], B, T, HQ, HKV, cap, depth=np.arange(T, dtype=np.int32))
+    for a, b in zip(chain, same):
+        assert np.array_equal(a, b)
+    depth = np.array([0, 3, 1, 1, 2], np.int32)
+    q_t, k_t, _ = _oracle_rope(qkv, qw, kw, cos, sin, [start], B, T, HQ, HKV, cap, depth=depth)
+    for t in range(T):
+        q1, k1, _ = _oracle_rope(qkv[t:t + 1], qw, kw, cos, sin, [start + int(depth[t])], 1, 1, HQ, HKV, cap)
+        assert np.array_equal(q_t[0, :, t], q1[0, :, 0])
+        assert np.array_equal(k_t[0, :, start + t], k1[0, :, start + int(depth[t])])
+    q0, _, _ = _oracle_rope(qkv, qw, kw, cos, sin, [start], B, T, HQ, HKV, cap, depth=np.full(T, -start, np.int32))
+    x = qkv[0, :128].double()
+    r = 1.0 / torch.sqrt((x * x).mean() + 1e-6)
+    assert np.array_equal(q0[0, 0, 0], bits((qw.float() * (x * r).float().to(BF16).float()).to(BF16)))
+
+
+def test_oracle_rope_rejects_positions_outside_the_table():
+    B, T, HQ, HKV, start = 1, 3, 4, 2, 5
+    cap = start + T
+    qkv, qw, kw, cos, sin = _rope_inputs(B, T, HQ, HKV, cap, seed=23)
+    with pytest.raises(ValueError):
+        _oracle_rope(qkv, qw, kw, cos, sin, [start], B, T, HQ, HKV, cap, depth=np.array([0, 1, cap], np.int32))
+    with pytest.raises(ValueError):
+        _oracle_rope(qkv, qw, kw, cos, sin, [start], B, T, HQ, HKV, cap, depth=np.array([0, 1], np.int32))
 
 
 # --------------------------------------------------------------------------
