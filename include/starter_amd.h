@@ -50,8 +50,12 @@ typedef enum sk_status {
   SK_ERR_CONFIG = 5,      /* explicit config invalid for this shape */
   SK_ERR_LAUNCH = 6,      /* the HIP runtime rejected a launch */
   SK_ERR_DEVICE = 7,      /* no usable gfx950 device / runtime query failed */
-  SK_ERR_ALIAS = 8        /* an output overlaps an input it must not alias */
+  SK_ERR_ALIAS = 8,       /* an output overlaps an input it must not alias */
+  SK_ERR_SCRATCH = 9      /* sk_gemm_bf16_noalloc: needs more than SK_NOALLOC_SCRATCH_BYTES */
 } sk_status;
+
+/* Static device scratch of sk_gemm_bf16_noalloc, per GPU (4 MiB). */
+#define SK_NOALLOC_SCRATCH_BYTES ((size_t)4 << 20)
 
 typedef enum sk_op {
   SK_OP_GEMM = 0,         /* C = A @ W^T                                  */
@@ -130,6 +134,22 @@ size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg);
 int sk_gemm_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw,
                  sk_bf16* C, int64_t ldc, int M, int N, int K,
                  const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream);
+
+/* sk_gemm_bf16 without a workspace argument: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as sk_gemm_bf16; the split-K arrival
+ * counters and partials live in a static device array of
+ * SK_NOALLOC_SCRATCH_BYTES (4 MiB) per GPU, held until the process ends.  The
+ * call allocates nothing (no hipMalloc/hipFree, no allocating library call);
+ * a plan that needs more scratch than that returns SK_ERR_SCRATCH before
+ * anything is enqueued.  A split-K call first clears the counters it uses
+ * (one small fill kernel).  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads) race and must
+ * be ordered by the caller. */
+int sk_gemm_bf16_noalloc(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw,
+                         sk_bf16* C, int64_t ldc, int M, int N, int K,
+                         const sk_config* cfg, hipStream_t stream);
 
 /* Out[M,I] = bf16(bf16(silu(bf16 g)) * bf16 u), g = A @ Wg^T, u = A @ Wu^T,
  * both fp32-accumulated.  Wg/Wu are the gate and up halves of the fused

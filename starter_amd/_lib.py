@@ -23,6 +23,9 @@ SK_ERR_CONFIG = 5
 SK_ERR_LAUNCH = 6
 SK_ERR_DEVICE = 7
 SK_ERR_ALIAS = 8
+SK_ERR_SCRATCH = 9
+
+SK_NOALLOC_SCRATCH_BYTES = 4 << 20
 
 SK_OP_GEMM = 0
 SK_OP_GATEUP = 1
@@ -44,7 +47,7 @@ SK_PATH_MFMA_LDS = 3
 # Every symbol include/starter_amd.h declares (checked by the CPU tests).
 EXPORTS = (
     "sk_version", "sk_strerror", "sk_default_config", "sk_check_config", "sk_workspace_bytes",
-    "sk_gemm_bf16", "sk_gateup_swiglu_bf16", "sk_lm_argmax_bf16", "sk_argmax_bf16",
+    "sk_gemm_bf16", "sk_gemm_bf16_noalloc", "sk_gateup_swiglu_bf16", "sk_lm_argmax_bf16", "sk_argmax_bf16",
     "sk_add_rmsnorm_bf16", "sk_swiglu_bf16",
     "sk_rmsnorm_gemm_bf16", "sk_rmsnorm_gateup_swiglu_bf16", "sk_rmsnorm_lm_argmax_bf16",
     "sk_gemm_residual_bf16", "sk_rmsnorm_pre_gemm_bf16", "sk_rmsnorm_pre_gateup_swiglu_bf16",
@@ -102,6 +105,7 @@ _SIGNATURES = {
     "sk_check_config": (_i32, [_i32, _i32, _i32, _i32, _cfgp]),
     "sk_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _cfgp]),
     "sk_gemm_bf16": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
+    "sk_gemm_bf16_noalloc": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32, _cfgp, _p]),
     "sk_gateup_swiglu_bf16": (_i32, [_p, _i64, _p, _p, _i64, _p, _i64, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
     "sk_lm_argmax_bf16": (_i32, [_p, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _cfgp, _p, _sz, _p]),
     "sk_argmax_bf16": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),

@@ -13,6 +13,12 @@
 #define SK_AUX_KERNELS 1
 #include "sk_registry.hpp"
 
+// Device scratch of sk_gemm_bf16_noalloc: split-K arrival counters and fp32
+// partials, SK_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends.
+// In host code this name is only a stand-in: kernels get the device address
+// from hipGetSymbolAddress (scratch_address below), never the name itself.
+static __device__ __align__(256) unsigned char scratch[SK_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 constexpr int kDefaultCU = 256;          // MI355X compute units
@@ -537,6 +543,26 @@ int bind_plan(Plan* pl, int num_cu, int* grid) {
   return SK_OK;
 }
 
+// Device address of the current device's copy of `scratch`, looked up once
+// per device with that device current (each GPU holds its own copy at its own
+// address).
+void* g_scratch_ptr[64];
+int g_scratch_status[64] = {};   // 0: not looked up yet, else sk_status + 1
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SK_ERR_DEVICE;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_scratch_status[dev] == 0) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = p;
+    g_scratch_status[dev] = (e == hipSuccess && p) ? SK_OK + 1 : SK_ERR_DEVICE + 1;
+  }
+  *out = g_scratch_ptr[dev];
+  return g_scratch_status[dev] - 1;
+}
+
 bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
   const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
   return pa < pb + bbytes && pb < pa + abytes;
@@ -609,7 +635,8 @@ int plan_call(int op, int M, int N, int K, const sk_config* cfg, CallPlan* cp) {
 // projection consumes rmsnorm(x + y) (op is then a SK_OP_RMSNORM_* op).
 int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, const sk_bf16* W0, const sk_bf16* W1,
                     int64_t ldw, sk_bf16* C, int64_t ldc, int64_t* ids, float* maxv, int M, int N, int K,
-                    const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
+                    const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream,
+                    bool noalloc = false) {
   const int bop = base_op(op);
   if (M < 0 || N < 1 || K < 32) return SK_ERR_SHAPE;
   if (M == 0) return SK_OK;   // empty batch: nothing to read or write (pointers may be NULL)
@@ -635,7 +662,11 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
   CallPlan cp;
   int st = plan_call(op, M, N, K, cfg, &cp);
   if (st) return st;
-  if (cp.need > 0 && (!ws || ws_bytes < cp.need)) return SK_ERR_WORKSPACE;
+  if (noalloc) {   // the library's static scratch stands in for the workspace
+    if (cp.need > SK_NOALLOC_SCRATCH_BYTES) return SK_ERR_SCRATCH;
+  } else if (cp.need > 0 && (!ws || ws_bytes < cp.need)) {
+    return SK_ERR_WORKSPACE;
+  }
   int num_cu = 0;
   st = device_info(&num_cu);
   if (st) return st;
@@ -643,6 +674,21 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
   for (int i = 0; i < cp.nplans; ++i) {
     st = bind_plan(&cp.plans[i], num_cu, &grids[i]);
     if (st) return st;
+  }
+  if (noalloc && cp.need > 0) {
+    if ((st = scratch_address(&ws))) return st;
+    ws_bytes = SK_NOALLOC_SCRATCH_BYTES;
+    // The arrival counters must start at zero.  Every finished call leaves
+    // them at zero, but the array keeps whatever the last call on this GPU
+    // left, so the counters this call uses are cleared first (a fill kernel,
+    // which also replays correctly from a captured graph).
+    size_t tb = 0;
+    for (int i = 0; i < cp.nplans; ++i) {
+      const size_t t = ticket_bytes(cp.plans[i].nrb);
+      tb = t > tb ? t : tb;
+    }
+    sk::clear_words_kernel<<<dim3(1), dim3(256), 0, stream>>>(static_cast<unsigned*>(ws), (int)(tb / 4));
+    if ((st = launch_status())) return st;
   }
   // Separate prologue: xout and the normalised rows (in the workspace) first.
   const sk_bf16* Ause = A;
@@ -874,6 +920,7 @@ const char* sk_strerror(int status) {
     case SK_ERR_LAUNCH: return "kernel launch failed";
     case SK_ERR_DEVICE: return "no usable gfx950 device";
     case SK_ERR_ALIAS: return "output overlaps an input";
+    case SK_ERR_SCRATCH: return "call needs more than the library's static scratch (SK_NOALLOC_SCRATCH_BYTES)";
   }
   return "unknown status";
 }
@@ -914,6 +961,12 @@ int sk_gemm_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, s
                  int K, const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
   return run_gemm_family(SK_OP_GEMM, A, lda, nullptr, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, ws,
                          ws_bytes, stream);
+}
+
+int sk_gemm_bf16_noalloc(const sk_bf16* A, int64_t lda, const sk_bf16* W, int64_t ldw, sk_bf16* C, int64_t ldc,
+                         int M, int N, int K, const sk_config* cfg, hipStream_t stream) {
+  return run_gemm_family(SK_OP_GEMM, A, lda, nullptr, W, nullptr, ldw, C, ldc, nullptr, nullptr, M, N, K, cfg, nullptr,
+                         0, stream, /*noalloc=*/true);
 }
 
 int sk_gateup_swiglu_bf16(const sk_bf16* A, int64_t lda, const sk_bf16* Wg, const sk_bf16* Wu, int64_t ldw,

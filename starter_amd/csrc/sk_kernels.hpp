@@ -1417,6 +1417,12 @@ __global__ void __launch_bounds__(RMS_THREADS) add_rmsnorm_kernel(const uint16_t
   }
 }
 
+// Zero n 32-bit words with plain vector stores (clears arrival counters; a
+// kernel rather than a memset node, so it also replays from a captured graph).
+__global__ void __launch_bounds__(256) clear_words_kernel(unsigned* __restrict__ p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
 // Unfused SwiGLU over gu = [g | u] (engine/kernels/swiglu.py:14-24).
 __global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t* __restrict__ gu, int64_t ld_gu,
                                                      uint16_t* __restrict__ out, int64_t ld_out, int M, int I) {

@@ -42,8 +42,8 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_status_strings():
     lib = _lib.lib()
     assert lib.sk_version() >= 1
-    msgs = {lib.sk_strerror(c).decode() for c in range(9)}
-    assert len(msgs) == 9 and "ok" in msgs
+    msgs = {lib.sk_strerror(c).decode() for c in range(10)}
+    assert len(msgs) == 10 and "ok" in msgs
     assert lib.sk_strerror(99).decode() == "unknown status"
 
 
@@ -181,6 +181,33 @@ def test_valid_call_without_gpu_fails_loudly():
         pytest.skip("a GPU is present; the GPU tests exercise this path")
     assert _gemm(_lib.lib()) == SK_ERR_DEVICE
     assert _rms_gemm(_lib.lib(), M=1) == SK_ERR_DEVICE   # fused GEMV default: no workspace
+
+
+def _gemm_noalloc(lib, A=A0, lda=2560, W=W0, ldw=2560, C=C0, ldc=6144, M=8, N=6144, K=2560, cfg=None):
+    return lib.sk_gemm_bf16_noalloc(A, lda, W, ldw, C, ldc, M, N, K, _lib.cfg_ptr(cfg), None)
+
+
+def test_noalloc_gemm_validates_like_the_workspace_entry_point():
+    """sk_gemm_bf16_noalloc takes sk_gemm_bf16's arguments without the
+    workspace: the same argument checks, and a plan whose split-K scratch
+    exceeds the static array is refused with SK_ERR_SCRATCH before any device
+    work (here: no GPU at all)."""
+    lib = _lib.lib()
+    assert _gemm_noalloc(lib, M=0) == SK_OK
+    assert _gemm_noalloc(lib, A=0) == SK_ERR_NULL
+    assert _gemm_noalloc(lib, K=2568) == SK_ERR_SHAPE
+    assert _gemm_noalloc(lib, A=A0 + 2) == SK_ERR_ALIGN
+    assert _gemm_noalloc(lib, C=A0 + 64) == SK_ERR_ALIAS
+    big = SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=8, rows=16, split=2)   # lm logits, split 2: 77.8 MB of partials
+    assert _lib.workspace_bytes(SK_OP_GEMM, 64, 151936, 2560, big) > _lib.SK_NOALLOC_SCRATCH_BYTES
+    assert _gemm_noalloc(lib, M=64, N=151936, ldc=151936, cfg=big) == _lib.SK_ERR_SCRATCH
+    # every default plan of the Qwen3-4B projections fits the scratch
+    for op, N, K in (QWEN[n] for n in ("qkv", "o", "d", "lm")):
+        for M in (1, 2, 4, 8, 16, 32, 40, 64):
+            assert _lib.workspace_bytes(op, M, N, K) <= _lib.SK_NOALLOC_SCRATCH_BYTES, (N, K, M)
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        assert _gemm_noalloc(lib) == SK_ERR_DEVICE   # a valid call without a GPU fails loudly
 
 
 # ---------------------------------------------------------------------------
