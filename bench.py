@@ -340,19 +340,21 @@ PROBE_LAUNCHES = 24
 PROBE_COPY_BYTES = 512 << 20
 
 
-def probe(M: int) -> int:
+def probe(M: int, name: str = "gate_up") -> int:
     """Untimed launches for the hardware-counter passes: PROBE_LAUNCHES
-    gate_up+SwiGLU launches at M rows over 12 rotating layers (1.2 GB of
-    weights, so no launch finds its weights in the MALL), then three copies of
-    PROBE_COPY_BYTES with torch's copy kernel as the calibration of known size."""
+    launches of one projection (default gate_up+SwiGLU) at M rows over rotating
+    weights (12 layers, or the two lm_head copies: no launch finds its weights
+    in the MALL), then three copies of PROBE_COPY_BYTES with torch's copy
+    kernel as the calibration of known size."""
     import torch
 
     wl = Workload(12, M)
-    wl.launch("gate_up", 0)
+    nl = 2 if name == "lm_head" else wl.L
+    wl.launch(name, 0)
     torch.cuda.synchronize()
-    log(f"probe: {PROBE_LAUNCHES} gate_up launches at M={M}")
+    log(f"probe: {PROBE_LAUNCHES} {name} launches at M={M}")
     for i in range(PROBE_LAUNCHES):
-        wl.launch("gate_up", i % wl.L)
+        wl.launch(name, i % nl)
     torch.cuda.synchronize()
     src = torch.empty(PROBE_COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
     dst = torch.empty_like(src)
@@ -381,18 +383,19 @@ def _counter_rows(folder: str, counter: str) -> list[tuple[str, float]]:
     return [(n, v) for _, n, v in sorted(rows)]
 
 
-def traffic_summary(fetch_dir: str, write_dir: str, M: int) -> int:
-    """HBM bytes per gate_up launch from FETCH_SIZE / WRITE_SIZE (KiB per
-    dispatch), each scaled by copy_bytes / (what the counter reads for the
-    PROBE_COPY_BYTES copy), written next to the profiles it came from."""
-    out = {"M": M, "copy_bytes": PROBE_COPY_BYTES}
+def traffic_summary(fetch_dir: str, write_dir: str, M: int, name: str = "gate_up") -> int:
+    """HBM bytes per launch of the probed projection from FETCH_SIZE /
+    WRITE_SIZE (KiB per dispatch), each scaled by copy_bytes / (what the
+    counter reads for the PROBE_COPY_BYTES copy), written next to the
+    profiles it came from."""
+    out = {"op": name, "M": M, "copy_bytes": PROBE_COPY_BYTES}
     total = 0.0
     for key, folder, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
         rows = _counter_rows(folder, counter)
         gu = [v for n, v in rows if "sk::" in n]   # the probe launches no other library kernel
         cp = [v for n, v in rows if "copy" in n.lower()][-3:]   # the probe ends with its three copies
         if not gu or not cp:
-            raise SystemExit(f"{counter}: gate_up dispatches {len(gu)}, copy dispatches {len(cp)} in {folder}")
+            raise SystemExit(f"{counter}: {name} dispatches {len(gu)}, copy dispatches {len(cp)} in {folder}")
         gu = gu[1:] if len(gu) > 1 else gu     # first launch warms code and workspace
         kib = statistics.median(gu)
         copy_kib = statistics.median(cp)
@@ -401,9 +404,9 @@ def traffic_summary(fetch_dir: str, write_dir: str, M: int) -> int:
                     "bytes_per_launch": round(kib * 1024.0 * factor)}
         total += kib * 1024.0 * factor
     out["hbm_bytes_per_launch"] = round(total)
-    out["algorithmic_bytes_per_launch"] = alg_bytes("gate_up", M)
-    out["ratio"] = round(total / alg_bytes("gate_up", M), 4)
-    path = ROOT / "profiles" / f"traffic_gate_up_m{M}.json"
+    out["algorithmic_bytes_per_launch"] = alg_bytes(name, M)
+    out["ratio"] = round(total / alg_bytes(name, M), 4)
+    path = ROOT / "profiles" / f"traffic_{name}_m{M}.json"
     path.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
     return 0
@@ -417,7 +420,7 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None
     end-to-end tok/s = B * (steps + 1) / (prefill + decode)."""
     import torch
 
-    from starter_amd.decode import DecodePlan, Qwen3Config, SyntheticModel, time_decode
+    from starter_amd.decode import DecodePlan, Qwen3Config, SyntheticModel, time_decode, time_delivery
 
     log(f"decode: building the synthetic Qwen3-4B (B={B}, prompt {T}, {steps} steps)")
     model = SyntheticModel(Qwen3Config(), "cuda:0", seed=7)
@@ -427,11 +430,18 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None
     plan = DecodePlan(model, B, T, max_new)
     g = torch.Generator(device="cuda:0").manual_seed(11)
     plan.ids.copy_(torch.randint(0, model.cfg.vocab, (B, T), device="cuda:0", generator=g))
+    ids = plan.ids.clone()
     r = time_decode(plan, steps)
     log(f"decode: {r['tok_s']:.0f} tok/s ({r['ms_per_step']:.3f} ms/step), prefill {r['prefill_s']:.3f} s, "
         f"end-to-end {r['e2e_tok_s']:.0f} tok/s")
+    # the same generation through the pipelined host delivery loop (every
+    # step's tokens copied to pinned host memory, GPU kept 3 steps ahead)
+    d = time_delivery(plan, ids, steps + 1)
+    log(f"decode with host delivery: {d['delivered_tok_s']:.0f} tok/s delivered, end-to-end {d['e2e_tok_s']:.0f} tok/s")
     out = {"tok_s": round(r["tok_s"], 1), "ms_per_step": round(r["ms_per_step"], 4), "steps": steps, "B": B,
            "prompt": T, "prefill_s": round(r["prefill_s"], 4), "e2e_tok_s": round(r["e2e_tok_s"], 1),
+           "host_delivery": {"delivered_tok_s": round(d["delivered_tok_s"], 1), "e2e_tok_s": round(d["e2e_tok_s"], 1),
+                             "first_token_s": round(d["first_token_s"], 4), "depth": d["depth"]},
            "workload": "synthetic qwen3-4b greedy decode, 36 layers, GQA 32/8, cap %d, HIP graph per step" % plan.cap}
     return out
 
@@ -523,13 +533,15 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the C5 decode measurement and print its JSON object")
     ap.add_argument("--probe", action="store_true",
-                    help="launch gate_up at --M (untimed) and a 512 MiB copy, for rocprofv3 --pmc passes")
+                    help="launch --probe-op at --M (untimed) and a 512 MiB copy, for rocprofv3 --pmc passes")
+    ap.add_argument("--probe-op", default="gate_up", choices=list(SHAPES),
+                    help="the projection --probe launches (default gate_up)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders of --probe (FETCH_SIZE, WRITE_SIZE) into "
-                         "profiles/traffic_gate_up_m<M>.json and exit")
+                         "profiles/traffic_<probe-op>_m<M>.json and exit")
     args = ap.parse_args()
     if args.traffic_from:
-        return traffic_summary(args.traffic_from[0], args.traffic_from[1], args.M)
+        return traffic_summary(args.traffic_from[0], args.traffic_from[1], args.M, args.probe_op)
 
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build measures the single-GPU hot path "
@@ -551,7 +563,7 @@ def main() -> int:
         return 1
     torch.cuda.set_device(0)
     if args.probe:
-        return probe(args.M)
+        return probe(args.M, args.probe_op)
     if args.attention_only:
         print(json.dumps({"attention": attention_benchmark()}), flush=True)
         return 0

@@ -312,24 +312,24 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 3, 32, 32, 1, 0}},  // qkv       12.84 us  2494 GB/s
-    {SK_OP_GEMM, 6144, 2560, 40, {1, 16, 5, 16, 1, 0}},  // qkv       17.01 us  1890 GB/s
+    {SK_OP_GEMM, 6144, 2560, 40, {3, 5, 8, 16, 2, 256}},  // qkv       15.51 us  2083 GB/s
     {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
     {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
     {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     7.02 us  2991 GB/s
-    {SK_OP_GEMM, 2560, 4096, 4, {3, 4, 32, 16, 1, 0}},  // o_proj     7.25 us  2899 GB/s
+    {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     6.95 us  3024 GB/s
     {SK_OP_GEMM, 2560, 4096, 8, {3, 4, 32, 16, 1, 0}},  // o_proj     7.09 us  2971 GB/s
     {SK_OP_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj     7.47 us  2834 GB/s
     {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj     9.13 us  2343 GB/s
-    {SK_OP_GEMM, 2560, 4096, 40, {3, 8, 8, 32, 2, 0}},  // o_proj    15.86 us  1356 GB/s
-    {SK_OP_GEMM, 2560, 4096, 64, {3, 8, 8, 16, 2, 0}},  // o_proj    20.33 us  1073 GB/s
+    {SK_OP_GEMM, 2560, 4096, 40, {3, 6, 8, 32, 3, 0}},  // o_proj    11.63 us  1849 GB/s
+    {SK_OP_GEMM, 2560, 4096, 64, {3, 6, 8, 16, 3, 0}},  // o_proj    14.44 us  1511 GB/s
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
     {SK_OP_GATEUP, 9728, 2560, 2, {3, 10, 8, 16, 1, 203}},  // gate_up   17.35 us  5746 GB/s
     {SK_OP_GATEUP, 9728, 2560, 4, {3, 10, 8, 16, 1, 203}},  // gate_up   17.37 us  5739 GB/s
     {SK_OP_GATEUP, 9728, 2560, 8, {3, 10, 8, 16, 1, 203}},  // gate_up   17.49 us  5707 GB/s
     {SK_OP_GATEUP, 9728, 2560, 16, {3, 10, 8, 16, 1, 203}},  // gate_up   18.13 us  5515 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 32, {3, 3, 32, 16, 1, 0}},  // gate_up   31.35 us  3203 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 40, {1, 8, 10, 16, 1, 0}},  // gate_up   35.69 us  2819 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 32, {3, 5, 8, 16, 2, 0}},  // gate_up   29.24 us  3434 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 40, {3, 5, 8, 16, 2, 0}},  // gate_up   33.86 us  2976 GB/s
     {SK_OP_GATEUP, 9728, 2560, 64, {1, 5, 8, 16, 2, 0}},  // gate_up   56.95 us  1777 GB/s
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
@@ -337,8 +337,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 8, {3, 13, 8, 32, 3, 240}},  // down      12.78 us  3913 GB/s
     {SK_OP_GEMM, 2560, 9728, 16, {3, 4, 32, 32, 3, 0}},  // down      15.14 us  3316 GB/s
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
-    {SK_OP_GEMM, 2560, 9728, 40, {1, 16, 5, 16, 4, 0}},  // down      26.15 us  1942 GB/s
-    {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 16, 5, 0}},  // down      36.59 us  1404 GB/s
+    {SK_OP_GEMM, 2560, 9728, 40, {3, 7, 8, 32, 6, 240}},  // down      19.22 us  2642 GB/s
+    {SK_OP_GEMM, 2560, 9728, 64, {3, 7, 8, 16, 6, 240}},  // down      24.95 us  2059 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 4, {3, 10, 8, 32, 1, 0}},  // lm_head  113.49 us  6855 GB/s

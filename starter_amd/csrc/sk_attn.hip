@@ -455,20 +455,41 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   if (threadIdx.x == 0) s_last = take_ticket(&a.tickets[bq], (unsigned)S) ? 1 : 0;
   __syncthreads();
   if (!s_last) return;
+  // Each output loads its splits' (m, l, o) in batches of MB, all loads of a
+  // batch issued before any arithmetic (one memory round trip per batch, not
+  // one per split); the merge itself runs in split order 0..S-1.
+  constexpr int MB = 4;
   for (int idx = threadIdx.x; idx < QR * HEAD_D; idx += 64 * ATTN_WAVES) {
     const int r = idx / HEAD_D, d = idx - (idx / HEAD_D) * HEAD_D;
     const int gr = rbk * QR + r;
     const int t = gr / a.G, g = gr - (gr / a.G) * a.G;
     if (gr >= rows) continue;
+    const int64_t pr0 = (int64_t)bq * S * QR + r;   // split sp: pr0 + sp * QR
     float M = -INFINITY;
-    for (int sp = 0; sp < S; ++sp) M = fmaxf(M, load_agent(&a.part_ml[2 * (((int64_t)bq * S + sp) * QR + r)]));
+    for (int s0 = 0; s0 < S; s0 += MB) {
+      float ms[MB];
+#pragma unroll
+      for (int k = 0; k < MB; ++k) ms[k] = load_agent(&a.part_ml[2 * (pr0 + (int64_t)min(s0 + k, S - 1) * QR)]);
+#pragma unroll
+      for (int k = 0; k < MB; ++k) M = fmaxf(M, ms[k]);   // repeats of split S-1 change nothing
+    }
     float L = 0.f, O = 0.f;
-    for (int sp = 0; sp < S; ++sp) {
-      const int64_t pr = ((int64_t)bq * S + sp) * QR + r;
-      const float ms = load_agent(&a.part_ml[2 * pr]);
-      const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
-      L += w * load_agent(&a.part_ml[2 * pr + 1]);
-      O += w * load_agent(&a.part_o[pr * HEAD_D + d]);
+    for (int s0 = 0; s0 < S; s0 += MB) {
+      float ms[MB], ls[MB], os[MB];
+#pragma unroll
+      for (int k = 0; k < MB; ++k) {
+        const int64_t pr = pr0 + (int64_t)min(s0 + k, S - 1) * QR;
+        ms[k] = load_agent(&a.part_ml[2 * pr]);
+        ls[k] = load_agent(&a.part_ml[2 * pr + 1]);
+        os[k] = load_agent(&a.part_o[pr * HEAD_D + d]);
+      }
+#pragma unroll
+      for (int k = 0; k < MB; ++k) {
+        if (s0 + k >= S) break;
+        const float w = ms[k] == -INFINITY ? 0.f : __expf(ms[k] - M);
+        L += w * ls[k];
+        O += w * os[k];
+      }
     }
     a.out[((int64_t)(b * a.R + t) * a.HQ + kh * a.G + g) * HEAD_D + d] = f2bf(L > 0.f ? O / L : 0.f);
   }

@@ -430,44 +430,75 @@ __device__ __forceinline__ bool take_ticket(unsigned* ticket, unsigned expected)
   return last;
 }
 
+// Splits whose partials are requested together before the first add: a
+// finish costs one memory round trip per batch of splits, not one per split
+// and output.
+constexpr int kFixupBatch = 4;
+
 template <int OUT_ROWS, int EPI, bool RESID = false>
 __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0, int* lds_flags) {
   const int M = p.M, S = p.S;
   const int64_t MN = (int64_t)M * p.N;
+  const int nthr = 64 * p.nw;
   __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores are performed
   __syncthreads();
-  // Tickets of up to `cap` tiles per round (the flags reuse the partials' LDS).
-  const int cap = 2 * p.nw * M * OUT_ROWS;
+  // Tickets of up to `cap` tiles per round, one thread per tile so they are
+  // taken together (the flags reuse the partials' LDS).
+  const int cap = min(2 * p.nw * M * OUT_ROWS, nthr);
   for (int j0 = 0; j0 < ntiles; j0 += cap) {
     const int jn = min(ntiles - j0, cap);
-    if (threadIdx.x == 0)
-      for (int j = 0; j < jn; ++j)
-        lds_flags[j] = take_ticket(&p.tickets[rb0 + (j0 + j) * p.rbstep], (unsigned)S) ? 1 : 0;
+    if ((int)threadIdx.x < jn)
+      lds_flags[threadIdx.x] = take_ticket(&p.tickets[rb0 + (j0 + threadIdx.x) * p.rbstep], (unsigned)S) ? 1 : 0;
     __syncthreads();
     for (int j = 0; j < jn; ++j) {
       if (!lds_flags[j]) continue;
       const int rb = rb0 + (j0 + j) * p.rbstep;
-      for (int idx = threadIdx.x; idx < M * OUT_ROWS; idx += 64 * p.nw) {
-        const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
-        const int n = rb * OUT_ROWS + r;
-        if constexpr (RESID) {
-          // every lane of a 16-column group takes part in the group sum
-          static_assert(EPI == EPI_PART && OUT_ROWS % 16 == 0, "residual after split-K partials");
-          const bool ok = n < p.N;
-          const int64_t e = (int64_t)m * p.N + (ok ? n : 0);
-          float g = 0.f;
-          for (int s = 0; s < S; ++s) g += ok ? load_agent(&p.part[s * MN + e]) : 0.f;
-          resid_out(p, m, n, ok, f2bf(g));
-          continue;
+      // Every output of the tile is finished by one thread; a thread's outputs
+      // (up to 4 per pass) issue all their partial loads before any add.
+      for (int base = 0; base < M * OUT_ROWS; base += 4 * nthr) {
+        constexpr int NP = EPI == EPI_PART_GU ? 2 : 1;   // gate and up partials
+        float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
+        int64_t e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int idx = min(base + (int)threadIdx.x + i * nthr, M * OUT_ROWS - 1);
+          const int m = idx / OUT_ROWS, n = rb * OUT_ROWS + idx % OUT_ROWS;
+          e[i] = (int64_t)m * p.N + (n < p.N ? n : 0);   // clamped in bounds; stored only if real
         }
-        if (n >= p.N) continue;
-        const int64_t e = (int64_t)m * p.N + n;
-        float g = 0.f, u = 0.f;
-        for (int s = 0; s < S; ++s) {
-          g += load_agent(&p.part[s * MN + e]);
-          if constexpr (EPI == EPI_PART_GU) u += load_agent(&p.part[(S + s) * MN + e]);
+        // Sums in split order s = 0..S-1, all loads of a batch issued first.
+        for (int s0 = 0; s0 < S; s0 += kFixupBatch) {
+          float v[NP][4][kFixupBatch];
+#pragma unroll
+          for (int h = 0; h < NP; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int k = 0; k < kFixupBatch; ++k)
+                v[h][i][k] = load_agent(&p.part[((int64_t)h * S + min(s0 + k, S - 1)) * MN + e[i]]);
+#pragma unroll
+          for (int k = 0; k < kFixupBatch; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (s0 + k < S) {
+                g[i] += v[0][i][k];
+                if constexpr (NP == 2) u[i] += v[NP - 1][i][k];
+              }
         }
-        p.C[(int64_t)m * p.ldc + n] = (EPI == EPI_PART_GU) ? swiglu_bf(g, u) : f2bf(g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int idx = base + (int)threadIdx.x + i * nthr;
+          const int m = idx / OUT_ROWS, r = idx % OUT_ROWS;
+          const int n = rb * OUT_ROWS + r;
+          if constexpr (RESID) {
+            // every lane of a 16-column group takes part in the group sum
+            // (idx < M*OUT_ROWS is uniform over each 16-lane group)
+            static_assert(EPI == EPI_PART && OUT_ROWS % 16 == 0, "residual after split-K partials");
+            if (idx < M * OUT_ROWS) resid_out(p, m, n, n < p.N, f2bf(n < p.N ? g[i] : 0.f));
+            continue;
+          }
+          if (idx >= M * OUT_ROWS || n >= p.N) continue;
+          p.C[(int64_t)m * p.ldc + n] = (EPI == EPI_PART_GU) ? swiglu_bf(g[i], u[i]) : f2bf(g[i]);
+        }
       }
     }
     __syncthreads();   // flags are rewritten by the next round

@@ -286,6 +286,42 @@ class DecodePlan:
         self.steps_done += 1
 
     @torch.inference_mode()
+    def run(self, ids: torch.Tensor, max_new_tokens: int | None = None, depth: int = 3):
+        """Yield one host list of B greedy token ids per generated position,
+        keeping the GPU up to ``depth`` steps ahead of the consumer
+        (engine/engine.py:388-419): step t's tokens are copied into pinned host
+        slot t % depth and fenced with an event, and the following steps are
+        launched before the host waits on that event, so reading step t
+        overlaps the compute of steps t+1..t+depth-1.  Copies and graph replays
+        share the current stream, so each copy follows its own step."""
+        n = self.max_new if max_new_tokens is None else max_new_tokens
+        if not 1 <= n <= self.max_new:
+            raise ValueError(f"max_new_tokens must be in 1..{self.max_new}, got {n}")
+        if depth < 1:
+            raise ValueError("depth must be at least 1")
+        if getattr(self, "_host_tok", None) is None or self._host_tok.shape[0] != depth:
+            self._host_tok = torch.empty((depth, self.B), dtype=torch.int64, pin_memory=True)
+            self._events = [torch.cuda.Event() for _ in range(depth)]
+        host, events = self._host_tok, self._events
+        self.ids.copy_(ids)
+        self.prefill()
+        if self.g_decode is None:
+            self.capture()
+        host[0].copy_(self.tok, non_blocking=True)
+        events[0].record()
+        launched = 1
+        for step in range(n):
+            while launched < n and launched - step < depth:
+                slot = launched % depth
+                self.step()
+                host[slot].copy_(self.tok, non_blocking=True)
+                events[slot].record()
+                launched += 1
+            slot = step % depth
+            events[slot].synchronize()
+            yield host[slot].tolist()
+
+    @torch.inference_mode()
     def generate(self, ids: torch.Tensor, max_new: int | None = None) -> torch.Tensor:
         """Greedy tokens [B, max_new]: the prefill's token, then one per decode step."""
         max_new = self.max_new if max_new is None else max_new
@@ -322,3 +358,23 @@ def time_decode(plan: DecodePlan, steps: int) -> dict:
     ms = a.elapsed_time(b)
     return {"tok_s": plan.B * steps / (ms * 1e-3), "ms_per_step": ms / steps, "steps": steps,
             "prefill_s": prefill_s, "e2e_tok_s": plan.B * (steps + 1) / (prefill_s + ms * 1e-3)}
+
+
+def time_delivery(plan: DecodePlan, ids: torch.Tensor, new_tokens: int, depth: int = 3) -> dict:
+    """Throughput as a consumer of ``DecodePlan.run`` sees it (host clock):
+    every position's tokens copied to pinned host memory and handed over as a
+    Python list, the GPU kept ``depth`` steps ahead.  delivered tok/s = B x
+    (new_tokens - 1) / (time from the prefill's tokens to the last step's);
+    end-to-end tok/s = B x new_tokens / (time from the call to the last step's
+    tokens, prefill included), the reference's definition
+    (QWEN_ENGINE_CONTRACT.md:93-102).  Returns the tokens too."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks, times = [], []
+    for row in plan.run(ids, new_tokens, depth=depth):
+        times.append(time.perf_counter())
+        toks.append(row)
+    decode_s = times[-1] - times[0]
+    return {"delivered_tok_s": plan.B * (new_tokens - 1) / decode_s if new_tokens > 1 else 0.0,
+            "e2e_tok_s": plan.B * new_tokens / (times[-1] - t0), "first_token_s": times[0] - t0,
+            "depth": depth, "tokens": toks}

@@ -109,6 +109,28 @@ def test_graph_replay_matches_eager_decode(handoff):
     assert torch.equal(torch.stack(toks, 1), eager)
 
 
+@pytest.mark.parametrize("depth", [1, 3])
+def test_pipelined_host_delivery_yields_the_decoded_tokens(depth):
+    """DecodePlan.run (engine/engine.py:388-419): one host list per position,
+    the GPU kept up to `depth` steps ahead through pinned slots and events;
+    the lists equal generate()'s tokens, also when run twice on one plan (the
+    captured step graph replays for the second run)."""
+    model = SyntheticModel(CFG, DEV, seed=5, norm_noise=0.1)
+    B, T, N = 3, 37, 9
+    ids = torch.randint(0, CFG.vocab, (B, T), device=DEV, generator=torch.Generator(device=DEV).manual_seed(6))
+    ref = DecodePlan(model, B, T, N).generate(ids, N).cpu()
+    plan = DecodePlan(model, B, T, N)
+    for _ in range(2):
+        rows = list(plan.run(ids, N, depth=depth))
+        assert len(rows) == N and all(isinstance(r, list) and len(r) == B for r in rows)
+        assert torch.equal(torch.tensor(rows).t(), ref)
+    with pytest.raises(ValueError):
+        next(plan.run(ids, N + 1))
+    plan.step()                         # step N of N planned: attends over T + N keys, still covered
+    with pytest.raises(RuntimeError):   # a step past the planned length is refused, not silently truncated
+        plan.step()
+
+
 @pytest.mark.parametrize("handoff", [True, False])
 def test_decode_tokens_match_torch_reference(handoff):
     """Both decode steps: the reference's normed projections, and the residual
