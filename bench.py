@@ -348,14 +348,18 @@ def probe(M: int, name: str = "gate_up") -> int:
     kernel as the calibration of known size."""
     import torch
 
-    wl = Workload(12, M)
-    nl = 2 if name == "lm_head" else wl.L
-    wl.launch(name, 0)
-    torch.cuda.synchronize()
-    log(f"probe: {PROBE_LAUNCHES} {name} launches at M={M}")
-    for i in range(PROBE_LAUNCHES):
-        wl.launch(name, i % nl)
-    torch.cuda.synchronize()
+    if name == "attention":   # the decode step's fused rope + attention launch (B = 16, position 1088)
+        log(f"probe: {PROBE_LAUNCHES} attention launches (B = 16, position {ATTN_POS})")
+        attention_benchmark(launches=PROBE_LAUNCHES, timed=False)
+    else:
+        wl = Workload(12, M)
+        nl = 2 if name == "lm_head" else wl.L
+        wl.launch(name, 0)
+        torch.cuda.synchronize()
+        log(f"probe: {PROBE_LAUNCHES} {name} launches at M={M}")
+        for i in range(PROBE_LAUNCHES):
+            wl.launch(name, i % nl)
+        torch.cuda.synchronize()
     src = torch.empty(PROBE_COPY_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1.0)
     dst = torch.empty_like(src)
     log(f"probe: 3 copies of {PROBE_COPY_BYTES} bytes")
@@ -412,6 +416,91 @@ def traffic_summary(fetch_dir: str, write_dir: str, M: int, name: str = "gate_up
     return 0
 
 
+COUNTER_PASSES = {   # rocprofv3 --pmc sets, each within one run's per-block limits
+    "A": "SQ_WAVES SQ_BUSY_CU_CYCLES SQ_WAVE_CYCLES SQ_WAIT_INST_ANY SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
+         "SQ_LDS_BANK_CONFLICT",
+    "B": "SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_LDS SQ_INSTS_VMEM_RD SQ_LDS_IDX_ACTIVE "
+         "SQ_WAIT_INST_LDS GRBM_GUI_ACTIVE TA_BUSY_avr TA_BUSY_max",
+    "C": "FETCH_SIZE",
+    "D": "WRITE_SIZE TCC_HIT_sum TCC_MISS_sum",
+}
+MI355X_SIMDS = 1024
+SHADER_GHZ = 2.4   # MI355X peak engine clock: busy fractions are of the kernel's duration at this clock
+
+
+def _dispatches(folder: Path, csv_name: str) -> list[dict]:
+    """Rows of rocprofv3's csv_name files under folder grouped per dispatch, in dispatch order."""
+    import csv
+
+    per = {}
+    for f in sorted(folder.rglob(f"*{csv_name}")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                d = per.setdefault(int(r.get("Dispatch_Id") or r.get("Correlation_Id")), {"_name": r["Kernel_Name"]})
+                if "Counter_Name" in r:
+                    d[r["Counter_Name"]] = float(r["Counter_Value"])
+                    d["_grid"] = int(r["Grid_Size"]) // int(r["Workgroup_Size"])
+                    d["_wg"] = int(r["Workgroup_Size"])
+                else:
+                    d["_us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+    return [per[k] for k in sorted(per)]
+
+
+def counters_summary(folder: str) -> int:
+    """One markdown row per probe from the counter passes of ``--probe`` runs
+    laid out as <folder>/<op>_m<M>_{kt,A,B,C,D} (kernel trace, then the four
+    COUNTER_PASSES).  Library launches (kernel names in namespace sk) are kept
+    and the first one dropped (it warms code and workspace); FETCH_SIZE and
+    WRITE_SIZE are scaled by copy bytes / what the counter reads for the
+    probe's PROBE_COPY_BYTES copies.  Busy fractions divide by the kernel
+    trace's average duration in cycles at SHADER_GHZ (times the SIMD count
+    for MFMA busy cycles, which the counter sums over SIMDs); TA_BUSY_avr and
+    _max are per texture-address unit."""
+    root = Path(folder)
+    probes = sorted({p.name[:-3] for p in root.glob("*_kt")})
+    print("| op | M | instance | WGs x threads | avg us | % of 8 TB/s | TFLOP/s (% of 2.5 P) | MFMA busy % "
+          "| MFMA insts/wave | VALU insts/wave | LDS bank confl % | wait % of wave cycles | TA busy avg/max % "
+          "| HBM read MB (alg MB) | HBM write MB | L2 hit % |")
+    print("|---|---:|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+
+    def med(rs, k):
+        v = [r[k] for r in rs if k in r]
+        return statistics.median(v) if v else float("nan")
+
+    for pr in probes:
+        op, m = pr.rsplit("_m", 1)
+        M = int(m)
+        sets = {x: _dispatches(root / f"{pr}_{x}", "counter_collection.csv") for x in "ABCD"}
+        lib = {x: [r for r in rs if "sk::" in r["_name"]][1:] for x, rs in sets.items()}
+        cal = {}
+        for x, ctr in (("C", "FETCH_SIZE"), ("D", "WRITE_SIZE")):
+            cp = [r[ctr] for r in sets[x] if "copy" in r["_name"].lower() and ctr in r][-3:]
+            cal[ctr] = (PROBE_COPY_BYTES / 1024.0) / statistics.median(cp) if cp else float("nan")
+        kt = [r["_us"] for r in _dispatches(root / f"{pr}_kt", "kernel_trace.csv") if "sk::" in r["_name"]][1:]
+        A, B, C, D = lib["A"], lib["B"], lib["C"], lib["D"]
+        if op == "attention":
+            alg, flops = 16 * 8 * (ATTN_POS + 1) * 128 * 2 * 2, 16 * 32 * (ATTN_POS + 1) * 128 * 2 * 2
+        else:
+            alg, flops = alg_bytes(op, M), alg_flops(op, M)
+        us = statistics.mean(kt)
+        cycles = us * SHADER_GHZ * 1e3          # kernel duration in shader cycles
+        waves = med(A, "SQ_WAVES")
+        name = A[0]["_name"].replace("void ", "").split("(")[0]
+        hits, miss = med(D, "TCC_HIT_sum"), med(D, "TCC_MISS_sum")
+        print(f"| {op} | {M if op != 'attention' else 16} | `{name}` | {A[0]['_grid']} x {A[0]['_wg']} | {us:.2f} "
+              f"| {100 * alg / us / 1e3 / PEAK_HBM_GBS:.1f} "
+              f"| {flops / us / 1e6:.1f} ({100 * flops / us / 1e6 / PEAK_BF16_TFLOPS:.2f}) "
+              f"| {100 * med(B, 'SQ_VALU_MFMA_BUSY_CYCLES') / (cycles * MI355X_SIMDS):.2f} "
+              f"| {med(A, 'SQ_INSTS_MFMA') / waves:.0f} | {med(A, 'SQ_INSTS_VALU') / waves:.0f} "
+              f"| {100 * med(A, 'SQ_LDS_BANK_CONFLICT') / max(med(B, 'SQ_LDS_IDX_ACTIVE'), 1):.1f} "
+              f"| {100 * med(A, 'SQ_WAIT_INST_ANY') / med(A, 'SQ_WAVE_CYCLES'):.1f} "
+              f"| {100 * med(B, 'TA_BUSY_avr') / cycles:.0f} / {100 * med(B, 'TA_BUSY_max') / cycles:.0f} "
+              f"| {med(C, 'FETCH_SIZE') * 1024 * cal['FETCH_SIZE'] / 1e6:.1f} ({alg / 1e6:.1f}) "
+              f"| {med(D, 'WRITE_SIZE') * 1024 * cal['WRITE_SIZE'] / 1e6:.2f} "
+              f"| {100 * hits / max(hits + miss, 1):.1f} |")
+    return 0
+
+
 def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None = None) -> dict:
     """synthetic Qwen3-4B (36 layers, random bf16
     weights ~N(0, 0.02)), B prompts of T uniform-random token ids, prefill, then
@@ -449,7 +538,11 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None
 _KEEP: list = []   # attention workloads stay allocated until the process ends (no device frees)
 
 
-def attention_benchmark(launches: int = 64, B: int = 16, pos: int = 1088, cap: int = 1408, ncache: int = 8) -> dict:
+ATTN_POS = 1088
+
+
+def attention_benchmark(launches: int = 64, B: int = 16, pos: int = ATTN_POS, cap: int = 1408, ncache: int = 8,
+                        timed: bool = True) -> dict:
     """Decode attention with the rotary step (sk_decode_attention_rope_bf16, the
     launch the decode step makes per layer) at the Qwen3-4B decode shape: B
     sequences at position ``pos``, 32/8 heads of 128, plan length 1152 (one key
@@ -492,6 +585,11 @@ def attention_benchmark(launches: int = 64, B: int = 16, pos: int = 1088, cap: i
             call(i)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
+    if not timed:   # counter probe: untimed eager launches only
+        for i in range(launches):
+            call(i)
+        torch.cuda.synchronize()
+        return {}
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(launches):
@@ -534,12 +632,17 @@ def main() -> int:
                     help="run only the C5 decode measurement and print its JSON object")
     ap.add_argument("--probe", action="store_true",
                     help="launch --probe-op at --M (untimed) and a 512 MiB copy, for rocprofv3 --pmc passes")
-    ap.add_argument("--probe-op", default="gate_up", choices=list(SHAPES),
+    ap.add_argument("--probe-op", default="gate_up", choices=list(SHAPES) + ["attention"],
                     help="the projection --probe launches (default gate_up)")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders of --probe (FETCH_SIZE, WRITE_SIZE) into "
                          "profiles/traffic_<probe-op>_m<M>.json and exit")
+    ap.add_argument("--counters-from", metavar="FOLDER",
+                    help="print a markdown row per probe from the rocprofv3 passes under FOLDER "
+                         "(<op>_m<M>_kt, _A, _B, _C, _D) and exit")
     args = ap.parse_args()
+    if args.counters_from:
+        return counters_summary(args.counters_from)
     if args.traffic_from:
         return traffic_summary(args.traffic_from[0], args.traffic_from[1], args.M, args.probe_op)
 

@@ -11,6 +11,7 @@ PyTorch-ROCm when both are loaded in one process.
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -22,6 +23,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "lib" / "libstarter_amd.so"
+TIERS_INC = CSRC / "sk_tiers.inc"
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -53,47 +55,46 @@ def _units() -> list[tuple[Path, list[str], Path]]:
     return units
 
 
-def _run(cmd: list[str]) -> list[tuple[str, int]]:
-    """Run one hipcc command; returns (kernel, VGPR spill count) of every
-    kernel whose resource-usage remark reports spilled registers."""
+def _run(cmd: list[str]) -> list[tuple[str, int, int]]:
+    """Run one hipcc command; returns (kernel, VGPR spill count, VGPRs + AGPRs
+    allocated) of every kernel whose resource-usage remark reports spilled
+    registers."""
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     # hipcc's host pass warns about the device-only target feature and the
     # resource-usage remarks are parsed, not printed; anything else is surfaced.
-    noise = ("packed-fp32-ops", "warning: feature flag", "1 warning generated", "warnings generated")
-    spills, name = [], None
+    noise = ("packed-fp32-ops", "warning: feature flag", "1 warning generated", "warnings generated",
+             "In file included from")
+    spills, name, regs = [], None, 0
     for line in (r.stderr or "").splitlines():
         if "kernel-resource-usage" in line:
+            field = lambda key: int(line.split(key)[1].split("[")[0])  # noqa: E731
             if "Function Name:" in line:
-                name = line.split("Function Name:")[1].split("[")[0].strip()
+                name, regs = line.split("Function Name:")[1].split("[")[0].strip(), 0
             elif "VGPRs Spill:" in line:
-                n = int(line.split("VGPRs Spill:")[1].split("[")[0])
-                if n:
-                    spills.append((name, n))
+                if field("VGPRs Spill:"):
+                    spills.append((name, field("VGPRs Spill:"), regs))
+            elif "VGPRs:" in line or "AGPRs:" in line:
+                regs += field("VGPRs:" if "VGPRs:" in line else "AGPRs:")
+            continue
+        if re.match(r"\s*\d*\s*\|", line):   # source excerpt under a remark
             continue
         if line.strip() and not any(n in line for n in noise):
             print(line, file=sys.stderr)
     return spills
 
 
-def build(jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> Path:
-    """Compile every HIP translation unit and link the shared library.
-    ``incremental``: recompile only the units whose object is older than their
-    source or any header (a development shortcut; the default rebuilds all)."""
-    if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
-        raise RuntimeError("hipcc not found; the library needs ROCm's hipcc to build")
-    BUILD.mkdir(parents=True, exist_ok=True)
-    LIB.parent.mkdir(parents=True, exist_ok=True)
-    jobs = jobs or min(16, os.cpu_count() or 4)
-    units = _units()
-    headers = max(p.stat().st_mtime for p in [*CSRC.glob("*.hpp"), *(ROOT / "include").glob("*.h")])
+def _compile(units, jobs: int, incremental: bool = False, verbose: bool = False):
+    """Compile units in parallel; returns [(object, spills)] in unit order."""
+    headers = max(p.stat().st_mtime for p in [*CSRC.glob("*.hpp"), *CSRC.glob("*.inc"),
+                                              *(ROOT / "include").glob("*.h")])
     spill_file = BUILD / "spills_by_unit.txt"
-    old_spills: dict[str, list[tuple[str, int]]] = {}
+    old_spills: dict[str, list[tuple[str, int, int]]] = {}
     if incremental and spill_file.exists():
         for line in spill_file.read_text().splitlines():
-            unit, name, n = line.split("\t")
-            old_spills.setdefault(unit, []).append((name, int(n)))
+            unit, name, n, regs = line.split("\t")
+            old_spills.setdefault(unit, []).append((name, int(n), int(regs)))
 
     def compile_one(u):
         src, defs, obj = u
@@ -106,21 +107,91 @@ def build(jobs: int | None = None, verbose: bool = False, incremental: bool = Fa
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         done = list(ex.map(compile_one, units))
-    objs = [o for o, _ in done]
+    spill_file.write_text("".join(f"{o.name}\t{n}\t{c}\t{g}\n" for o, sp in done for n, c, g in sp))
+    return done
+
+
+def build(jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile every HIP translation unit and link the shared library.
+    ``incremental``: recompile only the units whose object is older than their
+    source or any header (a development shortcut; the default rebuilds all).
+    Fails if any kernel spills VGPRs: every instance is compiled for a wave
+    count at which it keeps its registers (csrc/sk_tiers.inc, see retier)."""
+    if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
+        raise RuntimeError("hipcc not found; the library needs ROCm's hipcc to build")
+    BUILD.mkdir(parents=True, exist_ok=True)
+    LIB.parent.mkdir(parents=True, exist_ok=True)
+    jobs = jobs or min(16, os.cpu_count() or 4)
+    done = _compile(_units(), jobs, incremental, verbose)
     spilled = [s for _, sp in done for s in sp]
-    spill_file.write_text("".join(f"{o.name}\t{n}\t{c}\n" for o, sp in done for n, c in sp))
-    (BUILD / "spills.txt").write_text("".join(f"{n}\t{c}\n" for n, c in spilled))
     if spilled:
-        print(f"note: {len(spilled)} kernel instances spill VGPRs (list in {BUILD / 'spills.txt'})", file=sys.stderr)
+        names = "\n  ".join(f"{n} ({c} VGPRs spilled)" for n, c, _ in spilled[:20])
+        raise RuntimeError(f"{len(spilled)} kernel instances spill VGPRs:\n  {names}\n"
+                           "re-measure the tiers with `python -m starter_amd.build --retier`")
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, [o for o, _ in done])])
     os.replace(tmp, LIB)
     return LIB
+
+
+_INSTANCE = re.compile(r"_ZN2sk10(gemv|mfma|mfmt)_entryILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)EEEvNS_4ArgsE")
+_KINDS = {"gemv": 0, "mfma": 1, "mfmt": 2}
+# (waves per workgroup, VGPRs + AGPRs per lane the compiler may then use)
+_TIERS = ((16, 128), (12, 168), (8, 256), (4, 512))
+
+
+def _write_tiers(overrides: dict[tuple[int, ...], int]) -> None:
+    rows = "".join(f"    {{{k[0]}, {k[1]}, {k[2]}, {k[3]}, {k[4]}, {w}}},\n" for k, w in sorted(overrides.items()))
+    TIERS_INC.write_text(
+        "// Generated by `python -m starter_amd.build --retier`: instances compiled for\n"
+        "// fewer waves than their register estimate allows, or not compiled (waves 0).\n"
+        "// Fields: {kind (0 gemv, 1 mfma, 2 mfmt), template arguments a, b, c, epilogue, waves}.\n"
+        "constexpr TierOverride kTierOverrides[] = {\n" + rows +
+        "    {-1, 0, 0, 0, 0, 0},   // end marker\n};\n")
+
+
+def _read_tiers() -> dict[tuple[int, ...], int]:
+    out = {}
+    for line in TIERS_INC.read_text().splitlines() if TIERS_INC.exists() else []:
+        m = re.match(r"\s*\{(\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\},", line)
+        if m:
+            out[tuple(map(int, m.groups()[:5]))] = int(m.group(6))
+    return out
+
+
+def retier(jobs: int | None = None, fresh: bool = False) -> dict[tuple[int, ...], int]:
+    """Measure csrc/sk_tiers.inc: compile the kernel instances at their
+    estimated tiers, move every instance that spills one tier down (16, 12, 8,
+    4 waves; below 4 it is dropped) and compile again until nothing spills.
+    Starts from the current list unless ``fresh`` (then every instance starts
+    at its estimate: use after changing a kernel body)."""
+    BUILD.mkdir(parents=True, exist_ok=True)
+    jobs = jobs or min(16, os.cpu_count() or 4)
+    units = [u for u in _units() if u[0].name.startswith("sk_inst_")]
+    overrides: dict[tuple[int, ...], int] = {} if fresh else _read_tiers()
+    for rnd in range(len(_TIERS) + 1):
+        _write_tiers(overrides)
+        spilled = [s for _, sp in _compile(units, jobs) for s in sp]
+        print(f"retier pass {rnd}: {len(spilled)} instances spill", flush=True)
+        if not spilled:
+            return overrides
+        for name, _, regs in spilled:
+            m = _INSTANCE.fullmatch(name)
+            if not m:
+                raise RuntimeError(f"spilling kernel {name} is not a GEMM instance")
+            key = (_KINDS[m.group(1)], *map(int, m.groups()[1:]))
+            cur = overrides.get(key) or next(w for w, cap in _TIERS if regs <= cap)
+            lower = [w for w, _ in _TIERS if w < cur]
+            overrides[key] = lower[0] if lower else 0
+    raise RuntimeError("instances still spill at the 4-wave tier")
 
 
 if __name__ == "__main__":
     import time
 
     t0 = time.time()
+    if "--retier" in sys.argv:
+        ov = retier(fresh="--fresh" in sys.argv)
+        print(f"{len(ov)} tier overrides ({sum(w == 0 for w in ov.values())} instances dropped) in {TIERS_INC}")
     out = build(verbose="-v" in sys.argv, incremental="--incremental" in sys.argv)
     print(f"built {out} in {time.time() - t0:.1f}s")

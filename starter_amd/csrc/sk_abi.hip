@@ -201,7 +201,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tn = gateup ? 2 : c.rows / 16;
     pl->tku = bucket(sk::kMfmaKU, (int)(sizeof(sk::kMfmaKU) / sizeof(int)), c.ku);
     partial_rows = 16 * pl->tn;
-    if (c.waves > sk::max_waves_for_regs(sk::mfma_regs(pl->tm, pl->tn, pl->tku < 0 ? 20 : pl->tku)))
+    if (pl->tku < 0 || c.waves > sk::instance_waves(sk::KIND_MFMA, pl->tm, pl->tn, pl->tku, pl->epi))
       return SK_ERR_CONFIG;
   } else if (c.path == SK_PATH_MFMA_LDS) {
     // One K range of KW = 32*ku columns per wave: 256 or 1024 (one or four
@@ -214,7 +214,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tn = gateup ? 2 : c.rows / 16;
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
-    if (c.waves > sk::mfmt_max_waves(pl->tm, pl->tn, KW, variant == 1)) return SK_ERR_CONFIG;
+    if (c.waves > sk::instance_waves(sk::KIND_MFMT, pl->tm, pl->tn, KW, pl->epi)) return SK_ERR_CONFIG;
     pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
@@ -224,7 +224,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tn = c.rows;
     pl->tku = bucket(sk::kGemvKU, (int)(sizeof(sk::kGemvKU) / sizeof(int)), c.ku);
     partial_rows = gateup ? 2 * c.rows : c.rows;
-    if (c.waves > sk::max_waves_for_regs(sk::gemv_regs(pl->tm, partial_rows, pl->tku < 0 ? 10 : pl->tku, fused), fused))
+    if (pl->tku < 0 || c.waves > sk::instance_waves(sk::KIND_GEMV, pl->tm, pl->tn, pl->tku, pl->epi))
       return SK_ERR_CONFIG;
   } else {
     return SK_ERR_CONFIG;
@@ -320,7 +320,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 8, {3, 4, 32, 16, 1, 0}},  // o_proj     7.09 us  2971 GB/s
     {SK_OP_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj     7.47 us  2834 GB/s
     {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj     9.13 us  2343 GB/s
-    {SK_OP_GEMM, 2560, 4096, 40, {3, 6, 8, 32, 3, 0}},  // o_proj    11.63 us  1849 GB/s
+    {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 16, 1, 0}},  // o_proj    11.47 us  1874 GB/s
     {SK_OP_GEMM, 2560, 4096, 64, {3, 6, 8, 16, 3, 0}},  // o_proj    14.44 us  1511 GB/s
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
@@ -330,7 +330,7 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 16, {3, 10, 8, 16, 1, 203}},  // gate_up   18.13 us  5515 GB/s
     {SK_OP_GATEUP, 9728, 2560, 32, {3, 5, 8, 16, 2, 0}},  // gate_up   29.24 us  3434 GB/s
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 5, 8, 16, 2, 0}},  // gate_up   33.86 us  2976 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 64, {1, 5, 8, 16, 2, 0}},  // gate_up   56.95 us  1777 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 64, {1, 4, 10, 16, 2, 0}},  // gate_up   44.93 us  2252 GB/s
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {3, 13, 8, 32, 3, 0}},  // down      12.60 us  3962 GB/s
@@ -345,8 +345,8 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 8, {3, 10, 8, 32, 1, 0}},  // lm_head  113.31 us  6866 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 16, {3, 10, 8, 32, 1, 0}},  // lm_head  114.35 us  6804 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 32, {3, 5, 16, 16, 1, 0}},  // lm_head  119.79 us  6495 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 40, {1, 8, 10, 16, 1, 0}},  // lm_head  160.11 us  4860 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {1, 8, 10, 16, 1, 0}},  // lm_head  190.38 us  4088 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 40, {1, 8, 10, 16, 1, 0}},  // lm_head  167.51 us  4645 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {1, 4, 20, 16, 1, 0}},  // lm_head  216.47 us  3595 GB/s
 };
 
 // Tuned entry for op/N/K at the smallest tuned row count >= M (rows beyond

@@ -11,15 +11,20 @@
 namespace sk {
 
 template <int MR, int R, int KU, int EPI>
-__global__ void __launch_bounds__(
-    64 * max_waves_for_regs(gemv_regs(MR, EpiTraits<EPI>::gateup ? 2 * R : R, KU, EpiTraits<EPI>::norm),
-                            EpiTraits<EPI>::norm))
+__global__ void __launch_bounds__(64 * instance_waves(KIND_GEMV, MR, R, KU, EPI))
 gemv_entry(Args p) {
   gemv_body<MR, R, KU, EPI>(p);
 }
 
+// An instance with no spill-free tier is not instantiated.
+template <int MR, int R, int KU, int EPI>
+KernelFn gemv_ptr() {
+  if constexpr (instance_waves(KIND_GEMV, MR, R, KU, EPI) > 0) return &gemv_entry<MR, R, KU, EPI>;
+  else return nullptr;
+}
+
 #define SK_C(MR, R, KU) \
-  case MR * 10000 + R * 100 + KU: return &gemv_entry<MR, R, KU, SK_EPI>;
+  case MR * 10000 + R * 100 + KU: return gemv_ptr<MR, R, KU, SK_EPI>();
 #define SK_R(MR, R) SK_C(MR, R, 2) SK_C(MR, R, 5) SK_C(MR, R, 8) SK_C(MR, R, 10)
 #define SK_MR(MR) SK_R(MR, 2) SK_R(MR, 4) SK_R(MR, 8)
 

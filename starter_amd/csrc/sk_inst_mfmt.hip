@@ -11,16 +11,23 @@
 namespace sk {
 
 template <int MT, int NT, int KW, int EPI>
-__global__ void __launch_bounds__(64 * mfmt_max_waves(MT, NT, KW, EpiTraits<EPI>::pre))
+__global__ void __launch_bounds__(64 * instance_waves(KIND_MFMT, MT, NT, KW, EPI))
 mfmt_entry(Args p) {
   mfmt_body<MT, NT, KW, EPI>(p);
 }
 
+// An instance with no spill-free tier is not instantiated.
+template <int MT, int NT, int KW, int EPI>
+KernelFn mfmt_ptr() {
+  if constexpr (instance_waves(KIND_MFMT, MT, NT, KW, EPI) > 0) return &mfmt_entry<MT, NT, KW, EPI>;
+  else return nullptr;
+}
+
 #define SK_C(MT, NT, KW) \
-  case MT * 100000 + NT * 1000 + KW: return &mfmt_entry<MT, NT, KW, SK_EPI>;
+  case MT * 100000 + NT * 1000 + KW: return mfmt_ptr<MT, NT, KW, SK_EPI>();
 #define SK_LIST(NT) \
   SK_C(1, NT, 512) SK_C(2, NT, 512) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(3, NT, 256) SK_C(4, NT, 256) \
-  SK_C(1, NT, 1024) SK_C(2, NT, 1024)
+  SK_C(1, NT, 1024) SK_C(2, NT, 1024) SK_C(3, NT, 1024) SK_C(4, NT, 1024)
 
 // Residual hand-off epilogues exist on the ring path only: the consumers
 // (EPI 8-10) with one 256-column chunk per wave, the producers (EPI 11-12)

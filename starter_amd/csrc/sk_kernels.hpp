@@ -287,17 +287,24 @@ __device__ __forceinline__ u32x4 norm_line_bf16x8(u32x4 x, const u32x4& wlo, con
 // only weight loads, so the compiler can keep all of them in flight (global
 // stores would share the vmcnt counter with those loads).
 // ---------------------------------------------------------------------------
+constexpr bool epi_norm(int e) { return e >= EPI_STORE_NORM && e <= EPI_ARGMAX_NORM; }
+constexpr bool epi_pre(int e) { return e >= EPI_STORE_PRE && e <= EPI_ARGMAX_PRE; }
+constexpr int epi_base(int e) {   // the epilogue proper, without prologue or residual hand-off
+  return epi_norm(e) ? e - EPI_STORE_NORM
+         : epi_pre(e) ? e - EPI_STORE_PRE
+         : e == EPI_STORE_RESID ? EPI_STORE
+         : e == EPI_PART_RESID  ? EPI_PART
+                                : e;
+}
+constexpr bool epi_gateup(int e) { return epi_base(e) == EPI_SWIGLU || epi_base(e) == EPI_PART_GU; }
+
 template <int EPI>
 struct EpiTraits {
-  static constexpr bool norm = EPI >= EPI_STORE_NORM && EPI <= EPI_ARGMAX_NORM;
-  static constexpr bool pre = EPI >= EPI_STORE_PRE && EPI <= EPI_ARGMAX_PRE;
+  static constexpr bool norm = epi_norm(EPI);
+  static constexpr bool pre = epi_pre(EPI);
   static constexpr bool resid = EPI == EPI_STORE_RESID || EPI == EPI_PART_RESID;
-  static constexpr int base = norm  ? EPI - EPI_STORE_NORM   // the epilogue proper
-                              : pre ? EPI - EPI_STORE_PRE
-                              : EPI == EPI_STORE_RESID ? EPI_STORE
-                              : EPI == EPI_PART_RESID  ? EPI_PART
-                                                       : EPI;
-  static constexpr bool gateup = (base == EPI_SWIGLU || base == EPI_PART_GU);
+  static constexpr int base = epi_base(EPI);
+  static constexpr bool gateup = epi_gateup(EPI);
   // bytes per staged output element (PART_GU stages gate and up fp32 sums)
   static constexpr int stage_bytes = base == EPI_STORE || base == EPI_SWIGLU ? 2 : (base == EPI_PART ? 4 : 8);
 };

@@ -55,6 +55,31 @@ constexpr int mfmt_max_waves(int MT, int NT, int KW, bool pre = false) {
   return pre ? max_waves_for_regs(mfmt_regs(MT, NT, KW) + 48, true) : max_waves_for_regs(mfmt_regs(MT, NT, KW));
 }
 
+// Waves per workgroup each instance is compiled for.  The estimates above
+// decide it, except for the instances listed in sk_tiers.inc: those spilled
+// VGPRs at their estimate's tier and are compiled for the largest tier at
+// which the compiler reported no spill (waves 0: they spill even with 512
+// registers per lane and are not compiled at all).  The list is measured by
+// `python -m starter_amd.build --retier`; the regular build fails if any
+// instance spills, so a stale list cannot go unnoticed.
+enum InstKind { KIND_GEMV = 0, KIND_MFMA = 1, KIND_MFMT = 2 };
+struct TierOverride {
+  int kind, a, b, c, epi, waves;   // (a, b, c) = the instance's template arguments before EPI
+};
+#include "sk_tiers.inc"   // constexpr TierOverride kTierOverrides[] = {..., {-1, ...}}
+
+constexpr int estimate_waves(int kind, int a, int b, int c, int epi) {
+  return kind == KIND_GEMV
+             ? max_waves_for_regs(gemv_regs(a, epi_gateup(epi) ? 2 * b : b, c, epi_norm(epi)), epi_norm(epi))
+         : kind == KIND_MFMA ? max_waves_for_regs(mfma_regs(a, b, c))
+                             : mfmt_max_waves(a, b, c, epi_pre(epi));
+}
+constexpr int instance_waves(int kind, int a, int b, int c, int epi) {
+  for (const TierOverride& t : kTierOverrides)
+    if (t.kind == kind && t.a == a && t.b == b && t.c == c && t.epi == epi) return t.waves;
+  return estimate_waves(kind, a, b, c, epi);
+}
+
 KernelFn mfma_for_epi0(int MT, int NT, int KU);
 KernelFn mfma_for_epi1(int MT, int NT, int KU);
 KernelFn mfma_for_epi2(int MT, int NT, int KU);

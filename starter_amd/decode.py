@@ -114,6 +114,30 @@ class SyntheticModel:
         self.scale = 1.0 / math.sqrt(D)
 
 
+def decode_matmuls(m: SyntheticModel, M: int, log=None) -> dict:
+    """The per-shape projection callables for M-row decode/verify steps
+    (engine/model.py:137-179, the norm-fused branch): "qkv", "gu" and "lm" take
+    ``(x, y, w_norm, xout, w)``, write ``xout = x + y`` and project
+    ``rms_norm(xout)``; "o" and "d" take ``(a, w)``.  "lm" returns the logits
+    like the reference's; "lm_argmax" is the same call with the greedy argmax
+    fused in, returning ``(ids, maxv)`` without storing logits.  The configs
+    come from the library's table (no warmup timing); ``log`` receives one
+    line per choice."""
+    cfg = m.cfg
+    layer = m.layers[0]
+    x = torch.empty((M, cfg.hidden), dtype=BF16, device=m.device)
+    a = torch.empty((M, cfg.heads * cfg.head_dim), dtype=BF16, device=m.device)
+    act = torch.empty((M, cfg.intermediate), dtype=BF16, device=m.device)
+    return {
+        "qkv": K.pick_normed("matmul", x, x, layer.in_norm, layer.wqkv, cfg.eps, log),
+        "o": K.pick_matmul(a, layer.wo, log),
+        "gu": K.pick_normed("gateup", x, x, layer.post_norm, layer.wgu, cfg.eps, log),
+        "d": K.pick_matmul(act, layer.wd, log),
+        "lm": K.pick_normed("matmul", x, x, m.final_norm, m.lm_head, cfg.eps, log),
+        "lm_argmax": K.pick_lm_argmax(x, m.lm_head, cfg.eps, log),
+    }
+
+
 class DecodePlan:
     """Static buffers, KV cache and step functions for one (B, T, max_new) shape
     (engine/model.py:215-262).  ``decode()`` touches only preallocated tensors
@@ -143,12 +167,8 @@ class DecodePlan:
         self.q = torch.empty((B, HQ, 1, D), dtype=BF16, device=dev)
         self.attn_out = torch.empty((B, 1, HQ, D), dtype=BF16, device=dev)
         self.attention = K.DecodeAttention(B, HQ, HKV, D, self.cap, dev, maxlen=min(self.cap, T + max_new))
-        # the decode-step projections (decode_matmuls, engine/model.py:137-179)
-        self.mm_qkv = K.SkinnyMatmul(B, (HQ + 2 * HKV) * D, H, dev, normed=True)
-        self.mm_o = K.SkinnyMatmul(B, H, HQ * D, dev)
-        self.mm_gu = K.SkinnyGateUp(B, I, H, dev, normed=True)
-        self.mm_d = K.SkinnyMatmul(B, H, I, dev)
-        self.mm_lm = K.LmArgmax(B, cfg.vocab, H, dev, normed=True)
+        # the decode-step projections (engine/model.py:137-179)
+        self.mm = decode_matmuls(model, B)
         if handoff:
             # residual hand-off: partial sums of squares of the residual rows
             # (16-column groups) and one zero-filled workspace per call site
@@ -208,18 +228,19 @@ class DecodePlan:
         if self.handoff:
             self._decode_handoff(x)
             return
+        # run_layers (engine/model.py:182-210) over the decode_matmuls callables
+        mm = self.mm
         cur, y = x, self.zero
         for i, layer in enumerate(m.layers):
-            qkv = self.mm_qkv(cur, layer.wqkv, norm=(y, layer.in_norm, self.xa, cfg.eps))
+            qkv = mm["qkv"](cur, y, layer.in_norm, self.xa, layer.wqkv)
             K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, self.cos, self.sin, self.pos, self.q,
                                  self.k_cache[i], self.v_cache[i], 1, cfg.eps)
             self.attention(self.q, self.k_cache[i], self.v_cache[i], self.pos, self.attn_out)
-            o = self.mm_o(self.attn_out.view(B, cfg.heads * cfg.head_dim), layer.wo)
-            I = cfg.intermediate
-            act = self.mm_gu(self.xa, layer.wgu[:I], layer.wgu[I:], norm=(o, layer.post_norm, self.xb, cfg.eps))
-            y = self.mm_d(act, layer.wd)
+            o = mm["o"](self.attn_out.view(B, cfg.heads * cfg.head_dim), layer.wo)
+            act = mm["gu"](self.xa, o, layer.post_norm, self.xb, layer.wgu)
+            y = mm["d"](act, layer.wd)
             cur = self.xb
-        ids, _ = self.mm_lm(cur, m.lm_head, norm=(y, m.final_norm, self.xa, cfg.eps))
+        ids, _ = mm["lm_argmax"](cur, y, m.final_norm, self.xa, m.lm_head)
         self.tok.copy_(ids)
         self.pos.add_(1)
 
@@ -232,7 +253,7 @@ class DecodePlan:
         B, I, eps = self.B, cfg.intermediate, cfg.eps
         for i, layer in enumerate(m.layers):
             if i == 0:
-                qkv = self.mm_qkv(x, layer.wqkv, norm=(self.zero, layer.in_norm, self.xa, eps))
+                qkv = self.mm["qkv"](x, self.zero, layer.in_norm, self.xa, layer.wqkv)
             else:
                 qkv = K.rmsnorm_pre_gemm(self.xa, self.sq_a, layer.in_norm, eps, layer.wqkv, out=self.qkv,
                                          ws=self.ws_qkv)

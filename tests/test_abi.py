@@ -262,7 +262,11 @@ def test_normed_workspace_layout_for_unfused_configs():
     mfma = SkConfig.make(SK_PATH_MFMA, 8, 10, 16)
     assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 8, 6144, 2560, mfma) == 8 * 2560 * 2
     # rows beyond 64: the separate prologue normalises all rows at once
-    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 100, 6144, 2560, mfma) == 100 * 2560 * 2
+    mfma_split = SkConfig.make(SK_PATH_MFMA, 8, 5, 16, 2)
+    base100 = _lib.workspace_bytes(SK_OP_GEMM, 100, 6144, 2560, mfma_split)
+    assert base100 > 0
+    assert _lib.workspace_bytes(SK_OP_RMSNORM_GEMM, 100, 6144, 2560, mfma_split) == \
+        (base100 + 255) // 256 * 256 + 100 * 2560 * 2
 
 
 def test_normed_argument_validation():

@@ -182,7 +182,7 @@ def test_decode_c5_size_graph_replay_matches_eager_and_reference():
     (seed 11), prefill, then all 127 decode steps replayed from the captured
     graph (M = 16 hand-off consumers, one-split attention over ~1100 keys).
     The replayed tokens equal eager decode token for token, and each token
-    scores within max(0.125, 2D) of the maximum logit at its position of both
+    scores within max(0.125, D) of the maximum logit at its position of both
     the fp32 and the fp64 restatement, D being how far those two restatements
     themselves differ there (the restatements run over the sequence the engine
     consumed; their lm_head only at the 128 decoded positions)."""
@@ -229,3 +229,43 @@ def test_decode_c5_size_graph_replay_matches_eager_and_reference():
         assert torch.equal(out[decided], top2.indices[..., 0][decided]), report
     assert report["fp64"]["agree"] >= agree32 - 0.05, report
     print("C5 decode parity:", report)
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_decode_matmuls_callables(M):
+    """decode_matmuls (engine/model.py:137-179): each callable returns what the
+    library call it wraps returns for the same inputs, bit for bit, and writes
+    the same residual; "lm_argmax" picks the argmax of "lm"'s logits."""
+    from starter_amd import kernels as K
+    from starter_amd.decode import decode_matmuls
+
+    m = SyntheticModel(CFG, DEV, seed=5, norm_noise=0.1)
+    mm = decode_matmuls(m, M)
+    g = torch.Generator(device=DEV).manual_seed(M)
+    H, I = CFG.hidden, CFG.intermediate
+    x = torch.randn(M, H, generator=g, device=DEV).to(torch.bfloat16)
+    y = torch.randn(M, H, generator=g, device=DEV).to(torch.bfloat16)
+    a = torch.randn(M, CFG.heads * CFG.head_dim, generator=g, device=DEV).to(torch.bfloat16)
+    act = torch.randn(M, I, generator=g, device=DEV).to(torch.bfloat16)
+    layer, eps = m.layers[0], CFG.eps
+    xo1, xo2 = torch.empty_like(x), torch.empty_like(x)
+
+    out = mm["qkv"](x, y, layer.in_norm, xo1, layer.wqkv)
+    ref = K.rmsnorm_gemm(x, y, layer.in_norm, eps, xo2, layer.wqkv)
+    assert torch.equal(out, ref) and torch.equal(xo1, xo2) and torch.equal(xo1, (x.float() + y.float()).bfloat16())
+    assert torch.equal(mm["o"](a, layer.wo), K.gemm(a, layer.wo))
+    out = mm["gu"](x, y, layer.post_norm, xo1, layer.wgu)
+    ref = K.rmsnorm_gateup_swiglu(x, y, layer.post_norm, eps, xo2, layer.wgu[:I], layer.wgu[I:])
+    assert torch.equal(out, ref) and torch.equal(xo1, xo2)
+    assert torch.equal(mm["d"](act, layer.wd), K.gemm(act, layer.wd))
+    logits = mm["lm"](x, y, m.final_norm, xo1, m.lm_head)
+    assert torch.equal(logits, K.rmsnorm_gemm(x, y, m.final_norm, eps, xo2, m.lm_head))
+    ids, maxv = mm["lm_argmax"](x, y, m.final_norm, xo2, m.lm_head)
+    torch.cuda.synchronize()
+    # the fused argmax may sum in another order than the logits GEMM's config:
+    # ids must agree wherever the top-2 margin exceeds 1e-2 of the max
+    top2 = logits.float().topk(2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 1e-2 * top2[:, 0].abs()
+    assert clear.sum() >= M // 2
+    assert torch.equal(ids[clear], logits.float().argmax(-1)[clear])
+    assert torch.allclose(maxv, top2[:, 0], rtol=1e-2, atol=0)

@@ -108,7 +108,7 @@ GEMM_CONFIGS = [
     SkConfig.make(SK_PATH_MFMA, waves=4, ku=5, rows=16, split=4),
     SkConfig.make(SK_PATH_MFMA, waves=4, ku=20, rows=16, grid=64),
     SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=4),
-    SkConfig.make(SK_PATH_GEMV, waves=1, ku=5, rows=8),
+    SkConfig.make(SK_PATH_GEMV, waves=3, ku=2, rows=8),
     SkConfig.make(SK_PATH_GEMV, waves=2, ku=3, rows=2),
     SkConfig.make(SK_PATH_GEMV, waves=1, ku=2, rows=4, split=3),
     SkConfig.make(SK_PATH_MFMA_LDS, waves=5, ku=16, rows=16),
