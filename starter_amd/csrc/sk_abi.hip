@@ -114,7 +114,8 @@ struct Plan {
   int slice_units = 0;
   int out_rows = 0;             // output columns per tile
   size_t pre_lds = 0;           // per-wave weight staging (LDS-transposed MFMA path)
-  size_t parts_lds = 0;         // double-buffered fp32 partial tiles
+  size_t parts_lds = 0;         // fp32 partial tiles (pbuf buffers)
+  int pbuf = 2;                 // partial tile buffers (1 only on the ring path when 2 do not fit)
   size_t stage_elem = 0;        // LDS bytes per staged tile (0: argmax keeps 8*M bytes)
   size_t lds = 0;               // total dynamic LDS (set once the grid is known)
   bool norm = false;            // the op has the add + RMSNorm prologue
@@ -247,6 +248,14 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   if (c.grid > 0 && (c.grid % c.split) != 0) return SK_ERR_CONFIG;
   const int tiles_per = c.grid > 0 ? cdiv(pl->nrb, c.grid / c.split) : 1;
   pl->lds = plan_lds(*pl, M, tiles_per);
+  // The ring path can work with one partial tile buffer (one more barrier per
+  // tile) where two would not fit.
+  const bool ring = c.path == SK_PATH_MFMA_LDS && pl->tku != 512;
+  if (ring && (pl->lds > kMaxLds || (c.grid == 0 && plan_lds(*pl, M, cdiv(pl->nrb, kMaxGrid)) > kMaxLds))) {
+    pl->pbuf = 1;
+    pl->parts_lds /= 2;
+    pl->lds = plan_lds(*pl, M, tiles_per);
+  }
   if (pl->lds > kMaxLds) return SK_ERR_CONFIG;
   // A derived grid holds at most kMaxGrid workgroups per K split, so every
   // workgroup may have to stage cdiv(nrb, kMaxGrid) tiles.
@@ -311,7 +320,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 6144, 2560, 16, {3, 10, 8, 32, 1, 192}},  // qkv        8.43 us  3764 GB/s
     {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
-    {SK_OP_GEMM, 6144, 2560, 32, {3, 3, 32, 32, 1, 0}},  // qkv       12.84 us  2494 GB/s
+    {SK_OP_GEMM, 6144, 2560, 32, {3, 10, 8, 32, 1, 0}},  // qkv       10.22 us  3134 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {3, 5, 8, 16, 2, 256}},  // qkv       15.51 us  2083 GB/s
     {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
     {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
@@ -328,7 +337,7 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 4, {3, 10, 8, 16, 1, 203}},  // gate_up   17.37 us  5739 GB/s
     {SK_OP_GATEUP, 9728, 2560, 8, {3, 10, 8, 16, 1, 203}},  // gate_up   17.49 us  5707 GB/s
     {SK_OP_GATEUP, 9728, 2560, 16, {3, 10, 8, 16, 1, 203}},  // gate_up   18.13 us  5515 GB/s
-    {SK_OP_GATEUP, 9728, 2560, 32, {3, 5, 8, 16, 2, 0}},  // gate_up   29.24 us  3434 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 32, {3, 10, 8, 16, 1, 0}},  // gate_up   21.56 us  4656 GB/s (one partial buffer)
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 5, 8, 16, 2, 0}},  // gate_up   33.86 us  2976 GB/s
     {SK_OP_GATEUP, 9728, 2560, 64, {1, 4, 10, 16, 2, 0}},  // gate_up   44.93 us  2252 GB/s
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
@@ -338,7 +347,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 16, {3, 4, 32, 32, 3, 0}},  // down      15.14 us  3316 GB/s
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {3, 7, 8, 32, 6, 240}},  // down      19.22 us  2642 GB/s
-    {SK_OP_GEMM, 2560, 9728, 64, {3, 7, 8, 16, 6, 240}},  // down      24.95 us  2059 GB/s
+    {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 4, {3, 10, 8, 32, 1, 0}},  // lm_head  113.49 us  6855 GB/s
@@ -741,6 +750,7 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
     a.nw = pl.cfg.waves;
     a.grid = grid;
     a.rbstep = grid / pl.cfg.split;
+    a.pbuf = pl.pbuf;
     pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
     if ((st = launch_status())) return st;
   }
@@ -899,6 +909,7 @@ int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const s
   a.nw = pl.cfg.waves;
   a.grid = grid;
   a.rbstep = grid / pl.cfg.split;
+  a.pbuf = pl.pbuf;
   pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
   return launch_status();
 }

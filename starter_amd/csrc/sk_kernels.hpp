@@ -105,6 +105,10 @@ struct Args {
   int64_t ldr;
   float* SQ;
   int sq_ld;
+  // LDS buffers for the waves' fp32 partial tiles on the ring path: 2 (tile
+  // j + 1 writes while tile j is reduced), or 1 when two do not fit (one more
+  // barrier per tile).  The other bodies always use 2.
+  int pbuf;
 };
 
 // ---------------------------------------------------------------------------
@@ -938,7 +942,7 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
   float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
   const int part_floats = nw * M * ROWS;
-  void* stage = parts + 2 * part_floats;
+  void* stage = parts + p.pbuf * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
   if constexpr (BASE == EPI_ARGMAX) {
     if (tid < M) lds_best[tid] = 0ull;
@@ -1122,7 +1126,8 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
         }
       }
     }
-    float* P = parts + (j & 1) * part_floats;
+    float* P = parts + (p.pbuf == 2 ? (j & 1) : 0) * part_floats;
+    if (p.pbuf == 1 && j > 0) lds_barrier();   // one buffer: the previous tile's reduction has read it
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll

@@ -43,16 +43,15 @@ constexpr int mfmt_regs(int MT, int NT, int KW) {
 }
 
 // Waves per workgroup an instance is compiled for (its __launch_bounds__):
-// 16 waves leave 128 VGPRs per lane, 8 waves 256; norm-prologue instances
-// also have a 12-wave tier (168 VGPRs).
-constexpr int max_waves_for_regs(int regs, bool norm = false) {
-  return regs <= 128 ? 16 : (norm && regs <= 168 ? 12 : (regs <= 256 ? 8 : 4));
+// 16 waves leave 128 VGPRs per lane, 12 waves 168, 8 waves 256, 4 waves 512.
+constexpr int max_waves_for_regs(int regs) {
+  return regs <= 128 ? 16 : (regs <= 168 ? 12 : (regs <= 256 ? 8 : 4));
 }
 // Waves per workgroup an LDS-fed MFMA instance is compiled for.  The residual
 // hand-off consumers (pre) also hold the norm weights of their chunk and the
-// producer's partial sums (48 more registers) and use the 12-wave tier.
+// producer's partial sums (48 more registers).
 constexpr int mfmt_max_waves(int MT, int NT, int KW, bool pre = false) {
-  return pre ? max_waves_for_regs(mfmt_regs(MT, NT, KW) + 48, true) : max_waves_for_regs(mfmt_regs(MT, NT, KW));
+  return max_waves_for_regs(mfmt_regs(MT, NT, KW) + (pre ? 48 : 0));
 }
 
 // Waves per workgroup each instance is compiled for.  The estimates above
@@ -70,7 +69,7 @@ struct TierOverride {
 
 constexpr int estimate_waves(int kind, int a, int b, int c, int epi) {
   return kind == KIND_GEMV
-             ? max_waves_for_regs(gemv_regs(a, epi_gateup(epi) ? 2 * b : b, c, epi_norm(epi)), epi_norm(epi))
+             ? max_waves_for_regs(gemv_regs(a, epi_gateup(epi) ? 2 * b : b, c, epi_norm(epi)))
          : kind == KIND_MFMA ? max_waves_for_regs(mfma_regs(a, b, c))
                              : mfmt_max_waves(a, b, c, epi_pre(epi));
 }

@@ -212,6 +212,27 @@ def test_gateup_qwen_default_config(M):
     assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup M={M}")
 
 
+@pytest.mark.parametrize("M", [17, 24, 32])
+@pytest.mark.parametrize("grid", [0, 96])
+def test_ring_one_partial_buffer(M, grid):
+    """10 waves of 32 rows on the ring path need one partial-tile buffer in LDS
+    (two do not fit): one more barrier per tile, several tiles per workgroup
+    (grid 96: six or seven tiles each).  gate/up+SwiGLU and a ragged GEMM."""
+    I2, Kd = GU
+    I = I2 // 2
+    cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, grid=grid)
+    wgu = _weights(I2, Kd, seed=29)
+    x = _acts(M, Kd, seed=29)
+    wd = _gpu(wgu)
+    out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:], config=cfg)
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup one buffer M={M} grid={grid}")
+    N = 6144 - 48
+    w = _weights(N, Kd, seed=31)
+    cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=32, grid=grid)
+    out = K.gemm(x.to(DEV), _gpu(w), config=cfg)
+    assert_parity(out, _oracle_gemm(x, w), f"gemm one buffer M={M} grid={grid}")
+
+
 GATEUP_CONFIGS = [
     SkConfig.make(SK_PATH_MFMA, waves=8, ku=10, rows=16),
     SkConfig.make(SK_PATH_MFMA, waves=16, ku=5, rows=16),
