@@ -380,13 +380,18 @@ __device__ __forceinline__ float load_agent(const float* p) {
 
 // Write the staged outputs of this workgroup's tiles (after the stream).
 // Split-K partials are stored device-coherent for the fixup below.
-// Residual hand-off for output element (m, n) with bf16 projection value yb:
+// Residual hand-off for output element (m, n) with bf16 projection value yb
+// and residual rb = R[m][n] (resid_in; the split-K finish requests it with the
+// partials, so it costs no round trip of its own):
 // xout = bf16(r + y) goes to RO and the sum of xout^2 over each 16-column
 // group (the 16 consecutive lanes that hold it, added in a fixed butterfly
 // order) goes to SQ[m][n / 16].  Every lane of the group must call this;
 // ok = false (a column past N) contributes zero and stores nothing.
-__device__ __forceinline__ void resid_out(const Args& p, int m, int n, bool ok, uint16_t yb) {
-  const float xo = ok ? round_bf(bf2f(p.R[(int64_t)m * p.ldr + n]) + bf2f(yb)) : 0.f;
+__device__ __forceinline__ uint16_t resid_in(const Args& p, int m, int n, bool ok) {
+  return ok ? p.R[(int64_t)m * p.ldr + n] : (uint16_t)0;
+}
+__device__ __forceinline__ void resid_out(const Args& p, int m, int n, bool ok, uint16_t yb, uint16_t rb) {
+  const float xo = ok ? round_bf(bf2f(rb) + bf2f(yb)) : 0.f;
   if (ok) p.RO[(int64_t)m * p.ldr + n] = f2bf(xo);
   float sq = xo * xo;
   sq += __shfl_xor(sq, 1);
@@ -410,7 +415,7 @@ __device__ __forceinline__ void flush_stage(const Args& p, const void* stage, in
     const int n = (rb0 + j * p.rbstep) * OUT_ROWS + r;
     if constexpr (RESID) {
       static_assert(EPI == EPI_STORE, "the residual follows a finished projection");
-      resid_out(p, m, n, n < p.N, static_cast<const uint16_t*>(stage)[idx]);
+      resid_out(p, m, n, n < p.N, static_cast<const uint16_t*>(stage)[idx], resid_in(p, m, n, n < p.N));
       continue;
     }
     if (n >= p.N) continue;
@@ -470,11 +475,13 @@ __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0,
         constexpr int NP = EPI == EPI_PART_GU ? 2 : 1;   // gate and up partials
         float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
         int64_t e[4];
+        uint16_t rres[4];   // RESID: the residual, requested with the partials
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int idx = min(base + (int)threadIdx.x + i * nthr, M * OUT_ROWS - 1);
           const int m = idx / OUT_ROWS, n = rb * OUT_ROWS + idx % OUT_ROWS;
           e[i] = (int64_t)m * p.N + (n < p.N ? n : 0);   // clamped in bounds; stored only if real
+          if constexpr (RESID) rres[i] = resid_in(p, m, n, n < p.N);
         }
         // Sums in split order s = 0..S-1, all loads of a batch issued first.
         for (int s0 = 0; s0 < S; s0 += kFixupBatch) {
@@ -504,7 +511,7 @@ __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0,
             // every lane of a 16-column group takes part in the group sum
             // (idx < M*OUT_ROWS is uniform over each 16-lane group)
             static_assert(EPI == EPI_PART && OUT_ROWS % 16 == 0, "residual after split-K partials");
-            if (idx < M * OUT_ROWS) resid_out(p, m, n, n < p.N, f2bf(n < p.N ? g[i] : 0.f));
+            if (idx < M * OUT_ROWS) resid_out(p, m, n, n < p.N, f2bf(n < p.N ? g[i] : 0.f), rres[i]);
             continue;
           }
           if (idx >= M * OUT_ROWS || n >= p.N) continue;
