@@ -527,12 +527,61 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None
     # step's tokens copied to pinned host memory, GPU kept 3 steps ahead)
     d = time_delivery(plan, ids, steps + 1)
     log(f"decode with host delivery: {d['delivered_tok_s']:.0f} tok/s delivered, end-to-end {d['e2e_tok_s']:.0f} tok/s")
+    v = verify_benchmark(plan)
     out = {"tok_s": round(r["tok_s"], 1), "ms_per_step": round(r["ms_per_step"], 4), "steps": steps, "B": B,
            "prompt": T, "prefill_s": round(r["prefill_s"], 4), "e2e_tok_s": round(r["e2e_tok_s"], 1),
            "host_delivery": {"delivered_tok_s": round(d["delivered_tok_s"], 1), "e2e_tok_s": round(d["e2e_tok_s"], 1),
                              "first_token_s": round(d["first_token_s"], 4), "depth": d["depth"]},
-           "workload": "synthetic qwen3-4b greedy decode, 36 layers, GQA 32/8, cap %d, HIP graph per step" % plan.cap}
+           "workload": "synthetic qwen3-4b greedy decode, 36 layers, GQA 32/8, cap %d, HIP graph per step" % plan.cap,
+           "verify": v}
     return out
+
+
+def verify_benchmark(plan, R: int = 4, parents=(-1, 0, 0, 1), replays: int = 20) -> dict:
+    """One speculative verify pass (engine/model.py:334-375) over the decode
+    model's cache: B sequences x R rows (a draft tree), M = B*R rows through
+    every projection, tree-masked attention, greedy token per row; captured
+    into a HIP graph and replayed at the position the decode left (the same
+    cache slots are rewritten each replay).  Reports the pass time and rows
+    verified per second."""
+    import statistics
+
+    import torch
+
+    from starter_amd.decode import VerifyPlan
+
+    vp = VerifyPlan(plan, R, tree=True)
+    vp.set_tree(list(parents))
+    g = torch.Generator(device="cuda:0").manual_seed(5)
+    vp.blk.copy_(torch.randint(0, plan.model.cfg.vocab, vp.blk.shape, device="cuda:0", generator=g))
+    vp.pos.copy_(plan.pos)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        vp.verify()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        vp.verify()
+    graph.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = statistics.median(ts)
+    B = plan.B
+    pos = int(plan.pos[0])
+    _KEEP.append((vp, graph))
+    log(f"verify: B={B} x R={R} rows (tree {list(parents)}) at position {pos}: {ms:.3f} ms per pass, "
+        f"{B * R / ms * 1e3:.0f} rows/s")
+    return {"B": B, "R": R, "tree_parents": list(parents), "position": pos, "ms_per_pass": round(ms, 4),
+            "rows_per_s": round(B * R / ms * 1e3, 1), "replays": replays}
 
 
 _KEEP: list = []   # attention workloads stay allocated until the process ends (no device frees)

@@ -356,6 +356,80 @@ class DecodePlan:
         return out
 
 
+class VerifyPlan:
+    """Speculative verification (engine/model.py:334-375): R query rows per
+    sequence in one pass over the plan's model and KV cache.  Row 0 holds the
+    last accepted token, rows 1..R-1 the drafts, as a chain or, with
+    ``tree=True``, a draft tree given by its parent list (``set_tree``).  The
+    forward writes row t of sequence b to cache slot pos[b] + t (rotated by
+    position pos[b] + depth[t] in a tree) and returns the greedy token after
+    every row; accepting a path is the caller's policy.  The projections run
+    at M = B * R rows through ``decode_matmuls`` (the reference's run_layers
+    sequence), so one instance can be captured into a HIP graph."""
+
+    def __init__(self, plan: DecodePlan, R: int, tree: bool = False):
+        m, cfg, B = plan.model, plan.model.cfg, plan.B
+        dev = m.device
+        H, HQ, HKV, D = cfg.hidden, cfg.heads, cfg.kv_heads, cfg.head_dim
+        if R < 1 or R * (HQ // HKV) > 64:
+            raise ValueError(f"R * (query heads per KV head) must be in 1..64, got R = {R}")
+        self.plan, self.R, self.tree = plan, R, tree
+        M = B * R
+        self.blk = torch.zeros((B, R), dtype=torch.int64, device=dev)
+        self.pos = torch.zeros((B,), dtype=torch.int32, device=dev)
+        # a chain until set_tree: parent of row t is row t - 1
+        self.masks = K.chain_tree(R, dev) if tree else None
+        self.depth = torch.arange(R, dtype=torch.int32, device=dev) if tree else None
+        self.q = torch.empty((B, HQ, R, D), dtype=BF16, device=dev)
+        self.attn_out = torch.empty((B, R, HQ, D), dtype=BF16, device=dev)
+        self.zero = torch.zeros((M, H), dtype=BF16, device=dev)
+        self.xa = torch.empty((M, H), dtype=BF16, device=dev)
+        self.xb = torch.empty((M, H), dtype=BF16, device=dev)
+        self.attention = K.DecodeAttention(B, HQ, HKV, D, plan.cap, dev, R=R, tree=tree, maxlen=plan.cap)
+        self.mm = decode_matmuls(m, M)
+
+    def set_tree(self, parents: list[int]) -> None:
+        """Draft tree of the R rows: parents[t] is the row of t's parent
+        (-1 for row 0 only, every parent before its child).  Sets the
+        ancestor masks (kernels.ancestor_masks) and the depths."""
+        if not self.tree:
+            raise ValueError("this plan was built without tree=True")
+        R = self.R
+        if len(parents) != R or parents[0] != -1 or any(not 0 <= parents[t] < t for t in range(1, R)):
+            raise ValueError("parents must list R rows: -1 for row 0, then a smaller row index for each")
+        depth = [0] * R
+        for t in range(1, R):
+            depth[t] = depth[parents[t]] + 1
+        self.masks.copy_(torch.tensor(K.ancestor_masks(parents), dtype=torch.int64))
+        self.depth.copy_(torch.tensor(depth, dtype=torch.int32))
+
+    @torch.inference_mode()
+    def verify(self) -> torch.Tensor:
+        """Consume ``blk`` [B, R] at ``pos``; returns the [B, R] greedy tokens
+        (run_layers, engine/model.py:182-210, then the fused lm_head argmax)."""
+        plan, m = self.plan, self.plan.model
+        cfg = m.cfg
+        B, R = plan.B, self.R
+        mm = self.mm
+        x = m.embed[self.blk.view(-1)]
+        cur, y = x, self.zero
+        for i, layer in enumerate(m.layers):
+            k_i, v_i = plan.k_cache[i], plan.v_cache[i]
+            qkv = mm["qkv"](cur, y, layer.in_norm, self.xa, layer.wqkv)
+            K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, plan.cos, plan.sin, self.pos, self.q, k_i, v_i, R,
+                                 cfg.eps, depth=self.depth)
+            if self.tree:
+                self.attention(self.q, k_i, v_i, self.pos, self.attn_out, self.masks)
+            else:
+                self.attention(self.q, k_i, v_i, self.pos, self.attn_out)
+            o = mm["o"](self.attn_out.view(B * R, cfg.heads * cfg.head_dim), layer.wo)
+            act = mm["gu"](self.xa, o, layer.post_norm, self.xb, layer.wgu)
+            y = mm["d"](act, layer.wd)
+            cur = self.xb
+        ids, _ = mm["lm_argmax"](cur, y, m.final_norm, self.xa, m.lm_head)
+        return ids.view(B, R)
+
+
 def time_decode(plan: DecodePlan, steps: int) -> dict:
     """Decode throughput the way the reference defines it (B tokens per step,
     QWEN_ENGINE_CONTRACT.md:93-102): ``steps`` graph replays after a prefill,

@@ -269,3 +269,79 @@ def test_decode_matmuls_callables(M):
     assert clear.sum() >= M // 2
     assert torch.equal(ids[clear], logits.float().argmax(-1)[clear])
     assert torch.allclose(maxv, top2[:, 0], rtol=1e-2, atol=0)
+
+
+def _path(parents: list[int], t: int) -> list[int]:
+    path = [t]
+    while parents[path[-1]] >= 0:
+        path.append(parents[path[-1]])
+    return path[::-1]
+
+
+@pytest.mark.parametrize("tree", [False, True])
+def test_verify_plan_matches_reference(tree):
+    """VerifyPlan (engine/model.py:334-375): after a prefill, one pass over
+    R = 4 rows per sequence (the last accepted token and three drafts, as a
+    chain or as the tree 0 -> {1, 2}, 1 -> 3).  Row t's token must be the
+    greedy token a causal restatement of the reference forward predicts after
+    the prompt followed by the path root..t (positions T + depth), wherever
+    that restatement's top-2 margin exceeds 0.05; a captured graph replays to
+    the same tokens; every row's K/V lands in cache slot T + t."""
+    from starter_amd.decode import VerifyPlan
+
+    model = SyntheticModel(CFG, DEV, seed=9, norm_noise=0.1)
+    B, T, R = 4, 40, 4
+    plan = DecodePlan(model, B, T, 16, handoff=False)
+    g = torch.Generator(device=DEV).manual_seed(21)
+    ids = torch.randint(0, CFG.vocab, (B, T), device=DEV, generator=g)
+    plan.ids.copy_(ids)
+    plan.prefill()
+    vp = VerifyPlan(plan, R, tree=tree)
+    parents = [-1, 0, 0, 1] if tree else [-1, 0, 1, 2]
+    if tree:
+        vp.set_tree(parents)
+    drafts = torch.randint(0, CFG.vocab, (B, R - 1), device=DEV, generator=g)
+    vp.blk.copy_(torch.cat([plan.tok[:, None], drafts], 1))
+    vp.pos.copy_(plan.pos)
+    k_before = plan.k_cache[:, :, :, T:T + R].clone()
+    out = vp.verify()
+    torch.cuda.synchronize()
+    assert not torch.equal(plan.k_cache[:, :, :, T:T + R], k_before)   # slots T .. T+R-1 written
+    decided = 0
+    for t in range(R):
+        seq = torch.cat([ids, vp.blk[:, _path(parents, t)]], 1)
+        logits = _reference_logits(model, seq, plan.cos, plan.sin, first=seq.shape[1] - 1)[:, 0].float()
+        top2 = logits.topk(2, dim=-1)
+        clear = (top2.values[:, 0] - top2.values[:, 1]) > 0.05
+        decided += int(clear.sum())
+        assert torch.equal(out[clear, t], top2.indices[clear, 0]), (t, out[:, t].tolist(), top2.indices[:, 0].tolist())
+    assert decided >= B * R // 2
+    # the same pass captured into a graph and replayed
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        vp.verify()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = vp.verify()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out)
+
+
+def test_verify_plan_rejects_bad_trees():
+    from starter_amd.decode import VerifyPlan
+
+    model = SyntheticModel(CFG, DEV, seed=9)
+    plan = DecodePlan(model, 2, 8, 8, handoff=False)
+    vp = VerifyPlan(plan, 3, tree=True)
+    for bad in ([-1, 0], [0, 0, 1], [-1, 1, 0], [-1, 0, 2]):
+        with pytest.raises(ValueError):
+            vp.set_tree(bad)
+    with pytest.raises(ValueError):
+        VerifyPlan(plan, 3, tree=False).set_tree([-1, 0, 1])
+    with pytest.raises(ValueError):
+        VerifyPlan(plan, 64 // (CFG.heads // CFG.kv_heads) + 1)
