@@ -321,7 +321,8 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 10, 8, 32, 1, 0}},  // qkv       10.22 us  3134 GB/s
-    {SK_OP_GEMM, 6144, 2560, 40, {3, 5, 8, 16, 2, 256}},  // qkv       15.51 us  2083 GB/s
+    {SK_OP_GEMM, 6144, 2560, 40, {3, 10, 8, 16, 1, 0}},  // qkv       11.34 us  2835 GB/s (half ring)
+    {SK_OP_GEMM, 6144, 2560, 48, {3, 10, 8, 16, 1, 0}},  // qkv       11.97 us  2697 GB/s (half ring)
     {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
     {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
     {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     7.02 us  2991 GB/s
@@ -329,7 +330,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 8, {3, 4, 32, 16, 1, 0}},  // o_proj     7.09 us  2971 GB/s
     {SK_OP_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj     7.47 us  2834 GB/s
     {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj     9.13 us  2343 GB/s
-    {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 16, 1, 0}},  // o_proj    11.47 us  1874 GB/s
+    {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 16, 1, 0}},  // o_proj    11.61 us  1853 GB/s
+    {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 16, 1, 0}},  // o_proj    11.54 us  1872 GB/s
     {SK_OP_GEMM, 2560, 4096, 64, {3, 6, 8, 16, 3, 0}},  // o_proj    14.44 us  1511 GB/s
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
@@ -338,7 +340,8 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 8, {3, 10, 8, 16, 1, 203}},  // gate_up   17.49 us  5707 GB/s
     {SK_OP_GATEUP, 9728, 2560, 16, {3, 10, 8, 16, 1, 203}},  // gate_up   18.13 us  5515 GB/s
     {SK_OP_GATEUP, 9728, 2560, 32, {3, 10, 8, 16, 1, 0}},  // gate_up   21.56 us  4656 GB/s (one partial buffer)
-    {SK_OP_GATEUP, 9728, 2560, 40, {3, 5, 8, 16, 2, 0}},  // gate_up   33.86 us  2976 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
+    {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 0}},  // gate_up   25.76 us  3912 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 64, {1, 4, 10, 16, 2, 0}},  // gate_up   44.93 us  2252 GB/s
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
@@ -346,7 +349,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 8, {3, 13, 8, 32, 3, 240}},  // down      12.78 us  3913 GB/s
     {SK_OP_GEMM, 2560, 9728, 16, {3, 4, 32, 32, 3, 0}},  // down      15.14 us  3316 GB/s
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
-    {SK_OP_GEMM, 2560, 9728, 40, {3, 7, 8, 32, 6, 240}},  // down      19.22 us  2642 GB/s
+    {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
+    {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
@@ -354,7 +358,8 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 8, {3, 10, 8, 32, 1, 0}},  // lm_head  113.31 us  6866 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 16, {3, 10, 8, 32, 1, 0}},  // lm_head  114.35 us  6804 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 32, {3, 5, 16, 16, 1, 0}},  // lm_head  119.79 us  6495 GB/s
-    {SK_OP_LM_ARGMAX, 151936, 2560, 40, {1, 8, 10, 16, 1, 0}},  // lm_head  167.51 us  4645 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {1, 4, 20, 16, 1, 0}},  // lm_head  216.47 us  3595 GB/s
 };
 

@@ -33,13 +33,13 @@ constexpr int gemv_regs(int MR, int RR, int KU, bool norm = false) {
 // LDS-transposed MFMA.  KW = 512: one chunk's activation units plus a whole
 // tile of weight rows in flight (16*NT rows, one row per load instruction).
 // Otherwise (ring, KW = 256 * chunks per wave): one 256-column chunk's
-// activation units plus an 8-instruction ring.
+// activation units plus the ring (ring_slots loads).
 constexpr int mfmt_regs(int MT, int NT, int KW) {
   // tile body: weight tile + fragments + accumulators; ring body: fragments +
   // ring + accumulators, plus, with several chunks, the next chunk's
   // activations and their addresses (measured: about twice the data alone)
   return KW == 512 ? 4 * 16 * MT + 4 * 16 * NT + 4 * NT * MT + 32
-                   : 4 * 8 * MT + 4 * 8 + 4 * NT * MT + 32 + (KW > 256 ? 8 * 8 * MT : 0);
+                   : 4 * 8 * MT + 4 * ring_slots(MT, KW / 256) + 4 * NT * MT + 32 + (KW > 256 ? 8 * 8 * MT : 0);
 }
 
 // Waves per workgroup an instance is compiled for (its __launch_bounds__):

@@ -233,6 +233,27 @@ def test_ring_one_partial_buffer(M, grid):
     assert_parity(out, _oracle_gemm(x, w), f"gemm one buffer M={M} grid={grid}")
 
 
+@pytest.mark.parametrize("M", [33, 40, 48])
+@pytest.mark.parametrize("grid", [0, 64])
+def test_ring_half_slab_in_flight(M, grid):
+    """48-row activation tiles keep half a weight slab in flight per wave (four
+    ring registers, each refilled with the load four ahead, across slab and
+    tile boundaries), ten waves of one 256-column chunk each, no K split;
+    several tiles per workgroup at grid 64.  gate/up+SwiGLU and a ragged GEMM."""
+    I2, Kd = GU
+    I = I2 // 2
+    cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, grid=grid)
+    wgu = _weights(I2, Kd, seed=37)
+    x = _acts(M, Kd, seed=37)
+    wd = _gpu(wgu)
+    out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:], config=cfg)
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup half ring M={M} grid={grid}")
+    N = 6144 - 40
+    w = _weights(N, Kd, seed=41)
+    out = K.gemm(x.to(DEV), _gpu(w), config=cfg)
+    assert_parity(out, _oracle_gemm(x, w), f"gemm half ring M={M} grid={grid}")
+
+
 GATEUP_CONFIGS = [
     SkConfig.make(SK_PATH_MFMA, waves=8, ku=10, rows=16),
     SkConfig.make(SK_PATH_MFMA, waves=16, ku=5, rows=16),
