@@ -25,12 +25,19 @@ The ``decode`` object of the JSON line is BASELINE configuration 5: a
 synthetic Qwen3-4B (36 layers, random bf16 weights) decoding greedily at
 batch 16 after a 1024-token prompt, one HIP graph per decode step, reported as
 decode tok/s = 16 * steps / decode time (and end-to-end tok/s including the
-prefill).  The ``attention`` object times the decode step's attention launch
-(q/k norm + rotary + KV write + GQA attention) alone at batch 16, position 1088,
-with its achieved HBM bandwidth (the K and V rows read per launch).
+prefill); inside it, ``host_delivery`` is the same generation through the
+pipelined host token loop and ``verify`` one speculative verify pass (16
+sequences x 4 draft-tree rows).  The ``attention`` object times the decode
+step's attention launch (q/k norm + rotary + KV write + GQA attention) alone at
+batch 16, position 1088, with its achieved HBM bandwidth (the K and V rows read
+per launch).  ``hipblaslt_us`` beside each per-GEMM point is the vendor
+library's GEMM (torch.mm) on the same rotating weights.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
                        [--decode-steps S] [--decode-only] [--attention-only]
+       python bench.py --probe --probe-op OP --M M      (launches for rocprofv3 --pmc)
+       python bench.py --counters-from FOLDER           (markdown table of the counter passes)
+       python bench.py --traffic-from FETCH_DIR WRITE_DIR --M M
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 
