@@ -96,6 +96,16 @@ typedef enum sk_path {
  *            the last workgroup to finish a tile sums them in fixed split
  *            order (no floating-point atomics, no second kernel)
  *   grid   : workgroups to launch (0 = derive from the device's CU count)
+ *   groups : row groups (0 or 1 = none).  g > 1 (MFMA_LDS with 256- or
+ *            1024-column waves, grid > 0 and a multiple of 8) splits the M
+ *            rows into g groups of ceil(M / g) rows, each run by its own
+ *            `grid` workgroups; the launch interleaves the groups in runs of
+ *            8 workgroups, so workgroup b of every group lands on the same
+ *            XCD (workgroups are dealt to the 8 XCDs round-robin) and reads
+ *            the same weight tiles at about the same time, and that XCD's L2
+ *            serves the later groups' reads.  Every group must hold a row.
+ *            For M where one group of all rows would need more registers per
+ *            wave than a ten-wave workgroup allows (M > 48 at K = 2560).
  */
 typedef struct sk_config {
   int32_t path;
@@ -104,6 +114,7 @@ typedef struct sk_config {
   int32_t rows;
   int32_t split;
   int32_t grid;
+  int32_t groups;
 } sk_config;
 
 /* Library version, (major << 16) | minor. */

@@ -59,7 +59,7 @@ EXPORTS = (
 
 
 class SkConfig(ctypes.Structure):
-    """Mirror of ``sk_config``: path, waves, ku, rows, split, grid."""
+    """Mirror of ``sk_config``: path, waves, ku, rows, split, grid, groups."""
 
     _fields_ = [
         ("path", ctypes.c_int32),
@@ -68,6 +68,7 @@ class SkConfig(ctypes.Structure):
         ("rows", ctypes.c_int32),
         ("split", ctypes.c_int32),
         ("grid", ctypes.c_int32),
+        ("groups", ctypes.c_int32),
     ]
 
     def as_dict(self) -> dict:
@@ -75,8 +76,8 @@ class SkConfig(ctypes.Structure):
 
     @classmethod
     def make(cls, path: int = SK_PATH_MFMA, waves: int = 4, ku: int = 20, rows: int = 16, split: int = 1,
-             grid: int = 0) -> "SkConfig":
-        return cls(path, waves, ku, rows, split, grid)
+             grid: int = 0, groups: int = 0) -> "SkConfig":
+        return cls(path, waves, ku, rows, split, grid, groups)
 
     def __repr__(self) -> str:
         return f"SkConfig({self.as_dict()})"

@@ -116,6 +116,8 @@ struct Plan {
   size_t pre_lds = 0;           // per-wave weight staging (LDS-transposed MFMA path)
   size_t parts_lds = 0;         // fp32 partial tiles (pbuf buffers)
   int pbuf = 2;                 // partial tile buffers (1 only on the ring path when 2 do not fit)
+  int groups = 1;               // row groups (sk_config::groups), each planned for `mrows` rows
+  int mrows = 0;
   size_t stage_elem = 0;        // LDS bytes per staged tile (0: argmax keeps 8*M bytes)
   size_t lds = 0;               // total dynamic LDS (set once the grid is known)
   bool norm = false;            // the op has the add + RMSNorm prologue
@@ -157,6 +159,16 @@ size_t plan_lds(const Plan& pl, int M, int tiles_per) {
   return pl.pre_lds + pl.parts_lds + (size_t)tiles_per * pl.stage_elem;
 }
 
+// The compiled instance a plan launches (host-side table code; nullptr when
+// that instance is not built).
+sk::KernelFn plan_kernel(const Plan& pl) {
+  if (pl.cfg.path == SK_PATH_MFMA) return sk::mfma_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku);
+  if (pl.cfg.path == SK_PATH_MFMA_LDS)
+    return pl.groups > 1 ? sk::mfmt_grouped_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku)
+                         : sk::mfmt_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku);
+  return sk::gemv_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku);
+}
+
 int bucket(const int* list, int n, int v) {
   for (int i = 0; i < n; ++i)
     if (list[i] >= v) return list[i];
@@ -177,8 +189,21 @@ int epi_for(int op, int split) {
 int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused, Plan* pl, int variant = 0) {
   if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   if (M < 1 || M > kMaxM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
-  if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0) return SK_ERR_CONFIG;
+  if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0 || c.groups < 0) return SK_ERR_CONFIG;
   if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
+  // Row groups: ring path, plain projections, an explicit grid that keeps
+  // sibling workgroups on one XCD, and a row in every group; the rest of the
+  // plan is that of one group.
+  const int groups = c.groups > 1 ? c.groups : 1;
+  if (groups > 1) {
+    if (fused || variant != 0 || c.path != SK_PATH_MFMA_LDS || (c.ku != 8 && c.ku != 32)) return SK_ERR_CONFIG;
+    if (c.grid <= 0 || (c.grid % 8) != 0) return SK_ERR_CONFIG;
+    const int mrows = cdiv(M, groups);
+    if ((groups - 1) * mrows >= M) return SK_ERR_CONFIG;
+    M = mrows;
+  }
+  pl->groups = groups;
+  pl->mrows = M;
   const bool gateup = (op == SK_OP_GATEUP);
   if (fused && (c.split != 1 || c.path != SK_PATH_GEMV)) return SK_ERR_CONFIG;
   if (variant != 0) {
@@ -232,10 +257,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   }
   if (pl->tku < 0) return SK_ERR_CONFIG;
   // The instance must be compiled (the lookup is host-side table code).
-  sk::KernelFn inst = c.path == SK_PATH_MFMA       ? sk::mfma_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku)
-                      : c.path == SK_PATH_MFMA_LDS ? sk::mfmt_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku)
-                                                   : sk::gemv_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
-  if (!inst) return SK_ERR_CONFIG;
+  if (!plan_kernel(*pl)) return SK_ERR_CONFIG;
   pl->slice_units = cdiv(units, c.split);
   const long per_wave = c.path == SK_PATH_MFMA_LDS ? 1 : c.ku;
   if ((long)c.waves * per_wave < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
@@ -293,11 +315,17 @@ int grid_bound(const Plan& pl) {
 // workspace zero-filled); every call returns them to zero.
 size_t ticket_bytes(int n) { return (((size_t)n * sizeof(unsigned)) + 255) & ~(size_t)255; }
 
+// With row groups: one counter (argmax) or one per tile for each group, the
+// argmax candidates of all M rows, and one partials region per group.
+size_t plan_tickets(int op, const Plan& pl) {
+  return ticket_bytes(pl.groups * (base_op(op) == SK_OP_LM_ARGMAX ? 1 : pl.nrb));
+}
 size_t plan_workspace(int op, int M, int N, const Plan& pl) {
   op = base_op(op);
-  if (op == SK_OP_LM_ARGMAX) return ticket_bytes(1) + (size_t)M * sizeof(unsigned long long);
+  if (op == SK_OP_LM_ARGMAX) return plan_tickets(op, pl) + (size_t)M * sizeof(unsigned long long);
   if (pl.cfg.split > 1)
-    return ticket_bytes(pl.nrb) + (size_t)(op == SK_OP_GATEUP ? 2 : 1) * pl.cfg.split * M * (size_t)N * sizeof(float);
+    return plan_tickets(op, pl) +
+           (size_t)pl.groups * (op == SK_OP_GATEUP ? 2 : 1) * pl.cfg.split * pl.mrows * (size_t)N * sizeof(float);
   return 0;
 }
 
@@ -306,7 +334,7 @@ size_t plan_workspace(int op, int M, int N, const Plan& pl) {
 // Each entry is the fastest configuration measured on one MI355X for that
 // shape at that row count, timed as graph replays of back-to-back launches
 // over 24 distinct weight copies (so HBM, not the 256 MB MALL, serves the
-// weights).  Fields: {path, waves, ku, rows, split, grid}.
+// weights).  Fields: {path, waves, ku, rows, split, grid, groups}.
 struct Tuned {
   int op, N, K, M;
   sk_config cfg;
@@ -322,8 +350,8 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 10, 8, 32, 1, 0}},  // qkv       10.22 us  3134 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {3, 10, 8, 16, 1, 0}},  // qkv       11.34 us  2835 GB/s (half ring)
-    {SK_OP_GEMM, 6144, 2560, 48, {3, 10, 8, 16, 1, 0}},  // qkv       11.97 us  2697 GB/s (half ring)
-    {SK_OP_GEMM, 6144, 2560, 64, {3, 5, 8, 16, 2, 0}},  // qkv       26.07 us  1250 GB/s
+    {SK_OP_GEMM, 6144, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // qkv       11.33 us  2849 GB/s (two row groups; 12.0 half ring)
+    {SK_OP_GEMM, 6144, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // qkv       12.30 us  2558 GB/s (two row groups; 18.7 without)
     {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
     {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     7.02 us  2991 GB/s
     {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     6.95 us  3024 GB/s
@@ -332,7 +360,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj     9.13 us  2343 GB/s
     {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 16, 1, 0}},  // o_proj    11.61 us  1853 GB/s
     {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 16, 1, 0}},  // o_proj    11.54 us  1872 GB/s
-    {SK_OP_GEMM, 2560, 4096, 64, {3, 6, 8, 16, 3, 0}},  // o_proj    14.44 us  1511 GB/s
+    {SK_OP_GEMM, 2560, 4096, 64, {3, 4, 32, 32, 1, 80, 3}},  // o_proj    12.37 us  1696 GB/s (three row groups; 14.8 without)
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
     {SK_OP_GATEUP, 9728, 2560, 2, {3, 10, 8, 16, 1, 203}},  // gate_up   17.35 us  5746 GB/s
@@ -342,7 +370,7 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 32, {3, 10, 8, 16, 1, 0}},  // gate_up   21.56 us  4656 GB/s (one partial buffer)
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 0}},  // gate_up   25.76 us  3912 GB/s (half ring)
-    {SK_OP_GATEUP, 9728, 2560, 64, {1, 4, 10, 16, 2, 0}},  // gate_up   44.93 us  2252 GB/s
+    {SK_OP_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   30.0 us  3373 GB/s (two row groups; 45.0 without)
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {3, 13, 8, 32, 3, 0}},  // down      12.60 us  3962 GB/s
@@ -360,22 +388,22 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 32, {3, 5, 16, 16, 1, 0}},  // lm_head  119.79 us  6495 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
-    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {1, 4, 20, 16, 1, 0}},  // lm_head  216.47 us  3595 GB/s
+    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
+    {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
 };
 
 // Tuned entry for op/N/K at the smallest tuned row count >= M (rows beyond
 // 64 run in 64-row chunks).  The lm_head logits GEMM shares the fused
-// argmax entries.
+// argmax entries, except at a row count with an entry of its own.
 const Tuned* tuned_lookup(int op, int M, int N, int K) {
-  for (int pass = 0; pass < 2; ++pass) {
-    const int want = pass == 0 ? op : (op == SK_OP_GEMM ? SK_OP_LM_ARGMAX : -1);
-    if (want < 0) break;
-    const Tuned* best = nullptr;
-    for (const Tuned& t : kTuned)
-      if (t.op == want && t.N == N && t.K == K && t.M >= M && (!best || t.M < best->M)) best = &t;
-    if (best) return best;
+  const Tuned* best = nullptr;
+  for (const Tuned& t : kTuned) {
+    const bool own = t.op == op;
+    const bool shared = op == SK_OP_GEMM && t.op == SK_OP_LM_ARGMAX;
+    if (!(own || shared) || t.N != N || t.K != K || t.M < M) continue;
+    if (!best || t.M < best->M || (t.M == best->M && own)) best = &t;
   }
-  return nullptr;
+  return best;
 }
 
 // Heuristic for shapes outside the table: VALU GEMV for M <= 4 when K is a
@@ -509,10 +537,7 @@ int resolve_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
 
 // Bind the kernel instance and compute the launch grid.
 int bind_plan(Plan* pl, int num_cu, int* grid) {
-  sk::KernelFn fn = nullptr;
-  if (pl->cfg.path == SK_PATH_MFMA) fn = sk::mfma_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
-  else if (pl->cfg.path == SK_PATH_MFMA_LDS) fn = sk::mfmt_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
-  else fn = sk::gemv_kernel_for(pl->epi, pl->tm, pl->tn, pl->tku);
+  sk::KernelFn fn = plan_kernel(*pl);
   if (!fn) return SK_ERR_CONFIG;
   FnInfo fi;
   int st = fn_info(reinterpret_cast<const void*>(fn), &fi);
@@ -698,7 +723,7 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
     // which also replays correctly from a captured graph).
     size_t tb = 0;
     for (int i = 0; i < cp.nplans; ++i) {
-      const size_t t = ticket_bytes(cp.plans[i].nrb);
+      const size_t t = plan_tickets(bop, cp.plans[i]);
       tb = t > tb ? t : tb;
     }
     sk::clear_words_kernel<<<dim3(1), dim3(256), 0, stream>>>(static_cast<unsigned*>(ws), (int)(tb / 4));
@@ -727,7 +752,7 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
     a.W1 = W1;
     a.C = C ? C + (int64_t)m0 * ldc : nullptr;
     if (ws) {
-      const size_t tb = ticket_bytes(bop == SK_OP_LM_ARGMAX ? 1 : pl.nrb);
+      const size_t tb = plan_tickets(bop, pl);
       a.tickets = static_cast<unsigned*>(ws);
       a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + tb);
       a.best = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + tb);
@@ -756,7 +781,9 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
     a.grid = grid;
     a.rbstep = grid / pl.cfg.split;
     a.pbuf = pl.pbuf;
-    pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
+    a.groups = pl.groups;
+    a.mrows = pl.mrows;
+    pl.fn<<<dim3(grid * pl.groups), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
     if ((st = launch_status())) return st;
   }
   return SK_OK;
@@ -923,7 +950,7 @@ int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const s
 
 extern "C" {
 
-int sk_version(void) { return (0 << 16) | 2; }
+int sk_version(void) { return (0 << 16) | 3; }
 
 const char* sk_strerror(int status) {
   switch (status) {

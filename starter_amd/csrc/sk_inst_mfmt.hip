@@ -16,10 +16,23 @@ mfmt_entry(Args p) {
   mfmt_body<MT, NT, KW, EPI>(p);
 }
 
+// Row-group entry points: the same body behind the group decode, compiled for
+// the register tier of the plain instance (the decode uses scalar registers).
+template <int MT, int NT, int KW, int EPI>
+__global__ void __launch_bounds__(64 * instance_waves(KIND_MFMT, MT, NT, KW, EPI))
+mfmt_grouped_entry(Args p) {
+  mfmt_grouped_body<MT, NT, KW, EPI>(p);
+}
+
 // An instance with no spill-free tier is not instantiated.
 template <int MT, int NT, int KW, int EPI>
 KernelFn mfmt_ptr() {
   if constexpr (instance_waves(KIND_MFMT, MT, NT, KW, EPI) > 0) return &mfmt_entry<MT, NT, KW, EPI>;
+  else return nullptr;
+}
+template <int MT, int NT, int KW, int EPI>
+KernelFn mfmt_grouped_ptr() {
+  if constexpr (instance_waves(KIND_MFMT, MT, NT, KW, EPI) > 0) return &mfmt_grouped_entry<MT, NT, KW, EPI>;
   else return nullptr;
 }
 
@@ -34,6 +47,25 @@ KernelFn mfmt_ptr() {
 // with one or four.
 #define SK_PRE_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256)
 #define SK_RESID_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(1, NT, 1024) SK_C(2, NT, 1024)
+
+// Row groups: plain projections (EPI 0-4) on the ring path, groups of up to
+// 32 rows.
+#define SK_G(MT, NT, KW) \
+  case MT * 100000 + NT * 1000 + KW: return mfmt_grouped_ptr<MT, NT, KW, SK_EPI>();
+#define SK_GROUP_LIST(NT) SK_G(1, NT, 256) SK_G(2, NT, 256) SK_G(1, NT, 1024) SK_G(2, NT, 1024)
+
+KernelFn SK_CAT(mfmt_grouped_for_epi, SK_EPI)(int MT, int NT, int KW) {
+  switch (MT * 100000 + NT * 1000 + KW) {
+#if SK_EPI == 1 || SK_EPI == 4
+    SK_GROUP_LIST(2)
+#elif SK_EPI <= 4
+    SK_GROUP_LIST(1)
+    SK_GROUP_LIST(2)
+#endif
+    default: break;
+  }
+  return nullptr;
+}
 
 KernelFn SK_CAT(mfmt_for_epi, SK_EPI)(int MT, int NT, int KW) {
   switch (MT * 100000 + NT * 1000 + KW) {

@@ -109,6 +109,10 @@ struct Args {
   // j + 1 writes while tile j is reduced), or 1 when two do not fit (one more
   // barrier per tile).  The other bodies always use 2.
   int pbuf;
+  // Row groups (ring path only): groups > 1 launches `groups` grids of `grid`
+  // workgroups, group g computing rows [g*mrows, min(M, (g+1)*mrows)); the
+  // workspace holds one region of counters and partials per group.
+  int groups, mrows;
 };
 
 // ---------------------------------------------------------------------------
@@ -550,6 +554,43 @@ __device__ __forceinline__ int wg_tiles(int rb0, int rbstep, int nrb) {
   return rb0 < nrb ? (nrb - 1 - rb0) / rbstep + 1 : 0;
 }
 
+// Row groups (the grouped entry points only).  Launch position x = 8*i + x8
+// runs workgroup b = 8*(i / groups) + x8 of group g = i % groups (the host
+// guarantees grid % 8 == 0, so this is a bijection onto groups x grid).  Workgroups are dealt to the 8 XCDs
+// round-robin, so workgroup b of every group runs on XCD b % 8, next to its
+// siblings, and streams the same weight tiles: the first group's loads fill
+// that XCD's L2 and the siblings' hit it.  Each group is an independent GEMM
+// on its rows: the pointers move to its rows and to its own region of
+// arrival counters and split-K partials.  Returns b.
+template <int EPI>
+__device__ __forceinline__ unsigned enter_row_group(Args& p) {
+  if (p.groups <= 1) return blockIdx.x;
+  const int i = blockIdx.x >> 3;
+  const int g = i % p.groups;
+  const int m0 = g * p.mrows;
+  p.A += (int64_t)m0 * p.lda;
+  p.M = min(p.mrows, p.M - m0);
+  constexpr int BASE = EpiTraits<EPI>::base;
+  if constexpr (BASE == EPI_ARGMAX) {
+    p.best += m0;
+    p.C = reinterpret_cast<uint16_t*>(reinterpret_cast<int64_t*>(p.C) + m0);   // ids
+    p.part += m0;                                                             // max logits
+    p.tickets += g;
+  } else {
+    if (p.C) p.C += (int64_t)m0 * p.ldc;
+    if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU) {
+      p.part += (int64_t)g * (BASE == EPI_PART_GU ? 2 : 1) * p.S * p.mrows * p.N;
+      p.tickets += g * p.nrb;
+    }
+  }
+  if constexpr (EpiTraits<EPI>::resid) {
+    p.R += (int64_t)m0 * p.ldr;
+    p.RO += (int64_t)m0 * p.ldr;
+  }
+  if constexpr (EpiTraits<EPI>::resid || EpiTraits<EPI>::pre) p.SQ += (int64_t)m0 * p.sq_ld;
+  return 8u * (i / p.groups) + (blockIdx.x & 7u);
+}
+
 // ---------------------------------------------------------------------------
 // MFMA path.
 //   MT : activation row tiles of 16 (M <= 16*MT)
@@ -917,7 +958,7 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
 constexpr int ring_slots(int MT, int CPW) { return MT == 3 && CPW == 1 ? 4 : 8; }
 
 template <int MT, int NT, int CPW, int EPI>
-__device__ __forceinline__ void mfmt_ring_body(Args p) {
+__device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int BASE = EpiTraits<EPI>::base;
   static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
@@ -944,9 +985,9 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
   const int M = p.M;
 
   const int S = p.S;
-  const int slice = blockIdx.x % S;
+  const int slice = bid % (unsigned)S;
   const int rbstep = p.rbstep;
-  const int rb0 = blockIdx.x / S;
+  const int rb0 = bid / (unsigned)S;
   const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
   const int units = (p.K + KW - 1) / KW;
   const int c_lo = slice * p.slice_units;
@@ -1178,7 +1219,16 @@ __device__ __forceinline__ void mfmt_ring_body(Args p) {
 template <int MT, int NT, int KW, int EPI>
 __device__ __forceinline__ void mfmt_body(Args p) {
   if constexpr (KW == 512) mfmt_tile_body<MT, NT, KW, EPI>(p);
-  else mfmt_ring_body<MT, NT, KW / 256, EPI>(p);
+  else mfmt_ring_body<MT, NT, KW / 256, EPI>(p, blockIdx.x);
+}
+
+// The ring path with row groups (Args::groups > 1).  A separate entry point,
+// so the plain launches carry none of the group arithmetic.
+template <int MT, int NT, int KW, int EPI>
+__device__ __forceinline__ void mfmt_grouped_body(Args p) {
+  static_assert(KW != 512, "row groups run on the ring path");
+  const unsigned bid = enter_row_group<EPI>(p);
+  mfmt_ring_body<MT, NT, KW / 256, EPI>(p, bid);
 }
 
 // ---------------------------------------------------------------------------

@@ -82,7 +82,7 @@ def test_tuned_table_drives_the_decode_shapes():
     assert _lib.default_config(SK_OP_GEMM, 1, 6144, 2560).path == SK_PATH_GEMV
     assert _lib.default_config(SK_OP_GEMM, 8, 6144, 2560).path == SK_PATH_MFMA_LDS
     assert _lib.default_config(SK_OP_GATEUP, 8, 9728, 2560).as_dict() == \
-        {"path": SK_PATH_MFMA_LDS, "waves": 10, "ku": 8, "rows": 16, "split": 1, "grid": 203}
+        {"path": SK_PATH_MFMA_LDS, "waves": 10, "ku": 8, "rows": 16, "split": 1, "grid": 203, "groups": 0}
     assert _lib.default_config(SK_OP_LM_ARGMAX, 8, 151936, 2560).path == SK_PATH_MFMA_LDS
     # the lm_head logits GEMM shares the argmax entries; M = 5 takes the M = 8 entry
     assert _lib.default_config(SK_OP_GEMM, 5, 151936, 2560).as_dict() == \
@@ -173,6 +173,38 @@ def test_workspace_bytes():
     assert _lib.workspace_bytes(SK_OP_GATEUP, 8, 9728, 2560, cfg) == _tickets(9728 // 16) + 2 * 2 * 8 * 9728 * 4
     lm = SkConfig.make(SK_PATH_MFMA, 4, 20, 16, 1, 500)
     assert _lib.workspace_bytes(SK_OP_LM_ARGMAX, 8, 151936, 2560, lm) == _tickets(1) + 8 * 8
+
+
+def test_row_groups_planning():
+    """Row groups run on the ring path only, with an explicit grid that is a
+    multiple of 8 (sibling workgroups on one XCD), and every group holds a
+    row; the workspace holds each group's counters and partials."""
+    ring = lambda **kw: SkConfig.make(_LDS, **{"waves": 10, "ku": 8, "rows": 16, "grid": 128, **kw})
+    ok = lambda cfg, op=SK_OP_GEMM, M=64, N=6144, K=2560: _lib.check_config(op, M, N, K, cfg)
+    assert ok(ring(groups=2)) == SK_OK
+    assert ok(ring(groups=2), SK_OP_GATEUP, N=9728) == SK_OK
+    assert ok(ring(groups=2, grid=640), SK_OP_LM_ARGMAX, N=151936) == SK_OK
+    assert ok(ring(groups=0)) == SK_ERR_CONFIG          # one group of 64 rows: over the ten-wave registers
+    assert ok(ring(groups=2, grid=0)) == SK_ERR_CONFIG  # derived grid
+    assert ok(ring(groups=2, grid=100)) == SK_ERR_CONFIG
+    assert ok(ring(groups=-1)) == SK_ERR_CONFIG
+    assert ok(ring(groups=2, ku=16, waves=5)) == SK_ERR_CONFIG   # whole-tile body
+    assert ok(SkConfig.make(SK_PATH_MFMA, 4, 20, 16, 1, 128, 2)) == SK_ERR_CONFIG
+    assert ok(ring(groups=3), M=2) == SK_ERR_CONFIG     # groups of one row: the third is empty
+    assert ok(ring(groups=2), M=1) == SK_ERR_CONFIG
+    assert ok(ring(groups=4), M=61) == SK_OK            # 16 + 16 + 16 + 13 rows
+    assert ok(ring(groups=2), SK_OP_RESID_GEMM, M=8, N=2560, K=4096) == SK_ERR_CONFIG
+    assert ok(ring(groups=2), SK_OP_PRE_GEMM, M=8) == SK_ERR_CONFIG
+    split = ring(groups=2, waves=5, split=2)
+    assert _lib.workspace_bytes(SK_OP_GEMM, 64, 6144, 2560, split) == _tickets(2 * 384) + 2 * 2 * 32 * 6144 * 4
+    assert _lib.workspace_bytes(SK_OP_GATEUP, 61, 9728, 2560, ring(groups=4, waves=5, split=2)) == \
+        _tickets(4 * 608) + 4 * 2 * 2 * 16 * 9728 * 4
+    assert _lib.workspace_bytes(SK_OP_LM_ARGMAX, 64, 151936, 2560, ring(groups=2, grid=640)) == _tickets(2) + 64 * 8
+    assert _lib.workspace_bytes(SK_OP_GEMM, 64, 6144, 2560, ring(groups=2)) == 0
+    # the tuned verify-width entries use them
+    for name in ("qkv", "gu", "lm_argmax"):
+        op, N, K = QWEN[name]
+        assert _lib.default_config(op, 64, N, K).groups == 2, name
 
 
 def test_valid_call_without_gpu_fails_loudly():

@@ -254,6 +254,58 @@ def test_ring_half_slab_in_flight(M, grid):
     assert_parity(out, _oracle_gemm(x, w), f"gemm half ring M={M} grid={grid}")
 
 
+@pytest.mark.parametrize("M,groups", [(33, 2), (50, 3), (61, 4), (64, 2)])
+@pytest.mark.parametrize("split", [1, 2])
+def test_ring_row_groups(M, groups, split):
+    """Row groups: the rows split into `groups` independent GEMMs launched side
+    by side (groups of ceil(M / groups) rows, the last one shorter), each with
+    its own counters and split-K partials.  gate/up+SwiGLU and a ragged GEMM at
+    one and two K splits, several tiles per workgroup (grid 64 or 32 per
+    group), and bit-identity with the ungrouped launch, whose per-element
+    summation order is the same (one chunk per wave, waves summed in order)."""
+    I2, Kd = GU
+    I = I2 // 2
+    waves = 10 if split == 1 else 5
+    cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=waves, ku=8, rows=16, split=split, grid=64 * split // 2 * 2,
+                        groups=groups)
+    wgu = _weights(I2, Kd, seed=43)
+    x = _acts(M, Kd, seed=43)
+    wd = _gpu(wgu)
+    xd = x.to(DEV)
+    out = K.gateup_swiglu(xd, wd[:I], wd[I:], config=cfg)
+    what = f"M={M} groups={groups} split={split}"
+    assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup row groups {what}")
+    N = 6144 - 56
+    w = _weights(N, Kd, seed=47)
+    cfg_g = SkConfig.make(SK_PATH_MFMA_LDS, waves=waves, ku=8, rows=32, split=split, grid=32 * split, groups=groups)
+    out = K.gemm(xd, _gpu(w), config=cfg_g)
+    assert_parity(out, _oracle_gemm(x, w), f"gemm row groups {what}")
+    # the same rows one group at a time through the plain launch, where its
+    # registers allow: identical bits
+    for g0 in range(0, M, -(-M // groups)):
+        rows = xd[g0:g0 + -(-M // groups)]
+        plain = SkConfig.make(SK_PATH_MFMA_LDS, waves=waves, ku=8, rows=32, split=split, grid=32 * split)
+        assert torch.equal(K.gemm(rows, _gpu(w), config=plain), out[g0:g0 + rows.shape[0]]), f"{what} rows {g0}+"
+
+
+@pytest.mark.parametrize("M,groups,grid", [(64, 2, 640), (49, 3, 96), (40, 2, 8)])
+def test_lm_argmax_row_groups(M, groups, grid):
+    """The fused argmax with row groups: one arrival counter per group, every
+    row's candidate in one table; a ragged vocabulary at one grid."""
+    V, Kd = LM
+    if grid == 8:
+        V = 40_000 - 13
+    w = _weights(V, Kd, seed=53)
+    x = _acts(M, Kd, seed=53)
+    cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, grid=grid, groups=groups)
+    ids, maxv = K.lm_argmax(x.to(DEV), _gpu(w), config=cfg)
+    logits = oracle.gemm(bits(x), bits(w))
+    o_ids, o_maxv = oracle.argmax(logits)
+    check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax row groups M={M} groups={groups}")
+    ids2, maxv2 = K.lm_argmax(x.to(DEV), _gpu(w), config=cfg)   # the counters were returned to zero
+    assert torch.equal(ids, ids2) and torch.equal(maxv, maxv2)
+
+
 GATEUP_CONFIGS = [
     SkConfig.make(SK_PATH_MFMA, waves=8, ku=10, rows=16),
     SkConfig.make(SK_PATH_MFMA, waves=16, ku=5, rows=16),
