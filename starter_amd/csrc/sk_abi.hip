@@ -265,6 +265,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   const int out_rows = (c.path == SK_PATH_MFMA) ? (gateup ? 16 : c.rows) : c.rows;
   pl->out_rows = out_rows;
   pl->nrb = cdiv(N, out_rows);
+  if (c.path == SK_PATH_MFMA_LDS && pl->tku != 512) partial_rows = sk::ring_part_stride(pl->tm, partial_rows);
   pl->parts_lds = (size_t)2 * c.waves * M * partial_rows * sizeof(float);
   pl->stage_elem = stage_bytes(pl->epi) * (size_t)M * out_rows;
   if (c.grid > 0 && (c.grid % c.split) != 0) return SK_ERR_CONFIG;

@@ -324,7 +324,8 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Sum the partials of tile j (output columns rb*OUT_ROWS + r) into staging.
-template <int ROWS, int EPI>
+// The partials of (wave w, row m) start at P[(w*M + m) * PST].
+template <int ROWS, int EPI, int PST = ROWS>
 __device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int nw, int rb, int j, void* stage,
                                             unsigned long long* lds_best) {
   constexpr bool GU = EpiTraits<EPI>::gateup;
@@ -345,8 +346,8 @@ __device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int n
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ws = min(w0 + i, nw - 1);
-        pg[i] = P[(ws * M + m) * ROWS + r];
-        if constexpr (GU) pu[i] = P[(ws * M + m) * ROWS + r + OUT_ROWS];
+        pg[i] = P[(ws * M + m) * PST + r];
+        if constexpr (GU) pu[i] = P[(ws * M + m) * PST + r + OUT_ROWS];
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -957,6 +958,15 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
 // lm_head 157 -> 129 us).
 constexpr int ring_slots(int MT, int CPW) { return MT == 3 && CPW == 1 ? 4 : 8; }
 
+// Floats per (wave, row) of the ring path's partial tiles in LDS.  A wave
+// stores its accumulators as f32x4 per lane, lane (r, g) at row r, column 4g:
+// with a row stride of 16 or 32 floats (64 or 128 B) the 16 rows of one store
+// fall on the same banks; 4 floats more shift each row by 4 banks (gate_up
+// M = 64: 30.2 -> 28.3 us, lm_head M = 64 -2%, neutral at M <= 8).  Kept to one
+// and two activation tiles: the extra address arithmetic tipped the 48- and
+// 64-row instances over their register tiers.
+constexpr int ring_part_stride(int MT, int ROWS) { return MT <= 2 ? ROWS + 4 : ROWS; }
+
 template <int MT, int NT, int CPW, int EPI>
 __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
@@ -998,7 +1008,8 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
 
   char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
   float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
-  const int part_floats = nw * M * ROWS;
+  constexpr int PST = ring_part_stride(MT, ROWS);
+  const int part_floats = nw * M * PST;
   void* stage = parts + p.pbuf * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
   if constexpr (BASE == EPI_ARGMAX) {
@@ -1194,12 +1205,12 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = 16 * mt + r16;
-        if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
+        if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * PST + 16 * nt + 4 * g4]) = acc[nt][mt];
       }
     // The barrier keeps the waves of a workgroup on the same tile rows
     // (measured faster than deferring every reduction to the end).
     lds_barrier();
-    tile_reduce<ROWS, BASE>(p, P, nw, rb, j, stage, lds_best);
+    tile_reduce<ROWS, BASE, PST>(p, P, nw, rb, j, stage, lds_best);
   };
 
   int j = 0;

@@ -56,12 +56,16 @@ def _noalloc(a: torch.Tensor, w: torch.Tensor, cfg: SkConfig | None) -> torch.Te
 
 SPLIT3 = SkConfig.make(SK_PATH_MFMA_LDS, waves=13, ku=8, rows=32, split=3)   # the tuned down plan at M = 2..8
 SPLIT4 = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, split=4)
+# two row groups, each with its own counters and partials in the scratch
+GROUPS_A = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, split=4, grid=128, groups=2)
+GROUPS_B = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, split=4, grid=64, groups=2)
 
 
 @pytest.mark.parametrize("first,second", [
     ((8, None), (3, None)),           # down projection, default (split-K) plans, then a smaller batch
     ((64, None), (16, None)),         # the M = 64 default (split 5) then M = 16 (split 3, 32-row tiles)
     ((8, SPLIT4), (5, SPLIT3)),       # explicit split counts: the second call uses fewer tiles
+    ((64, GROUPS_A), (40, GROUPS_B)),  # row groups with split K, then fewer rows and workgroups
 ])
 def test_noalloc_equals_workspace_entry_point_on_two_calls(first, second):
     N, K = 2560, 9728                 # down: every default plan above splits K, so the scratch is used
