@@ -278,17 +278,19 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   char* const ktile = s_k[wave];
   const int64_t kv_row0 = (int64_t)bk * a.cap;
   const int step = 16 * ATTN_WAVES;
+  // K and V rows are read once per launch: non-temporal loads keep them from
+  // displacing other lines in L2 (17.6 vs 19.1 us at B = 16, position 1088).
   auto load_block = [&](int n0, u32x4* kf, u32x4* vv) {
     const int base = n0 + 16 * wave;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kk = max(min(base + 4 * j + kr, end - 1), 0);
-      kf[j] = ld16(a.k + (kv_row0 + kk) * HEAD_D + 8 * dg);
+      kf[j] = ld16_stream(a.k + (kv_row0 + kk) * HEAD_D + 8 * dg);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kv = max(min(base + 4 * kr + j, end - 1), 0);
-      vv[j] = ld16(a.v + (kv_row0 + kv) * HEAD_D + 8 * dg);
+      vv[j] = ld16_stream(a.v + (kv_row0 + kv) * HEAD_D + 8 * dg);
     }
   };
   // Two blocks in flight beyond the one being processed.  Three buffers with

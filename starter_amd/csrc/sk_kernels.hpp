@@ -168,13 +168,13 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
-// Weight loads are streamed once per call: mark them non-temporal so they do
-// not evict the activations and partials from L2/MALL.
 // 128 zero bytes in device memory (never written): the source of loads for
 // columns outside K, so that such loads need neither a branch nor a mask on
 // the loaded data.
 static __device__ __attribute__((aligned(128))) uint32_t kZeroLine[32] = {};
 
+// Data read once per call (weights, K/V cache rows): non-temporal loads, so it
+// does not evict the activations and partials from L2/MALL.
 __device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
@@ -335,8 +335,6 @@ __device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int n
   const int nout = M * OUT_ROWS;
   for (int idx = tid; idx < nout; idx += nthr) {
     const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
-    // All waves' partials are read first (independent LDS loads in flight
-    // together), then summed in wave order 0..nw-1.
     // Four waves' partials per step are read together (independent LDS loads
     // in flight), then added in wave order 0..nw-1; slots past nw-1 read wave
     // nw-1's slot (in bounds) and are masked to +0.
