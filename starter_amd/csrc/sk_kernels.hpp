@@ -741,6 +741,17 @@ __device__ __forceinline__ void mfma_body(Args p) {
   }
 }
 
+// Floats per (wave, row) of the LDS-fed MFMA path's partial tiles in LDS.  A wave
+// stores its accumulators as f32x4 per lane, lane (r, g) at row r, column 4g:
+// with a row stride of 16 or 32 floats (64 or 128 B) the 16 rows of one store
+// fall on the same banks; 4 floats more shift each row by 4 banks (gate_up
+// M = 8: 19.05 -> 18.18 us, M = 64: 30.2 -> 28.3 us; lm_head M = 64 -2%).
+// Ring path (KW != 512) with one or two activation tiles only: the extra
+// address arithmetic tipped a 48-row instance and the whole-tile body's
+// two-row-tile instances over their register tiers, and three activation tiles
+// or the whole-tile body (lm_head M = 32) gained nothing.
+constexpr int lds_part_stride(int MT, int NT, int KW) { return MT <= 2 && KW != 512 ? 16 * NT + 4 : 16 * NT; }
+
 // ---------------------------------------------------------------------------
 // MFMA path with LDS-transposed weight rows ("rows through LDS").
 //   MT : activation row tiles of 16 (M <= 16*MT)
@@ -795,7 +806,8 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
   // turn][partials][staged outputs].
   char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
   float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
-  const int part_floats = nw * M * ROWS;
+  constexpr int PST = lds_part_stride(MT, NT, KW);
+  const int part_floats = nw * M * PST;
   void* stage = parts + 2 * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
   if constexpr (BASE == EPI_ARGMAX) {
@@ -913,10 +925,10 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = 16 * mt + r16;
-        if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * ROWS + 16 * nt + 4 * g4]) = acc[nt][mt];
+        if (m < M) *reinterpret_cast<f32x4*>(&P[(wave * M + m) * PST + 16 * nt + 4 * g4]) = acc[nt][mt];
       }
     lds_barrier();
-    tile_reduce<ROWS, BASE>(p, P, nw, rb, j, stage, lds_best);
+    tile_reduce<ROWS, BASE, PST>(p, P, nw, rb, j, stage, lds_best);
   };
 
   int j = 0;
@@ -956,14 +968,6 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
 // lm_head 157 -> 129 us).
 constexpr int ring_slots(int MT, int CPW) { return MT == 3 && CPW == 1 ? 4 : 8; }
 
-// Floats per (wave, row) of the ring path's partial tiles in LDS.  A wave
-// stores its accumulators as f32x4 per lane, lane (r, g) at row r, column 4g:
-// with a row stride of 16 or 32 floats (64 or 128 B) the 16 rows of one store
-// fall on the same banks; 4 floats more shift each row by 4 banks (gate_up
-// M = 64: 30.2 -> 28.3 us, lm_head M = 64 -2%, neutral at M <= 8).  Kept to one
-// and two activation tiles: the extra address arithmetic tipped the 48- and
-// 64-row instances over their register tiers.
-constexpr int ring_part_stride(int MT, int ROWS) { return MT <= 2 ? ROWS + 4 : ROWS; }
 
 template <int MT, int NT, int CPW, int EPI>
 __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
@@ -1006,7 +1010,7 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
 
   char* tr = reinterpret_cast<char*>(lds) + wave * (16 * PITCH);
   float* parts = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + nw * (16 * PITCH));
-  constexpr int PST = ring_part_stride(MT, ROWS);
+  constexpr int PST = lds_part_stride(MT, NT, 256 * CPW);
   const int part_floats = nw * M * PST;
   void* stage = parts + p.pbuf * part_floats;
   unsigned long long* lds_best = static_cast<unsigned long long*>(stage);
