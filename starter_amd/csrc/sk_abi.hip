@@ -191,12 +191,12 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   if (M < 1 || M > kMaxM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
   if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0 || c.groups < 0) return SK_ERR_CONFIG;
   if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
-  // Row groups: ring path, plain projections, an explicit grid that keeps
+  // Row groups: ring path (no norm prologue), an explicit grid that keeps
   // sibling workgroups on one XCD, and a row in every group; the rest of the
   // plan is that of one group.
   const int groups = c.groups > 1 ? c.groups : 1;
   if (groups > 1) {
-    if (fused || variant != 0 || c.path != SK_PATH_MFMA_LDS || (c.ku != 8 && c.ku != 32)) return SK_ERR_CONFIG;
+    if (fused || c.path != SK_PATH_MFMA_LDS || (c.ku != 8 && c.ku != 32)) return SK_ERR_CONFIG;
     if (c.grid <= 0 || (c.grid % 8) != 0) return SK_ERR_CONFIG;
     const int mrows = cdiv(M, groups);
     if ((groups - 1) * mrows >= M) return SK_ERR_CONFIG;
@@ -349,6 +349,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 6144, 2560, 16, {3, 10, 8, 32, 1, 192}},  // qkv        8.43 us  3764 GB/s
     {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
+    {SK_OP_PRE_GEMM, 6144, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer: 16-row groups (32-row consumers have 8 waves, too few for K)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 10, 8, 32, 1, 0}},  // qkv       10.22 us  3134 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {3, 10, 8, 16, 1, 0}},  // qkv       11.34 us  2835 GB/s (half ring)
     {SK_OP_GEMM, 6144, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // qkv       11.33 us  2849 GB/s (two row groups; 12.0 half ring)
@@ -372,6 +373,7 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 0}},  // gate_up   25.76 us  3912 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   30.0 us  3373 GB/s (two row groups; 45.0 without)
+    {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {3, 13, 8, 32, 3, 0}},  // down      12.60 us  3962 GB/s
@@ -381,6 +383,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
+    {SK_OP_RESID_GEMM, 2560, 9728, 64, {3, 10, 8, 16, 4, 128, 2}},  // down producer: its plain plan has no residual instance (64-row tiles)
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 4, {3, 10, 8, 32, 1, 0}},  // lm_head  113.49 us  6855 GB/s
@@ -390,18 +393,19 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
+    {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
 };
 
 // Tuned entry for op/N/K at the smallest tuned row count >= M (rows beyond
-// 64 run in 64-row chunks).  The lm_head logits GEMM shares the fused
-// argmax entries, except at a row count with an entry of its own.
-const Tuned* tuned_lookup(int op, int M, int N, int K) {
+// 64 run in 64-row chunks) among op's own entries and those of `also` (-1:
+// none), op's own entry first at equal row counts.  The lm_head logits GEMM
+// shares the fused argmax entries; a hand-off op shares its projection's.
+const Tuned* tuned_lookup(int op, int M, int N, int K, int also = -1) {
   const Tuned* best = nullptr;
   for (const Tuned& t : kTuned) {
     const bool own = t.op == op;
-    const bool shared = op == SK_OP_GEMM && t.op == SK_OP_LM_ARGMAX;
-    if (!(own || shared) || t.N != N || t.K != K || t.M < M) continue;
+    if (!(own || t.op == also) || t.N != N || t.K != K || t.M < M) continue;
     if (!best || t.M < best->M || (t.M == best->M && own)) best = &t;
   }
   return best;
@@ -512,7 +516,7 @@ int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   }
   op = base_op(op);
   if (!is_gemm_family(op)) return SK_ERR_CONFIG;
-  if (const Tuned* t = tuned_lookup(op, Mk, N, K)) {
+  if (const Tuned* t = tuned_lookup(op, Mk, N, K, op == SK_OP_GEMM ? SK_OP_LM_ARGMAX : -1)) {
     if (plan_shape(op, Mk, N, K, t->cfg, &pl) == SK_OK) {
       *out = t->cfg;
       return SK_OK;
@@ -810,8 +814,9 @@ int handoff_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
     *out = *cfg;
     return SK_OK;
   }
-  // The hand-off op's own table entry, then its projection's.
-  if (const Tuned* t = tuned_lookup(op, M, N, K)) {
+  // The table entry of the hand-off op or of its projection at the nearest
+  // row count (the hand-off op's own first), then the projection's default.
+  if (const Tuned* t = tuned_lookup(op, M, N, K, bop)) {
     if (plan_shape_impl(bop, M, N, K, t->cfg, false, &pl, variant) == SK_OK) {
       *out = t->cfg;
       return SK_OK;
@@ -823,7 +828,10 @@ int handoff_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
     return SK_OK;
   }
   // Ring candidates in order: one K split with 256-column chunks, then (the
-  // producer only) four chunks per wave, then global K splits.
+  // producer only) four chunks per wave, then global K splits.  The hand-off
+  // instances hold at most 32 rows (consumers: 16, and 4 per wave), so more
+  // rows run as row groups, each with a grid of one workgroup per tile and
+  // split, rounded up to a multiple of 8 split-sized runs.
   for (int ku : {8, 32}) {
     if (ku == 32 && variant == 1) continue;
     for (int split = 1; split <= (variant == 2 ? 4 : 1); ++split) {
@@ -834,6 +842,11 @@ int handoff_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
       d.split = split;
       const int units = (K + 32 * ku - 1) / (32 * ku);
       d.waves = (units + split - 1) / split;
+      const int group_rows = variant == 1 ? (4 * d.waves < 16 ? 4 * d.waves : 16) : 32;
+      if (M > group_rows) {
+        d.groups = cdiv(M, group_rows);
+        d.grid = cdiv(cdiv(N, 16) * split, 8 * split) * 8 * split;
+      }
       if (d.waves <= 16 && plan_shape_impl(bop, M, N, K, d, false, &pl, variant) == SK_OK) {
         *out = d;
         return SK_OK;
@@ -913,7 +926,7 @@ int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const s
   a.W1 = W1;
   a.C = C;
   if (ws) {
-    const size_t tb = ticket_bytes(bop == SK_OP_LM_ARGMAX ? 1 : pl.nrb);
+    const size_t tb = plan_tickets(bop, pl);
     a.tickets = static_cast<unsigned*>(ws);
     a.part = reinterpret_cast<float*>(static_cast<char*>(ws) + tb);
     a.best = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + tb);
@@ -943,7 +956,9 @@ int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const s
   a.grid = grid;
   a.rbstep = grid / pl.cfg.split;
   a.pbuf = pl.pbuf;
-  pl.fn<<<dim3(grid), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
+  a.groups = pl.groups;
+  a.mrows = pl.mrows;
+  pl.fn<<<dim3(grid * pl.groups), dim3(64 * pl.cfg.waves), pl.lds, stream>>>(a);
   return launch_status();
 }
 

@@ -48,17 +48,24 @@ KernelFn mfmt_grouped_ptr() {
 #define SK_PRE_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256)
 #define SK_RESID_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(1, NT, 1024) SK_C(2, NT, 1024)
 
-// Row groups: plain projections (EPI 0-4) on the ring path, groups of up to
-// 32 rows.
+// Row groups: groups of up to 32 rows on the ring path, for the plain
+// projections and the residual hand-off producers (256- and 1024-column
+// waves) and consumers (256-column waves).
 #define SK_G(MT, NT, KW) \
   case MT * 100000 + NT * 1000 + KW: return mfmt_grouped_ptr<MT, NT, KW, SK_EPI>();
 #define SK_GROUP_LIST(NT) SK_G(1, NT, 256) SK_G(2, NT, 256) SK_G(1, NT, 1024) SK_G(2, NT, 1024)
+#define SK_GROUP_PRE_LIST(NT) SK_G(1, NT, 256) SK_G(2, NT, 256)
 
 KernelFn SK_CAT(mfmt_grouped_for_epi, SK_EPI)(int MT, int NT, int KW) {
   switch (MT * 100000 + NT * 1000 + KW) {
-#if SK_EPI == 1 || SK_EPI == 4
+#if SK_EPI == 9
+    SK_GROUP_PRE_LIST(2)
+#elif SK_EPI == 8 || SK_EPI == 10
+    SK_GROUP_PRE_LIST(1)
+    SK_GROUP_PRE_LIST(2)
+#elif SK_EPI == 1 || SK_EPI == 4
     SK_GROUP_LIST(2)
-#elif SK_EPI <= 4
+#else
     SK_GROUP_LIST(1)
     SK_GROUP_LIST(2)
 #endif

@@ -99,6 +99,11 @@ KernelFn mfmt_grouped_for_epi1(int MT, int NT, int KW);
 KernelFn mfmt_grouped_for_epi2(int MT, int NT, int KW);
 KernelFn mfmt_grouped_for_epi3(int MT, int NT, int KW);
 KernelFn mfmt_grouped_for_epi4(int MT, int NT, int KW);
+KernelFn mfmt_grouped_for_epi8(int MT, int NT, int KW);
+KernelFn mfmt_grouped_for_epi9(int MT, int NT, int KW);
+KernelFn mfmt_grouped_for_epi10(int MT, int NT, int KW);
+KernelFn mfmt_grouped_for_epi11(int MT, int NT, int KW);
+KernelFn mfmt_grouped_for_epi12(int MT, int NT, int KW);
 KernelFn gemv_for_epi0(int MR, int R, int KU);
 KernelFn gemv_for_epi1(int MR, int R, int KU);
 KernelFn gemv_for_epi2(int MR, int R, int KU);
@@ -143,6 +148,11 @@ inline KernelFn mfmt_grouped_kernel_for(int epi, int MT, int NT, int KW) {
     case EPI_ARGMAX: return mfmt_grouped_for_epi2(MT, NT, KW);
     case EPI_PART: return mfmt_grouped_for_epi3(MT, NT, KW);
     case EPI_PART_GU: return mfmt_grouped_for_epi4(MT, NT, KW);
+    case EPI_STORE_PRE: return mfmt_grouped_for_epi8(MT, NT, KW);
+    case EPI_SWIGLU_PRE: return mfmt_grouped_for_epi9(MT, NT, KW);
+    case EPI_ARGMAX_PRE: return mfmt_grouped_for_epi10(MT, NT, KW);
+    case EPI_STORE_RESID: return mfmt_grouped_for_epi11(MT, NT, KW);
+    case EPI_PART_RESID: return mfmt_grouped_for_epi12(MT, NT, KW);
   }
   return nullptr;
 }

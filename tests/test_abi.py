@@ -193,18 +193,33 @@ def test_row_groups_planning():
     assert ok(ring(groups=3), M=2) == SK_ERR_CONFIG     # groups of one row: the third is empty
     assert ok(ring(groups=2), M=1) == SK_ERR_CONFIG
     assert ok(ring(groups=4), M=61) == SK_OK            # 16 + 16 + 16 + 13 rows
-    assert ok(ring(groups=2), SK_OP_RESID_GEMM, M=8, N=2560, K=4096) == SK_ERR_CONFIG
-    assert ok(ring(groups=2), SK_OP_PRE_GEMM, M=8) == SK_ERR_CONFIG
+    # the residual hand-off producers and consumers take groups too; the fused
+    # norm prologue (GEMV path) does not
+    assert ok(ring(groups=2, split=4), SK_OP_RESID_GEMM, N=2560, K=9728) == SK_OK
+    # consumers of 32 rows are compiled for 8 waves (the norm's registers), too
+    # few for K = 2560 in 256-column chunks: 16-row groups
+    assert ok(ring(groups=2), SK_OP_PRE_GEMM) == SK_ERR_CONFIG
+    assert ok(ring(groups=4, grid=64), SK_OP_PRE_GEMM) == SK_OK
+    assert ok(ring(groups=4, grid=64), SK_OP_PRE_GATEUP, N=9728) == SK_OK
+    assert ok(ring(groups=4, grid=64), SK_OP_PRE_LM_ARGMAX, N=151936) == SK_OK
+    assert ok(SkConfig.make(SK_PATH_GEMV, 1, 5, 2, 1, 8, 2), SK_OP_RMSNORM_GEMM, M=4) == SK_ERR_CONFIG
     split = ring(groups=2, waves=5, split=2)
     assert _lib.workspace_bytes(SK_OP_GEMM, 64, 6144, 2560, split) == _tickets(2 * 384) + 2 * 2 * 32 * 6144 * 4
     assert _lib.workspace_bytes(SK_OP_GATEUP, 61, 9728, 2560, ring(groups=4, waves=5, split=2)) == \
         _tickets(4 * 608) + 4 * 2 * 2 * 16 * 9728 * 4
     assert _lib.workspace_bytes(SK_OP_LM_ARGMAX, 64, 151936, 2560, ring(groups=2, grid=640)) == _tickets(2) + 64 * 8
     assert _lib.workspace_bytes(SK_OP_GEMM, 64, 6144, 2560, ring(groups=2)) == 0
-    # the tuned verify-width entries use them
+    # the tuned verify-width entries use them, for the hand-off ops as well
     for name in ("qkv", "gu", "lm_argmax"):
         op, N, K = QWEN[name]
         assert _lib.default_config(op, 64, N, K).groups == 2, name
+    for op, N, K in ((SK_OP_PRE_GEMM, 6144, 2560), (SK_OP_PRE_GATEUP, 9728, 2560), (SK_OP_PRE_LM_ARGMAX, 151936, 2560),
+                     (SK_OP_RESID_GEMM, 2560, 4096), (SK_OP_RESID_GEMM, 2560, 9728)):
+        cfg = _lib.default_config(op, 64, N, K)
+        assert cfg.groups >= 2 and _lib.check_config(op, 64, N, K, cfg) == SK_OK, (op, N, K)
+    # below M = 64 a hand-off op keeps its projection's nearer entry
+    assert _lib.default_config(SK_OP_RESID_GEMM, 32, 2560, 9728).as_dict() == \
+        _lib.default_config(SK_OP_GEMM, 32, 2560, 9728).as_dict()
 
 
 def test_valid_call_without_gpu_fails_loudly():
@@ -341,23 +356,23 @@ HANDOFF = {  # decode-step call sites at Qwen3-4B shapes
 }
 
 
-OWN_ENTRY = {"qkv_pre"}   # hand-off ops with table entries of their own (M <= 16)
+OWN_ENTRY = {"qkv_pre": (8, 16)}   # hand-off ops with table entries of their own at these M (<= 16)
 
 
 @pytest.mark.parametrize("name", list(HANDOFF))
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_handoff_default_config_is_a_ring_config(name, M):
     """Hand-off ops run on the ring-streamed LDS-fed MFMA path: their own
-    tuned entry where the table has one (the qkv consumer: 16-row tiles), else
-    the tuned projection configuration where it is a ring configuration (M >= 2
-    at these shapes), else a ring configuration; the workspace is the
-    projection's own."""
+    tuned entry where the table has one at the nearest row count (the qkv
+    consumer at M = 8 and 16: 16-row tiles), else the tuned projection
+    configuration where it is a ring configuration (M >= 2 at these shapes),
+    else a ring configuration; the workspace is the projection's own."""
     op, N, K, base = HANDOFF[name]
     cfg = _lib.default_config(op, M, N, K)
     assert cfg.path == _LDS and cfg.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,))
     assert _lib.check_config(op, M, N, K, cfg) == SK_OK
     b = _lib.default_config(base, M, N, K)
-    if name in OWN_ENTRY:
+    if M in OWN_ENTRY.get(name, ()):
         assert cfg.rows == 16
     elif b.path == _LDS and b.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,)):
         assert cfg.as_dict() == b.as_dict()
