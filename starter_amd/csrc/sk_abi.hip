@@ -360,8 +360,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 8, {3, 4, 32, 16, 1, 0}},  // o_proj     7.09 us  2971 GB/s
     {SK_OP_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj     7.47 us  2834 GB/s
     {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj     9.13 us  2343 GB/s
-    {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 16, 1, 0}},  // o_proj    11.61 us  1853 GB/s
-    {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 16, 1, 0}},  // o_proj    11.54 us  1872 GB/s
+    {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.96 us  2106 GB/s (three row groups; 11.6 without)
+    {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.92 us  2114 GB/s (three row groups; 11.5 without)
     {SK_OP_GEMM, 2560, 4096, 64, {3, 4, 32, 32, 1, 80, 3}},  // o_proj    12.37 us  1696 GB/s (three row groups; 14.8 without)
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
@@ -371,7 +371,7 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 16, {3, 10, 8, 16, 1, 203}},  // gate_up   18.13 us  5515 GB/s
     {SK_OP_GATEUP, 9728, 2560, 32, {3, 10, 8, 16, 1, 0}},  // gate_up   21.56 us  4656 GB/s (one partial buffer)
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
-    {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 0}},  // gate_up   25.76 us  3912 GB/s (half ring)
+    {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   24.7 us  4080 GB/s (two row groups; 25.8 half ring)
     {SK_OP_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   30.0 us  3373 GB/s (two row groups; 45.0 without)
     {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
