@@ -351,6 +351,23 @@ int sk_decode_attention_rope_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_b
                                   int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
                                   int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
 
+/*
+ * sk_decode_attention_rope_tree_bf16: the same fused launch for a draft tree,
+ * for qk_norm_rope_cache(..., depth=depth) followed by self.attention(q,
+ * k_cache, v_cache, pos, out, tree) in the reference's verify forward
+ * (engine/model.py:357, 369-370; rope.py:94-122 DEPTH path,
+ * attention.py:245-259 masks).  tree [R]: the ancestor bit masks of
+ * sk_decode_attention_bf16; depth [R]: row t is written to slot pos[b] + t
+ * and rotated by position pos[b] + depth[t].  Both are read at every call
+ * (a captured graph follows new trees).  Arguments otherwise as above.
+ */
+int sk_decode_attention_rope_tree_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w,
+                                       const sk_bf16* k_norm_w, const sk_bf16* cos, const sk_bf16* sin,
+                                       int rope_rows, float eps, sk_bf16* k_cache, sk_bf16* v_cache,
+                                       const int32_t* pos, const int64_t* tree, const int32_t* depth, sk_bf16* out,
+                                       int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                                       int nsplit, void* ws, size_t ws_bytes, hipStream_t stream);
+
 /* Exact argmax plus approximate top-k over bf16 logits L[N, V] (row stride
  * ld) in one pass.  Replaces fast_topk (engine/kernels/topk.py:17-46) with
  * the same algorithm and results: 2048 lanes sweep each row with stride 2048,

@@ -53,7 +53,7 @@ EXPORTS = (
     "sk_gemm_residual_bf16", "sk_rmsnorm_pre_gemm_bf16", "sk_rmsnorm_pre_gateup_swiglu_bf16",
     "sk_rmsnorm_pre_lm_argmax_bf16",
     "sk_qk_norm_rope_cache_bf16", "sk_decode_attention_workspace_bytes", "sk_decode_attention_bf16",
-    "sk_decode_attention_rope_bf16",
+    "sk_decode_attention_rope_bf16", "sk_decode_attention_rope_tree_bf16",
     "sk_topk_bf16",
 )
 
@@ -135,6 +135,9 @@ _SIGNATURES = {
     "sk_decode_attention_rope_bf16": (_i32, [_p, _i64, _p, _p, _p, _p, _i32, ctypes.c_float, _p, _p, _p, _p,
                                              _i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _i32,
                                              _p, _sz, _p]),
+    "sk_decode_attention_rope_tree_bf16": (_i32, [_p, _i64, _p, _p, _p, _p, _i32, ctypes.c_float, _p, _p, _p, _p,
+                                                  _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.c_float,
+                                                  _i32, _p, _sz, _p]),
 }
 
 

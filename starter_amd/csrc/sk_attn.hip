@@ -138,6 +138,7 @@ struct AttnArgs {
   uint16_t* v_out;
   int rope_rows;
   float eps;
+  const int32_t* depth;     // ROPE with TREE: [R] rotary offsets (row t rotates by pos + depth[t])
 };
 
 
@@ -158,7 +159,6 @@ __device__ __forceinline__ float rows4_sum(float x) {
 
 template <int QR, int ATTN_WAVES, bool TREE, bool ROPE = false>
 __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a) {
-  static_assert(!(ROPE && TREE), "the fused rotary prologue uses chain positions pos + t");
   __shared__ float s_m[ATTN_WAVES][QR], s_l[ATTN_WAVES][QR];
   __shared__ __attribute__((aligned(16))) float s_acc[ATTN_WAVES][QR][HEAD_D];
   __shared__ int s_last;
@@ -185,17 +185,19 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   bf16x8 qb[HEAD_D / 32];
   if constexpr (ROPE) {
     // Query rows through the norm + rotary step (one wave per row), into LDS.
-    // A row whose slot is outside the rotary table stays zero.
+    // Row t rotates by position pos + t (chain) or pos + depth[t] (draft
+    // tree); a row whose rotary position is outside the table stays zero.
     __shared__ __attribute__((aligned(16))) uint16_t s_q[QR][HEAD_D];
     const int T = a.R;
+    auto rot_of = [&](int t) { return TREE ? pos + a.depth[t] : pos + t; };
     for (int r = wave; r < QR; r += ATTN_WAVES) {   // wave-uniform
       const int gr = rbk * QR + r;
       const int t = gr / a.G, g = gr - (gr / a.G) * a.G;
-      const int slot = pos + t;
+      const int rot = gr < rows ? rot_of(t) : -1;
       uint16_t o1 = 0, o2 = 0;
-      if (gr < rows && slot >= 0 && slot < a.rope_rows)
+      if (rot >= 0 && rot < a.rope_rows)
         rope_head(a.qkv + (int64_t)(b * T + t) * a.ld_qkv + (int64_t)(kh * a.G + g) * HEAD_D, a.qw,
-                  a.cos + (int64_t)slot * HEAD_D, a.sin + (int64_t)slot * HEAD_D, a.eps, lane, o1, o2);
+                  a.cos + (int64_t)rot * HEAD_D, a.sin + (int64_t)rot * HEAD_D, a.eps, lane, o1, o2);
       s_q[r][lane] = o1;
       s_q[r][lane + 64] = o2;
     }
@@ -209,13 +211,13 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     // than waves the K/V rows run beside the query rows, not after them.
     constexpr int KV_WAVE0 = QR % ATTN_WAVES;
     for (int t = (wave - KV_WAVE0 + ATTN_WAVES) % ATTN_WAVES; t < T; t += ATTN_WAVES) {   // wave-uniform
-      const int slot = pos + t;
+      const int slot = pos + t, rot = rot_of(t);
       const bool mine = slot >= start && (slot < start + a.split_len || s == S - 1);
-      if (mine && slot < a.cap && slot < a.rope_rows) {
+      if (mine && slot < a.cap && rot >= 0 && rot < a.rope_rows) {
         const uint16_t* row = a.qkv + (int64_t)(b * T + t) * a.ld_qkv;
         uint16_t o1, o2;
-        rope_head(row + (int64_t)(a.HQ + kh) * HEAD_D, a.kw, a.cos + (int64_t)slot * HEAD_D,
-                  a.sin + (int64_t)slot * HEAD_D, a.eps, lane, o1, o2);
+        rope_head(row + (int64_t)(a.HQ + kh) * HEAD_D, a.kw, a.cos + (int64_t)rot * HEAD_D,
+                  a.sin + (int64_t)rot * HEAD_D, a.eps, lane, o1, o2);
         const int64_t cs = ((int64_t)bk * a.cap + slot) * HEAD_D;
         a.k_out[cs + lane] = o1;
         a.k_out[cs + lane + 64] = o2;
@@ -637,7 +639,11 @@ int attn_run(const AttnPlan& p, sk::AttnArgs& a, int B, int HQ, int HKV, int R, 
   a.scale = scale;
   const dim3 grid((unsigned)(B * HKV * p.NRB * p.S));
   const dim3 block(64 * kAttnWaves);
-  if (rope) {
+  if (rope && a.tree) {
+    if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, true, true><<<grid, block, 0, stream>>>(a);
+    else if (p.QR == 8) sk::decode_attn_kernel<8, kAttnWaves, true, true><<<grid, block, 0, stream>>>(a);
+    else sk::decode_attn_kernel<16, kAttnWaves, true, true><<<grid, block, 0, stream>>>(a);
+  } else if (rope) {
     if (p.QR == 4) sk::decode_attn_kernel<4, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
     else if (p.QR == 8) sk::decode_attn_kernel<8, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
     else sk::decode_attn_kernel<16, kAttnWaves, false, true><<<grid, block, 0, stream>>>(a);
@@ -658,39 +664,13 @@ bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
   return x < y + nb && y < x + na;
 }
 
-}  // namespace
-
-extern "C" {
-
-int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_bf16* v_cache, const int32_t* pos,
-                             const int64_t* tree, sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap,
-                             int max_len, float scale, int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
-  if (B < 0) return SK_ERR_SHAPE;
-  if (B == 0) return SK_OK;
-  AttnPlan p;
-  int st = attn_plan(B, HQ, HKV, D, R, cap, max_len, nsplit, &p);
-  if (st) return st;
-  if (!q || !k_cache || !v_cache || !pos || !out) return SK_ERR_NULL;
-  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return SK_ERR_ALIGN;
-  if (p.need > 0 && (!ws || ws_bytes < p.need)) return SK_ERR_WORKSPACE;
-  st = attn_device_ok();
-  if (st) return st;
-  sk::AttnArgs a;
-  memset(&a, 0, sizeof(a));
-  a.q = q;
-  a.k = k_cache;
-  a.v = v_cache;
-  a.pos = pos;
-  a.tree = tree;
-  a.out = out;
-  return attn_run(p, a, B, HQ, HKV, R, cap, scale, ws, false, stream);
-}
-
-int sk_decode_attention_rope_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w,
-                                  const sk_bf16* k_norm_w, const sk_bf16* cos, const sk_bf16* sin, int rope_rows,
-                                  float eps, sk_bf16* k_cache, sk_bf16* v_cache, const int32_t* pos, sk_bf16* out,
-                                  int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
-                                  int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
+// The fused rotary step + attention of both entry points: tree and depth
+// (the draft-tree masks and rotary offsets, both [R]) or both nullptr (chain).
+int rope_attention(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w, const sk_bf16* k_norm_w,
+                   const sk_bf16* cos, const sk_bf16* sin, int rope_rows, float eps, sk_bf16* k_cache,
+                   sk_bf16* v_cache, const int32_t* pos, const int64_t* tree, const int32_t* depth, sk_bf16* out,
+                   int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale, int nsplit, void* ws,
+                   size_t ws_bytes, hipStream_t stream) {
   if (B < 0) return SK_ERR_SHAPE;
   if (B == 0) return SK_OK;
   AttnPlan p;
@@ -725,7 +705,58 @@ int sk_decode_attention_rope_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_b
   a.v_out = v_cache;
   a.rope_rows = rope_rows;
   a.eps = eps;
+  a.tree = tree;
+  a.depth = depth;
   return attn_run(p, a, B, HQ, HKV, R, cap, scale, ws, true, stream);
+}
+
+
+}  // namespace
+
+extern "C" {
+
+int sk_decode_attention_bf16(const sk_bf16* q, const sk_bf16* k_cache, const sk_bf16* v_cache, const int32_t* pos,
+                             const int64_t* tree, sk_bf16* out, int B, int HQ, int HKV, int D, int R, int cap,
+                             int max_len, float scale, int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (B < 0) return SK_ERR_SHAPE;
+  if (B == 0) return SK_OK;
+  AttnPlan p;
+  int st = attn_plan(B, HQ, HKV, D, R, cap, max_len, nsplit, &p);
+  if (st) return st;
+  if (!q || !k_cache || !v_cache || !pos || !out) return SK_ERR_NULL;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache)) return SK_ERR_ALIGN;
+  if (p.need > 0 && (!ws || ws_bytes < p.need)) return SK_ERR_WORKSPACE;
+  st = attn_device_ok();
+  if (st) return st;
+  sk::AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.pos = pos;
+  a.tree = tree;
+  a.out = out;
+  return attn_run(p, a, B, HQ, HKV, R, cap, scale, ws, false, stream);
+}
+
+int sk_decode_attention_rope_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w,
+                                  const sk_bf16* k_norm_w, const sk_bf16* cos, const sk_bf16* sin, int rope_rows,
+                                  float eps, sk_bf16* k_cache, sk_bf16* v_cache, const int32_t* pos, sk_bf16* out,
+                                  int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                                  int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
+  return rope_attention(qkv, ld_qkv, q_norm_w, k_norm_w, cos, sin, rope_rows, eps, k_cache, v_cache, pos, nullptr,
+                        nullptr, out, B, HQ, HKV, D, R, cap, max_len, scale, nsplit, ws, ws_bytes, stream);
+}
+
+int sk_decode_attention_rope_tree_bf16(const sk_bf16* qkv, int64_t ld_qkv, const sk_bf16* q_norm_w,
+                                       const sk_bf16* k_norm_w, const sk_bf16* cos, const sk_bf16* sin,
+                                       int rope_rows, float eps, sk_bf16* k_cache, sk_bf16* v_cache,
+                                       const int32_t* pos, const int64_t* tree, const int32_t* depth, sk_bf16* out,
+                                       int B, int HQ, int HKV, int D, int R, int cap, int max_len, float scale,
+                                       int nsplit, void* ws, size_t ws_bytes, hipStream_t stream) {
+  if (B > 0 && (!tree || !depth)) return SK_ERR_NULL;
+  return rope_attention(qkv, ld_qkv, q_norm_w, k_norm_w, cos, sin, rope_rows, eps, k_cache, v_cache, pos, tree,
+                        depth, out, B, HQ, HKV, D, R, cap, max_len, scale, nsplit, ws, ws_bytes, stream);
 }
 
 }  // extern "C"

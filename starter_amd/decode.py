@@ -365,7 +365,8 @@ class VerifyPlan:
     position pos[b] + depth[t] in a tree) and returns the greedy token after
     every row; accepting a path is the caller's policy.  The projections run
     at M = B * R rows through ``decode_matmuls`` (the reference's run_layers
-    sequence), so one instance can be captured into a HIP graph."""
+    sequence; the q/k norm, rotary step and cache write run inside the
+    attention launch), so one instance can be captured into a HIP graph."""
 
     def __init__(self, plan: DecodePlan, R: int, tree: bool = False):
         m, cfg, B = plan.model, plan.model.cfg, plan.B
@@ -380,7 +381,6 @@ class VerifyPlan:
         # a chain until set_tree: parent of row t is row t - 1
         self.masks = K.chain_tree(R, dev) if tree else None
         self.depth = torch.arange(R, dtype=torch.int32, device=dev) if tree else None
-        self.q = torch.empty((B, HQ, R, D), dtype=BF16, device=dev)
         self.attn_out = torch.empty((B, R, HQ, D), dtype=BF16, device=dev)
         self.zero = torch.zeros((M, H), dtype=BF16, device=dev)
         self.xa = torch.empty((M, H), dtype=BF16, device=dev)
@@ -416,12 +416,10 @@ class VerifyPlan:
         for i, layer in enumerate(m.layers):
             k_i, v_i = plan.k_cache[i], plan.v_cache[i]
             qkv = mm["qkv"](cur, y, layer.in_norm, self.xa, layer.wqkv)
-            K.qk_norm_rope_cache(qkv, layer.q_norm, layer.k_norm, plan.cos, plan.sin, self.pos, self.q, k_i, v_i, R,
-                                 cfg.eps, depth=self.depth)
-            if self.tree:
-                self.attention(self.q, k_i, v_i, self.pos, self.attn_out, self.masks)
-            else:
-                self.attention(self.q, k_i, v_i, self.pos, self.attn_out)
+            # qk_norm_rope_cache (rotated by pos + depth in a tree) and the
+            # attention in one launch
+            self.attention.rope_attend(qkv, layer.q_norm, layer.k_norm, plan.cos, plan.sin, self.pos, k_i, v_i,
+                                       self.attn_out, cfg.eps, tree=self.masks, depth=self.depth)
             o = mm["o"](self.attn_out.view(B * R, cfg.heads * cfg.head_dim), layer.wo)
             act = mm["gu"](self.xa, o, layer.post_norm, self.xb, layer.wgu)
             y = mm["d"](act, layer.wd)

@@ -548,13 +548,22 @@ class DecodeAttention:
 
     def rope_attend(self, qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, cos: torch.Tensor,
                     sin: torch.Tensor, pos: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                    out: torch.Tensor, eps: float) -> None:
+                    out: torch.Tensor, eps: float, tree: torch.Tensor | None = None,
+                    depth: torch.Tensor | None = None) -> None:
         """``qk_norm_rope_cache(qkv, q_norm_w, k_norm_w, cos, sin, pos, q, k_cache, v_cache, R, eps)``
         followed by ``self(q, k_cache, v_cache, pos, out)`` in one launch
         (sk_decode_attention_rope_bf16): same outputs and cache contents, no q
-        buffer.  Chain mask only (an instance built with tree=True refuses)."""
+        buffer.  An instance built with ``tree=True`` takes the draft tree's
+        ancestor masks ``tree`` (int64 [R]) and rotary offsets ``depth`` (int32
+        [R], as ``qk_norm_rope_cache(..., depth=depth)``) and runs
+        sk_decode_attention_rope_tree_bf16; a chain instance takes neither."""
         B, HQ, HKV, D, R, cap = self.B, self.HQ, self.HKV, self.D, self.R, self.cap
-        _need(not self.tree, "the fused rotary path uses chain positions (no tree masks)")
+        if self.tree:
+            _need(tree is not None and depth is not None, "a tree instance needs the masks and the depths")
+            _vec(tree, "tree", torch.int64, R)
+            _vec(depth, "depth", torch.int32, R)
+        else:
+            _need(tree is None and depth is None, "masks and depths need an instance built with tree=True")
         _mat(qkv, "qkv")
         _need(qkv.shape[0] == B * R and qkv.shape[1] >= (HQ + 2 * HKV) * D, "qkv must be [B*R, (HQ+2*HKV)*D]")
         _need(k_cache.shape == (B, HKV, cap, D) and v_cache.shape == k_cache.shape, "cache shapes")
@@ -565,6 +574,13 @@ class DecodeAttention:
         _vec(pos, "pos", torch.int32, B, exact=False)
         _device_guard(qkv)
         wp, wn = _ws_args(self.ws)
+        if self.tree:
+            check(lib().sk_decode_attention_rope_tree_bf16(
+                qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos.data_ptr(),
+                sin.data_ptr(), cos.shape[0], float(eps), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(),
+                tree.data_ptr(), depth.data_ptr(), out.data_ptr(), B, HQ, HKV, D, R, cap, self.maxlen,
+                float(self.scale), self.nsplit, wp, wn, _stream(qkv)), "sk_decode_attention_rope_tree_bf16")
+            return
         check(lib().sk_decode_attention_rope_bf16(qkv.data_ptr(), qkv.stride(0), q_norm_w.data_ptr(),
                                                   k_norm_w.data_ptr(), cos.data_ptr(), sin.data_ptr(), cos.shape[0],
                                                   float(eps), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(),
