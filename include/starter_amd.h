@@ -106,6 +106,14 @@ typedef enum sk_path {
  *            serves the later groups' reads.  Every group must hold a row.
  *            For M where one group of all rows would need more registers per
  *            wave than a ten-wave workgroup allows (M > 48 at K = 2560).
+ *
+ * Rows per launch: at most 64 without row groups; with a configuration that
+ * splits them into groups (compiled for groups of up to 32 rows), up to 128
+ * rows in one launch, so each weight tile leaves HBM once for all of them.
+ * A call with more rows runs as several launches of that many rows (64, or
+ * 128 when the configuration for 128 rows has groups) plus the remainder,
+ * each streaming the weights again; the fused argmax ops (LM_ARGMAX and its
+ * norm/consumer variants) take at most one launch's rows per call.
  */
 typedef struct sk_config {
   int32_t path;
@@ -260,7 +268,7 @@ int sk_rmsnorm_lm_argmax_bf16(const sk_bf16* x, const sk_bf16* y, const sk_bf16*
  * Both run on the ring-streamed LDS-fed MFMA path (a configuration with
  * path 3 and ku 8, or ku 8 / 32 with any split for the producer); cfg NULL or
  * path AUTO picks the tuned configuration when it is such a path, else the
- * first ring configuration that fits.  M <= 64; a consumer holds all of K in
+ * first ring configuration that fits.  M <= 128; a consumer holds all of K in
  * one workgroup (12 waves of 256 columns, K <= 3072, at M <= 16; 8 waves,
  * K <= 2048, above), so shapes with no such configuration return
  * SK_ERR_CONFIG (Qwen3-4B's consumers, K = 2560: M <= 16). */

@@ -26,7 +26,8 @@ constexpr int kMaxGrid = 8192;           // bound on workgroups of a persistent 
 constexpr size_t kMaxLds = 160 * 1024;   // gfx950 LDS per CU (dynamic LDS budget per workgroup)
 constexpr size_t kPrefLds = 64 * 1024;   // keep >= 2 workgroups per CU when the table has a choice
 constexpr int kArgmaxChunk = 4096;       // columns per workgroup of sk_argmax_bf16
-constexpr int kMaxM = 64;                // rows per kernel launch; more are chunked
+constexpr int kMaxM = 64;                // rows of a launch without row groups, and of one row group
+constexpr int kMaxLaunchM = 128;         // rows of a launch with row groups; more are chunked
 
 int cdiv(int a, int b) { return (a + b - 1) / b; }
 
@@ -188,7 +189,7 @@ int epi_for(int op, int split) {
 // (EPI_*_RESID); both run on the ring-streamed LDS-fed MFMA path only.
 int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused, Plan* pl, int variant = 0) {
   if (!is_gemm_family(op)) return SK_ERR_CONFIG;
-  if (M < 1 || M > kMaxM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
+  if (M < 1 || M > kMaxLaunchM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
   if (c.waves < 1 || c.waves > 16 || c.ku < 1 || c.split < 1 || c.grid < 0 || c.groups < 0) return SK_ERR_CONFIG;
   if (op == SK_OP_LM_ARGMAX && c.split != 1) return SK_ERR_CONFIG;
   // Row groups: ring path (no norm prologue), an explicit grid that keeps
@@ -202,6 +203,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     if ((groups - 1) * mrows >= M) return SK_ERR_CONFIG;
     M = mrows;
   }
+  if (M > kMaxM) return SK_ERR_SHAPE;   // more rows than an instance holds: chunked, or row groups
   pl->groups = groups;
   pl->mrows = M;
   const bool gateup = (op == SK_OP_GATEUP);
@@ -350,10 +352,12 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
     {SK_OP_PRE_GEMM, 6144, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer: 16-row groups (32-row consumers have 8 waves, too few for K)
+    {SK_OP_PRE_GEMM, 6144, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 24.0 us (eight 16-row groups; 30.2 at grid 64)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 10, 8, 32, 1, 0}},  // qkv       10.22 us  3134 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {3, 10, 8, 16, 1, 0}},  // qkv       11.34 us  2835 GB/s (half ring)
     {SK_OP_GEMM, 6144, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // qkv       11.33 us  2849 GB/s (two row groups; 12.0 half ring)
     {SK_OP_GEMM, 6144, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // qkv       12.30 us  2558 GB/s (two row groups; 18.7 without)
+    {SK_OP_GEMM, 6144, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // qkv       16.6 us  (four row groups, one launch; 24.9 as two 64-row launches)
     {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
     {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     7.02 us  2991 GB/s
     {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     6.95 us  3024 GB/s
@@ -363,6 +367,8 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.96 us  2106 GB/s (three row groups; 11.6 without)
     {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.92 us  2114 GB/s (three row groups; 11.5 without)
     {SK_OP_GEMM, 2560, 4096, 64, {3, 4, 32, 32, 1, 80, 3}},  // o_proj    12.37 us  1696 GB/s (three row groups; 14.8 without)
+    {SK_OP_GEMM, 2560, 4096, 96, {3, 4, 32, 32, 1, 80, 3}},  // o_proj    12.7 us  (three 32-row groups; 14.8 with six)
+    {SK_OP_GEMM, 2560, 4096, 128, {3, 4, 32, 32, 1, 80, 8}},  // o_proj    20.1 us  (eight row groups; 24.9 as two 64-row launches)
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
     {SK_OP_GATEUP, 9728, 2560, 2, {3, 10, 8, 16, 1, 203}},  // gate_up   17.35 us  5746 GB/s
@@ -373,7 +379,9 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   24.7 us  4080 GB/s (two row groups; 25.8 half ring)
     {SK_OP_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   30.0 us  3373 GB/s (two row groups; 45.0 without)
+    {SK_OP_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // gate_up   40.7 us  (four row groups; 55.9 as two 64-row launches)
     {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
+    {SK_OP_PRE_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 58.7 us (67.3 at grid 64)
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {3, 13, 8, 32, 3, 0}},  // down      12.60 us  3962 GB/s
@@ -383,6 +391,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
+    {SK_OP_GEMM, 2560, 9728, 128, {3, 10, 8, 16, 4, 64, 4}},  // down      38.0 us  (four row groups; 47.3 as two 64-row launches)
     {SK_OP_RESID_GEMM, 2560, 9728, 64, {3, 10, 8, 16, 4, 128, 2}},  // down producer: its plain plan has no residual instance (64-row tiles)
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
@@ -393,13 +402,16 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // lm_head (four row groups, one launch)
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
+    {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer, as for qkv
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
+    {SK_OP_GEMM, 151936, 2560, 128, {3, 10, 8, 16, 1, 256, 4}},  // lm_head logits, four row groups
 };
 
-// Tuned entry for op/N/K at the smallest tuned row count >= M (rows beyond
-// 64 run in 64-row chunks) among op's own entries and those of `also` (-1:
-// none), op's own entry first at equal row counts.  The lm_head logits GEMM
+// Tuned entry for op/N/K at the smallest tuned row count >= M among op's own
+// entries and those of `also` (-1: none), op's own entry first at equal row
+// counts.  The lm_head logits GEMM
 // shares the fused argmax entries; a hand-off op shares its projection's.
 const Tuned* tuned_lookup(int op, int M, int N, int K, int also = -1) {
   const Tuned* best = nullptr;
@@ -501,8 +513,21 @@ int mfma_search_config(int op, int M, int N, int K, int num_cu, sk_config* out) 
 
 int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   if (M < 1 || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
-  const int Mk = M > kMaxM ? kMaxM : M;
   Plan pl;
+  // Above kMaxM rows: a table entry that splits up to kMaxLaunchM rows into
+  // row groups covers them in one launch; otherwise the call runs in kMaxM-row
+  // chunks, each planned as below.
+  if (M > kMaxM) {
+    const int Ml = M < kMaxLaunchM ? M : kMaxLaunchM;
+    const int bo = base_op(op);
+    if (const Tuned* t = tuned_lookup(bo, Ml, N, K, bo == SK_OP_GEMM ? SK_OP_LM_ARGMAX : -1)) {
+      if (t->cfg.groups > 1 && t->M > kMaxM && plan_shape(op, Ml, N, K, t->cfg, &pl) == SK_OK) {
+        *out = t->cfg;
+        return SK_OK;
+      }
+    }
+  }
+  const int Mk = M > kMaxM ? kMaxM : M;
   // A norm op takes its own entry where the table has one (the fused GEMV
   // prologue can beat a faster projection plus a separate norm launch), else
   // its projection's configuration.
@@ -627,13 +652,14 @@ struct NormIn {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-// Plans of one call: rows beyond 64 are processed in 64-row chunks (each
-// streaming the weights once more), so a call has at most two distinct
-// chunk sizes.  Also the workspace it needs: the plans' counters and partials,
+// Plans of one call: rows beyond one launch's (launch_rows) are processed in
+// chunks of that many rows (each streaming the weights once more), so a call
+// has at most two distinct chunk sizes.  Also the workspace it needs: the plans' counters and partials,
 // then, when the norm prologue runs as its own launch, the normalised
 // activations [M, K] at offset `norm_off`.
 struct CallPlan {
   Plan plans[2];
+  int chunk = 0;                // rows per launch
   int chunk_rows[2] = {0, 0};
   int nplans = 0;
   size_t base_need = 0;
@@ -642,10 +668,24 @@ struct CallPlan {
   bool fused = false;
 };
 
+// Rows one launch of a call covers: up to kMaxLaunchM when the configuration
+// for that many rows splits them into row groups, else kMaxM.
+int launch_rows(int op, int M, int N, int K, const sk_config* cfg) {
+  if (M <= kMaxM) return kMaxM;
+  const int R = M < kMaxLaunchM ? M : kMaxLaunchM;
+  sk_config c;
+  Plan pl;
+  if (resolve_config(op, R, N, K, cfg, &c) == SK_OK && c.groups > 1 && plan_shape(op, R, N, K, c, &pl) == SK_OK)
+    return kMaxLaunchM;
+  return kMaxM;
+}
+
 int plan_call(int op, int M, int N, int K, const sk_config* cfg, CallPlan* cp) {
-  cp->chunk_rows[0] = M < kMaxM ? M : kMaxM;
-  cp->chunk_rows[1] = M % kMaxM;
-  cp->nplans = (M > kMaxM && (M % kMaxM) != 0) ? 2 : 1;
+  const int chunk = launch_rows(op, M, N, K, cfg);
+  cp->chunk = chunk;
+  cp->chunk_rows[0] = M < chunk ? M : chunk;
+  cp->chunk_rows[1] = M % chunk;
+  cp->nplans = (M > chunk && (M % chunk) != 0) ? 2 : 1;
   for (int i = 0; i < cp->nplans; ++i) {
     sk_config c;
     int st = resolve_config(op, cp->chunk_rows[i], N, K, cfg, &c);
@@ -691,7 +731,7 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
   if (nrm && K > sk::RMS_THREADS * 8 * sk::RMS_MAX_CHUNKS) return SK_ERR_SHAPE;
   if (!aligned16(A) || !aligned16(W0) || (W1 && !aligned16(W1)) || (lda & 7) || (ldw & 7)) return SK_ERR_ALIGN;
   if (nrm && (!aligned16(nrm->y) || !aligned16(nrm->w) || !aligned16(nrm->xout))) return SK_ERR_ALIGN;
-  if (bop == SK_OP_LM_ARGMAX && M > kMaxM) return SK_ERR_SHAPE;   // ids of one call come from one pass
+  if (bop == SK_OP_LM_ARGMAX && M > launch_rows(op, M, N, K, cfg)) return SK_ERR_SHAPE;   // one pass
   // Outputs are written while other workgroups may still read the inputs.
   const size_t a_bytes = ((size_t)(M - 1) * lda + K) * sizeof(sk_bf16);
   const size_t c_bytes = bop == SK_OP_LM_ARGMAX ? 0 : ((size_t)(M - 1) * ldc + N) * sizeof(sk_bf16);
@@ -745,8 +785,8 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
     Ause = nb;
     ldause = K;
   }
-  for (int m0 = 0; m0 < M; m0 += kMaxM) {
-    const int rows = (M - m0) < kMaxM ? (M - m0) : kMaxM;
+  for (int m0 = 0; m0 < M; m0 += cp.chunk) {
+    const int rows = (M - m0) < cp.chunk ? (M - m0) : cp.chunk;
     const int pi = rows == cp.chunk_rows[0] ? 0 : 1;
     const Plan& pl = cp.plans[pi];
     const int grid = grids[pi];
@@ -857,7 +897,7 @@ int handoff_config(int op, int M, int N, int K, const sk_config* cfg, sk_config*
 }
 
 int plan_handoff(int op, int M, int N, int K, const sk_config* cfg, Plan* pl) {
-  if (M < 1 || M > kMaxM || N < 1 || K < 32) return SK_ERR_SHAPE;
+  if (M < 1 || M > kMaxLaunchM || N < 1 || K < 32) return SK_ERR_SHAPE;
   sk_config c;
   int st = handoff_config(op, M, N, K, cfg, &c);
   if (st) return st;
@@ -884,7 +924,7 @@ int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const s
                 const sk_config* cfg, void* ws, size_t ws_bytes, hipStream_t stream) {
   const int bop = handoff_base(op);
   const bool resid = handoff_variant(op) == 2;
-  if (M < 0 || N < 1 || K < 32 || M > kMaxM) return SK_ERR_SHAPE;
+  if (M < 0 || N < 1 || K < 32 || M > kMaxLaunchM) return SK_ERR_SHAPE;
   if (M == 0) return SK_OK;
   if (!A || !W0 || (bop == SK_OP_GATEUP && !W1) || !h.sq) return SK_ERR_NULL;
   if (resid ? (!h.r || !h.r_out) : !h.w) return SK_ERR_NULL;
@@ -986,7 +1026,7 @@ const char* sk_strerror(int status) {
 
 int sk_default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
   if (!out) return SK_ERR_NULL;
-  if (is_handoff_op(op)) return handoff_config(op, M > kMaxM ? kMaxM : M, N, K, nullptr, out);
+  if (is_handoff_op(op)) return handoff_config(op, M > kMaxLaunchM ? kMaxLaunchM : M, N, K, nullptr, out);
   if (!is_gemm_family(base_op(op))) return SK_ERR_CONFIG;
   return default_config(op, M, N, K, num_cu, out);
 }
@@ -997,11 +1037,14 @@ int sk_check_config(int op, int M, int N, int K, const sk_config* cfg) {
     Plan pl;
     return plan_handoff(op, M, N, K, cfg, &pl);
   }
+  if (M < 1) return SK_ERR_SHAPE;
+  const int rows = launch_rows(op, M, N, K, cfg);
+  const int Mk = M > rows ? rows : M;
   sk_config c;
-  int st = resolve_config(op, M > kMaxM ? kMaxM : M, N, K, cfg, &c);
+  int st = resolve_config(op, Mk, N, K, cfg, &c);
   if (st) return st;
   Plan pl;
-  return plan_shape(op, M > kMaxM ? kMaxM : M, N, K, c, &pl);
+  return plan_shape(op, Mk, N, K, c, &pl);
 }
 
 size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg) {

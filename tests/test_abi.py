@@ -51,8 +51,6 @@ def test_version_and_status_strings():
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16, 32, 40, 64, 96, 128])
 def test_default_config_is_valid_for_every_decode_shape(name, M):
     op, N, K = QWEN[name]
-    if op == SK_OP_LM_ARGMAX and M > 64:
-        pytest.skip("lm_argmax takes at most 64 rows per call")
     cfg = _lib.default_config(op, M, N, K)
     assert _lib.check_config(op, M, N, K, cfg) == SK_OK, cfg
     # The waves cover K (per path: 32-column units, 512-column units, or one
@@ -65,15 +63,18 @@ def test_default_config_is_valid_for_every_decode_shape(name, M):
         assert cfg.path == SK_PATH_MFMA_LDS
         assert cfg.waves * cfg.split >= -(-K // (32 * cfg.ku))
     ws = _lib.workspace_bytes(op, M, N, K, cfg)
+    # row groups: counters and partials per group of ceil(M / groups) rows
+    g = max(cfg.groups, 1)
     if op == SK_OP_LM_ARGMAX:
-        assert ws == _tickets(1) + 8 * min(M, 64)
+        assert ws == _tickets(g) + 8 * M
     elif cfg.split == 1:
         assert ws == 0
     else:
         # output columns per tile: 16 for MFMA gate/up (16 gate + 16 up rows), else `rows`
         out_rows = 16 if (op == SK_OP_GATEUP and cfg.path != SK_PATH_GEMV) else cfg.rows
         tiles = -(-N // out_rows)
-        assert ws == _tickets(tiles) + (2 if op == SK_OP_GATEUP else 1) * cfg.split * min(M, 64) * N * 4
+        rows = g * -(-M // g) if g > 1 else min(M, 64)
+        assert ws == _tickets(g * tiles) + (2 if op == SK_OP_GATEUP else 1) * cfg.split * rows * N * 4
 
 
 def test_tuned_table_drives_the_decode_shapes():
@@ -220,6 +221,40 @@ def test_row_groups_planning():
     # below M = 64 a hand-off op keeps its projection's nearer entry
     assert _lib.default_config(SK_OP_RESID_GEMM, 32, 2560, 9728).as_dict() == \
         _lib.default_config(SK_OP_GEMM, 32, 2560, 9728).as_dict()
+
+
+def test_wide_calls_plan_one_launch_of_row_groups():
+    """Up to 128 rows run as one launch when the configuration splits them
+    into row groups of at most 64 (the tuned entries do, for every Qwen3-4B
+    projection); more rows run as 128-row launches plus the remainder.  An
+    ungrouped configuration keeps 64-row launches."""
+    for name in ("qkv", "o", "gu", "d", "lm_argmax", "lm"):
+        op, N, K = QWEN[name]
+        for M in (65, 100, 128):
+            cfg = _lib.default_config(op, M, N, K)
+            assert cfg.groups > 1 and -(-M // cfg.groups) <= 32, (name, M, cfg)
+            assert _lib.check_config(op, M, N, K, cfg) == SK_OK, (name, M)
+    # one launch of four 32-row groups: the split-K partials of every group,
+    # once; 129 rows take one more launch, which reuses that workspace
+    op, N, K = QWEN["d"]
+    cfg = _lib.default_config(op, 128, N, K)
+    assert cfg.split > 1
+    one = _lib.workspace_bytes(op, 128, N, K)
+    assert one == _tickets(cfg.groups * (N // 16)) + cfg.groups * cfg.split * 32 * N * 4
+    assert _lib.workspace_bytes(op, 129, N, K) == one
+    assert _lib.workspace_bytes(op, 256, N, K) == one
+    # an explicit ungrouped configuration: 64-row launches
+    plain = SkConfig.make(_LDS, 8, 8, 32, 5, 0)
+    assert _lib.check_config(op, 128, N, K, plain) == SK_OK
+    assert _lib.workspace_bytes(op, 128, N, K, plain) == _lib.workspace_bytes(op, 64, N, K, plain)
+    # row groups hold at most 64 rows each, launches at most 128
+    ring = SkConfig.make(_LDS, 10, 8, 16, 1, 64, 2)
+    assert _lib.check_config(SK_OP_GEMM, 128, 6144, 2560, ring) == SK_OK   # two 64-row launches of 2 x 32
+    # the hand-off ops take up to 128 rows in one launch
+    for op, N, K in ((SK_OP_PRE_GEMM, 6144, 2560), (SK_OP_RESID_GEMM, 2560, 9728), (SK_OP_RESID_GEMM, 2560, 4096)):
+        cfg = _lib.default_config(op, 128, N, K)
+        assert cfg.groups > 1 and _lib.check_config(op, 128, N, K, cfg) == SK_OK, (op, N, K)
+        assert _lib.check_config(op, 129, N, K, cfg) == SK_ERR_SHAPE
 
 
 def test_valid_call_without_gpu_fails_loudly():
@@ -409,7 +444,7 @@ def test_handoff_argument_validation_precedes_any_device_work():
     assert _resid(lib, sq=RO0 + 64) == SK_ERR_ALIAS     # partial sums overlap the residual
     assert _resid(lib, ro=R0 + 2) == SK_ERR_ALIAS       # partially overlapping residuals
     assert _resid(lib, ldr=100) == SK_ERR_SHAPE
-    assert _resid(lib, M=65) == SK_ERR_SHAPE
+    assert _resid(lib, M=129) == SK_ERR_SHAPE
     assert _resid(lib, M=0, A=None, r=None, ro=None, sq=None) == SK_OK
     assert _resid(lib, K=9728, cfg=SkConfig.make(_LDS, 13, 8, 16, 3)) == SK_ERR_WORKSPACE
     assert _pre(lib, nw=None) == SK_ERR_NULL

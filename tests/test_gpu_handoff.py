@@ -71,7 +71,7 @@ PRODUCER_CASES = {   # (N, K): o_proj, down (split-K with fixup at M >= 2), ragg
 
 
 @pytest.mark.parametrize("case", list(PRODUCER_CASES))
-@pytest.mark.parametrize("M", [1, 5, 16, 32, 50, 64])
+@pytest.mark.parametrize("M", [1, 5, 16, 32, 50, 64, 100, 128])
 def test_gemm_residual_bit_exact_against_gemm_plus_add(case, M):
     N, Kd = PRODUCER_CASES[case]
     a, w, r = _rand((M, Kd), 1 + M), _rand((N, Kd), 2, 0.02), _rand((M, N), 3 + M)
@@ -128,7 +128,7 @@ def _sq_of(x: torch.Tensor) -> torch.Tensor:
     return _sums16(x).float().to(DEV)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8, 16, 64])
+@pytest.mark.parametrize("M", [1, 3, 8, 16, 64, 128])
 def test_rmsnorm_pre_gemm_exact_stats_equals_unfused_pipeline(M):
     x, wn, w = _exact((M, H), 20 + M), _gain(120), _rand((6144, H), 21, 0.02)
     xd, wnd, wd = x.to(DEV), wn.to(DEV), w.to(DEV)
@@ -139,7 +139,7 @@ def test_rmsnorm_pre_gemm_exact_stats_equals_unfused_pipeline(M):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("M", [1, 8, 16, 64])
+@pytest.mark.parametrize("M", [1, 8, 16, 64, 128])
 def test_rmsnorm_pre_gateup_exact_stats_equals_unfused_pipeline(M):
     I = 9728
     x, wn, wgu = _exact((M, H), 30 + M), _gain(130), _rand((2 * I, H), 31, 0.02)
@@ -152,7 +152,7 @@ def test_rmsnorm_pre_gateup_exact_stats_equals_unfused_pipeline(M):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 
 
-@pytest.mark.parametrize("M", [1, 8, 16, 64])
+@pytest.mark.parametrize("M", [1, 8, 16, 64, 128])
 def test_rmsnorm_pre_lm_argmax_exact_stats_equals_unfused_pipeline(M):
     V = 151936
     x, wn, w = _exact((M, H), 40 + M), _gain(140), _rand((V, H), 41, 0.02)
@@ -164,7 +164,7 @@ def test_rmsnorm_pre_lm_argmax_exact_stats_equals_unfused_pipeline(M):
     assert torch.equal(ids, rids) and torch.equal(mv, rmv)
 
 
-@pytest.mark.parametrize("M", [1, 16, 50, 64])
+@pytest.mark.parametrize("M", [1, 16, 50, 64, 100])
 def test_rmsnorm_pre_gemm_random_against_oracle(M):
     x, wn, w = _rand((M, H), 50 + M), _gain(150), _rand((6144, H), 51, 0.02)
     got = K.rmsnorm_pre_gemm(x.to(DEV), _sq_of(x), wn.to(DEV), EPS, w.to(DEV))
@@ -172,7 +172,7 @@ def test_rmsnorm_pre_gemm_random_against_oracle(M):
     assert_parity(got, from_bits(oracle.gemm(h, bits(w))), f"pre gemm M={M}")
 
 
-@pytest.mark.parametrize("M", [1, 5, 16, 64])
+@pytest.mark.parametrize("M", [1, 5, 16, 64, 128])
 def test_rmsnorm_pre_gateup_random_against_oracle(M):
     """The gate/up consumer on random residual rows (M = 16 is the decode
     step's batch) against the oracle's add_rmsnorm + gate/up + SwiGLU."""

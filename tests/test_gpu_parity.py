@@ -90,7 +90,8 @@ def test_gemm_lm_head_logits(M):
 @pytest.mark.parametrize("shape", [(6144, 2560), (2560, 9728), (777, 2560)], ids=["6144x2560", "2560x9728", "777x2560"])
 def test_gemm_reference_grid(shape, M):
     """The reference's own GEMM test grid (tests/test_kernels.py:111-124),
-    including M > 64 (processed as 64-row chunks) and the ragged N = 777."""
+    including M > 64 (row groups in one launch where the table has them, else
+    64-row launches) and the ragged N = 777."""
     N, Kd = shape
     w = _weights(N, Kd, seed=3 * N)
     x = _acts(M, Kd, seed=5)
@@ -98,6 +99,52 @@ def test_gemm_reference_grid(shape, M):
     ref = _oracle_gemm(x, w)
     assert_parity(out, ref, f"ref grid N={N} K={Kd} M={M}")
     assert reference_tolerance_ok(out, ref)
+
+
+M_WIDE = [65, 100, 128, 129, 200]
+
+
+@pytest.mark.parametrize("M", M_WIDE)
+@pytest.mark.parametrize("name", ["qkv", "o_proj", "gate_up", "down"])
+def test_wide_calls_default_config(name, M):
+    """More than 64 rows, as in the reference's verify forward at batch 16
+    (B x R = 128 rows): up to 128 rows run as one launch of row groups, more
+    as 128-row launches plus the remainder, default configuration."""
+    if name == "gate_up":
+        I2, Kd = GU
+        I = I2 // 2
+        wgu = _weights(I2, Kd, seed=17)
+        x = _acts(M, Kd, seed=17)
+        wd = _gpu(wgu)
+        out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:])
+        assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup M={M}")
+        return
+    N, Kd = {"qkv": QKV, "o_proj": O, "down": D}[name]
+    w = _weights(N, Kd, seed=N + Kd)
+    x = _acts(M, Kd, seed=N)
+    out = K.gemm(x.to(DEV), _gpu(w))
+    torch.cuda.synchronize()
+    assert_parity(out, _oracle_gemm(x, w), f"gemm {name} M={M}")
+
+
+@pytest.mark.parametrize("M", [100, 128])
+def test_wide_lm_head(M):
+    """lm_head at up to 128 rows in one launch: the fused argmax (default
+    configuration) and the logits GEMM; more rows than one launch holds are
+    refused by the fused argmax, whose ids come from one pass."""
+    V, Kd = LM
+    w = _weights(V, Kd, seed=7)
+    x = _acts(M, Kd, seed=11)
+    wd = _gpu(w)
+    ids, maxv = K.lm_argmax(x.to(DEV), wd)
+    logits = oracle.gemm(bits(x), bits(w))
+    o_ids, o_maxv = oracle.argmax(logits)
+    check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax M={M}")
+    out = K.gemm(x.to(DEV), wd)
+    torch.cuda.synchronize()
+    assert_parity(out, from_bits(logits), f"lm logits M={M}")
+    with pytest.raises(SkError):
+        K.lm_argmax(_acts(129, Kd, seed=11).to(DEV), wd)
 
 
 GEMM_CONFIGS = [
