@@ -26,8 +26,9 @@ synthetic Qwen3-4B (36 layers, random bf16 weights) decoding greedily at
 batch 16 after a 1024-token prompt, one HIP graph per decode step, reported as
 decode tok/s = 16 * steps / decode time (and end-to-end tok/s including the
 prefill); inside it, ``host_delivery`` is the same generation through the
-pipelined host token loop and ``verify`` one speculative verify pass (16
-sequences x 4 draft-tree rows).  The ``attention`` object times the decode
+pipelined host token loop and ``verify`` one speculative verify pass at the
+reference's batch-16 width (16 sequences x 8 draft-tree rows = 128 rows,
+engine.py:451), ``verify_r4`` the same with 4 rows per sequence.  The ``attention`` object times the decode
 step's attention launch (q/k norm + rotary + KV write + GQA attention) alone at
 batch 16, position 1088, with its achieved HBM bandwidth (the K and V rows read
 per launch).  ``hipblaslt_us`` beside each per-GEMM point is the vendor
@@ -535,16 +536,22 @@ def decode_benchmark(steps: int, B: int = 16, T: int = 1024, max_new: int | None
     d = time_delivery(plan, ids, steps + 1)
     log(f"decode with host delivery: {d['delivered_tok_s']:.0f} tok/s delivered, end-to-end {d['e2e_tok_s']:.0f} tok/s")
     v = verify_benchmark(plan)
+    v4 = verify_benchmark(plan, 4, (-1, 0, 0, 1))
     out = {"tok_s": round(r["tok_s"], 1), "ms_per_step": round(r["ms_per_step"], 4), "steps": steps, "B": B,
            "prompt": T, "prefill_s": round(r["prefill_s"], 4), "e2e_tok_s": round(r["e2e_tok_s"], 1),
            "host_delivery": {"delivered_tok_s": round(d["delivered_tok_s"], 1), "e2e_tok_s": round(d["e2e_tok_s"], 1),
                              "first_token_s": round(d["first_token_s"], 4), "depth": d["depth"]},
            "workload": "synthetic qwen3-4b greedy decode, 36 layers, GQA 32/8, cap %d, HIP graph per step" % plan.cap,
-           "verify": v}
+           "verify": v, "verify_r4": v4}
     return out
 
 
-def verify_benchmark(plan, R: int = 4, parents=(-1, 0, 0, 1), replays: int = 20) -> dict:
+# The reference's 8-node draft tree (its greedy template builder, recycle.py:75-95,
+# under the default "flat" rank prior): node t's parent.
+TREE8 = (-1, 0, 0, 1, 0, 2, 1, 0)
+
+
+def verify_benchmark(plan, R: int = 8, parents=TREE8, replays: int = 20) -> dict:
     """One speculative verify pass (engine/model.py:334-375) over the decode
     model's cache: B sequences x R rows (a draft tree), M = B*R rows through
     every projection, tree-masked attention, greedy token per row; captured

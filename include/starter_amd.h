@@ -112,8 +112,7 @@ typedef enum sk_path {
  * rows in one launch, so each weight tile leaves HBM once for all of them.
  * A call with more rows runs as several launches of that many rows (64, or
  * 128 when the configuration for 128 rows has groups) plus the remainder,
- * each streaming the weights again; the fused argmax ops (LM_ARGMAX and its
- * norm/consumer variants) take at most one launch's rows per call.
+ * each streaming the weights again (the hand-off ops take one launch's rows).
  */
 typedef struct sk_config {
   int32_t path;

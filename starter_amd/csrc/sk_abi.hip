@@ -731,7 +731,6 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
   if (nrm && K > sk::RMS_THREADS * 8 * sk::RMS_MAX_CHUNKS) return SK_ERR_SHAPE;
   if (!aligned16(A) || !aligned16(W0) || (W1 && !aligned16(W1)) || (lda & 7) || (ldw & 7)) return SK_ERR_ALIGN;
   if (nrm && (!aligned16(nrm->y) || !aligned16(nrm->w) || !aligned16(nrm->xout))) return SK_ERR_ALIGN;
-  if (bop == SK_OP_LM_ARGMAX && M > launch_rows(op, M, N, K, cfg)) return SK_ERR_SHAPE;   // one pass
   // Outputs are written while other workgroups may still read the inputs.
   const size_t a_bytes = ((size_t)(M - 1) * lda + K) * sizeof(sk_bf16);
   const size_t c_bytes = bop == SK_OP_LM_ARGMAX ? 0 : ((size_t)(M - 1) * ldc + N) * sizeof(sk_bf16);

@@ -278,11 +278,14 @@ def _path(parents: list[int], t: int) -> list[int]:
     return path[::-1]
 
 
-@pytest.mark.parametrize("tree", [False, True])
-def test_verify_plan_matches_reference(tree):
+@pytest.mark.parametrize("tree,B,R", [(False, 4, 4), (True, 4, 4), (True, 16, 8)])
+def test_verify_plan_matches_reference(tree, B, R):
     """VerifyPlan (engine/model.py:334-375): after a prefill, one pass over
     R = 4 rows per sequence (the last accepted token and three drafts, as a
-    chain or as the tree 0 -> {1, 2}, 1 -> 3).  Row t's token must be the
+    chain or as the tree 0 -> {1, 2}, 1 -> 3), and the reference's batch-16
+    shape: 8 tree rows per sequence (engine.py:451), B x R = 128 rows through
+    every projection, with the 8-node template its tree builder makes
+    (recycle.py:75-95, prior "flat").  Row t's token must be the
     greedy token a causal restatement of the reference forward predicts after
     the prompt followed by the path root..t (positions T + depth), wherever
     that restatement's top-2 margin exceeds 0.05; a captured graph replays to
@@ -290,14 +293,14 @@ def test_verify_plan_matches_reference(tree):
     from starter_amd.decode import VerifyPlan
 
     model = SyntheticModel(CFG, DEV, seed=9, norm_noise=0.1)
-    B, T, R = 4, 40, 4
+    T = 40
     plan = DecodePlan(model, B, T, 16, handoff=False)
     g = torch.Generator(device=DEV).manual_seed(21)
     ids = torch.randint(0, CFG.vocab, (B, T), device=DEV, generator=g)
     plan.ids.copy_(ids)
     plan.prefill()
     vp = VerifyPlan(plan, R, tree=tree)
-    parents = [-1, 0, 0, 1] if tree else [-1, 0, 1, 2]
+    parents = {4: [-1, 0, 0, 1], 8: [-1, 0, 0, 1, 0, 2, 1, 0]}[R] if tree else [-1, 0, 1, 2]
     if tree:
         vp.set_tree(parents)
     drafts = torch.randint(0, CFG.vocab, (B, R - 1), device=DEV, generator=g)

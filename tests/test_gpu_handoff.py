@@ -112,11 +112,11 @@ def test_gemm_residual_rejects_aliasing_and_large_m():
     with pytest.raises(SkError) as e:
         K.gemm_residual(a, w, a, a, sq)   # r_out overlaps the projection's input
     assert e.value.status == SK_ERR_ALIAS
-    big = torch.zeros((65, Kd), dtype=BF16, device=DEV)
-    rr = torch.zeros((65, N), dtype=BF16, device=DEV)
+    big = torch.zeros((129, Kd), dtype=BF16, device=DEV)   # more rows than one launch
+    rr = torch.zeros((129, N), dtype=BF16, device=DEV)
     with pytest.raises(SkError) as e:
-        K.gemm_residual(big, w, rr, torch.empty_like(rr), torch.zeros((65, N // 16), dtype=torch.float32,
-                                                                      device=DEV))
+        K.gemm_residual(big, w, rr, torch.empty_like(rr), torch.zeros((129, N // 16), dtype=torch.float32,
+                                                                       device=DEV))
     assert e.value.status == SK_ERR_SHAPE
 
 
