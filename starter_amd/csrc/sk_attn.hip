@@ -139,6 +139,7 @@ struct AttnArgs {
   int rope_rows;
   float eps;
   const int32_t* depth;     // ROPE with TREE: [R] rotary offsets (row t rotates by pos + depth[t])
+  int rb_xcd;               // row blocks of one (b, kv head, split) launched 8 apart (one XCD)
 };
 
 
@@ -168,8 +169,21 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   const int dg = lane & 15, kr = lane >> 4;
   // Workgroup (b, kv head, row block, split): query rows rbk*QR .. +QR-1 of
   // the KV head's G*R rows (row = t*G + g), keys of split s.
+  // With rb_xcd, launch position 8i + x runs row block i mod NRB of the
+  // (b, kv head, split) unit 8(i / NRB) + x: workgroups are dealt to the 8
+  // XCDs round-robin, so the row blocks of one unit run side by side on one
+  // XCD and the later ones read the keys from its L2.
   const int S = a.S;
-  const int bq = blockIdx.x / S, s = blockIdx.x - (blockIdx.x / S) * S;
+  int bq, s;
+  if (a.rb_xcd) {
+    const int i = blockIdx.x >> 3, x = blockIdx.x & 7;
+    const int unit = 8 * (i / a.NRB) + x;
+    s = unit % S;
+    bq = (unit / S) * a.NRB + i % a.NRB;
+  } else {
+    bq = blockIdx.x / S;
+    s = blockIdx.x - (blockIdx.x / S) * S;
+  }
   const int bk = bq / a.NRB, rbk = bq - (bq / a.NRB) * a.NRB;
   const int b = bk / a.HKV, kh = bk - (bk / a.HKV) * a.HKV;
   const int rows = a.G * a.R;
@@ -636,6 +650,7 @@ int attn_run(const AttnPlan& p, sk::AttnArgs& a, int B, int HQ, int HKV, int R, 
   a.S = p.S;
   a.split_len = p.split_len;
   a.NRB = p.NRB;
+  a.rb_xcd = p.NRB > 1 && (B * HKV * p.S) % 8 == 0;
   a.scale = scale;
   const dim3 grid((unsigned)(B * HKV * p.NRB * p.S));
   const dim3 block(64 * kAttnWaves);

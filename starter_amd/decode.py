@@ -432,7 +432,10 @@ def time_decode(plan: DecodePlan, steps: int) -> dict:
     """Decode throughput the way the reference defines it (B tokens per step,
     QWEN_ENGINE_CONTRACT.md:93-102): ``steps`` graph replays after a prefill,
     bracketed by HIP events on the replay stream.  Returns tok/s, ms per step
-    and the prefill time."""
+    and the prefill time.  One untimed prefill runs first, so the timed one
+    finds the libraries it calls initialised (as after the reference engine's
+    warmup, engine.py:149-175), whichever phase of the process ran before."""
+    plan.prefill()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     plan.prefill()

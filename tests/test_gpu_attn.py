@@ -274,11 +274,11 @@ def test_decode_attention_visible_key_boundary(nsplit):
             assert torch.allclose(o, vc[b, kh, pos[b]].float(), atol=0.05), (b, kh)
 
 
-@pytest.mark.parametrize("R,nsplit", [(5, None), (8, 3), (3, 1), (2, None), (4, 2)])
+@pytest.mark.parametrize("R,nsplit", [(5, None), (8, 3), (3, 1), (2, None), (4, 2), (16, None), (16, 2)])
 def test_decode_attention_verify_rows_chain(R, nsplit):
-    """Speculative verify: R query rows per sequence (G*R = 8 .. 32 here: the
-    8-row instance, one full or partial 16-row block, or two blocks), chain
-    mask (row t sees keys <= pos + t)."""
+    """Speculative verify: R query rows per sequence (G*R = 8 .. 64 here: the
+    8-row instance, one full or partial 16-row block, or two to four blocks,
+    which run side by side on one XCD), chain mask (row t sees keys <= pos + t)."""
     B, HQ, HKV, CAP = 4, 32, 8, 700
     g = torch.Generator().manual_seed(R * 10 + (nsplit or 0))
     q = randn_bf16((B, HQ, R, D), 1.0, g)

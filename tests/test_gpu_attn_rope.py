@@ -112,7 +112,8 @@ def test_fused_graph_replay_with_growing_length():
 
 
 @pytest.mark.parametrize("B,HQ,HKV,R,cap,starts,parents,nsplit", [
-    (16, 32, 8, 4, 1300, tuple(range(1100, 1116)), (-1, 0, 0, 1), None),   # the bench's verify tree
+    (16, 32, 8, 4, 1300, tuple(range(1100, 1116)), (-1, 0, 0, 1), None),   # the bench's 4-row verify tree
+    (16, 32, 8, 8, 1300, tuple(range(1100, 1116)), (-1, 0, 0, 1, 0, 2, 1, 0), None),   # batch-16 verify: 32 rows
     (2, 8, 2, 5, 200, (50, 124), (-1, 0, 1, 1, 0), 2),                       # 20 rows: two row blocks
     (3, 8, 2, 3, 300, (0, 150, 250), (-1, 0, 0), 3),                         # first positions, splits
 ])
