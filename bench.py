@@ -34,7 +34,7 @@ batch 16, position 1088, with its achieved HBM bandwidth (the K and V rows read
 per launch).  ``hipblaslt_us`` beside each per-GEMM point is the vendor
 library's GEMM (torch.mm) on the same rotating weights.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep [--wide]] [--no-cpu]
                        [--decode-steps S] [--decode-only] [--attention-only]
        python bench.py --probe --probe-op OP --M M      (launches for rocprofv3 --pmc)
        python bench.py --counters-from FOLDER           (markdown table of the counter passes)
@@ -684,6 +684,8 @@ def main() -> int:
     ap.add_argument("--M", type=int, default=8)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--sweep", action="store_true", help="also time all five shapes at M in 1..64 (BASELINE config 4)")
+    ap.add_argument("--wide", action="store_true",
+                    help="with --sweep, also M = 96 and 128 (the reference's batch-16 verify width)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="CPU work in the reference baseline's sample (the oracle port gets half)")
@@ -782,7 +784,7 @@ def main() -> int:
     sweep = None
     if args.sweep:
         sweep = {}
-        for M in (1, 2, 4, 8, 16, 32, 40, 64):
+        for M in (1, 2, 4, 8, 16, 32, 40, 64) + ((96, 128) if args.wide else ()):
             wlM = Workload(min(args.layers, 12), M, seed=2)
             for name in SHAPES:
                 n = 8 if name == "lm_head" else 36
