@@ -113,6 +113,8 @@ typedef enum sk_path {
  * A call with more rows runs as several launches of that many rows (64, or
  * 128 when the configuration for 128 rows has groups) plus the remainder,
  * each streaming the weights again (the hand-off ops take one launch's rows).
+ * An explicit configuration applies to every launch of a call, the shorter
+ * last one included; sk_check_config checks them all.
  */
 typedef struct sk_config {
   int32_t path;

@@ -1037,13 +1037,10 @@ int sk_check_config(int op, int M, int N, int K, const sk_config* cfg) {
     return plan_handoff(op, M, N, K, cfg, &pl);
   }
   if (M < 1) return SK_ERR_SHAPE;
-  const int rows = launch_rows(op, M, N, K, cfg);
-  const int Mk = M > rows ? rows : M;
-  sk_config c;
-  int st = resolve_config(op, Mk, N, K, cfg, &c);
-  if (st) return st;
-  Plan pl;
-  return plan_shape(op, Mk, N, K, c, &pl);
+  // Every launch of the call (a row count past one launch's takes several,
+  // the last one shorter) must accept the configuration.
+  CallPlan cp;
+  return plan_call(op, M, N, K, cfg, &cp);
 }
 
 size_t sk_workspace_bytes(int op, int M, int N, int K, const sk_config* cfg) {

@@ -250,6 +250,13 @@ def test_wide_calls_plan_one_launch_of_row_groups():
     # row groups hold at most 64 rows each, launches at most 128
     ring = SkConfig.make(_LDS, 10, 8, 16, 1, 64, 2)
     assert _lib.check_config(SK_OP_GEMM, 128, 6144, 2560, ring) == SK_OK   # two 64-row launches of 2 x 32
+    # an explicit configuration must suit every launch: 129 rows leave a
+    # one-row launch, where four groups would leave three empty
+    four = SkConfig.make(_LDS, 10, 8, 16, 1, 64, 4)
+    assert _lib.check_config(SK_OP_GEMM, 128, 6144, 2560, four) == SK_OK
+    assert _lib.check_config(SK_OP_GEMM, 129, 6144, 2560, four) == SK_ERR_CONFIG
+    assert _lib.check_config(SK_OP_GEMM, 132, 6144, 2560, four) == SK_OK     # 128 + 4: four one-row groups
+
     # the hand-off ops take up to 128 rows in one launch
     for op, N, K in ((SK_OP_PRE_GEMM, 6144, 2560), (SK_OP_RESID_GEMM, 2560, 9728), (SK_OP_RESID_GEMM, 2560, 4096)):
         cfg = _lib.default_config(op, 128, N, K)
