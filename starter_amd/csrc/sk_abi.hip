@@ -402,17 +402,17 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
-    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // lm_head (four row groups, one launch)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // lm_head  ~290-310 us (four row groups; 362 as two 64-row launches)
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer, as for qkv
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
-    {SK_OP_GEMM, 151936, 2560, 128, {3, 10, 8, 16, 1, 256, 4}},  // lm_head logits, four row groups
+    {SK_OP_GEMM, 151936, 2560, 128, {3, 10, 8, 16, 1, 256, 4}},  // lm_head logits 306-342 us (four row groups; 512-workgroup grid 318)
 };
 
 // Tuned entry for op/N/K at the smallest tuned row count >= M among op's own
 // entries and those of `also` (-1: none), op's own entry first at equal row
-// counts.  The lm_head logits GEMM
-// shares the fused argmax entries; a hand-off op shares its projection's.
+// counts.  The lm_head logits GEMM shares the fused argmax entries; a hand-off
+// op shares its projection's.
 const Tuned* tuned_lookup(int op, int M, int N, int K, int also = -1) {
   const Tuned* best = nullptr;
   for (const Tuned& t : kTuned) {
@@ -654,9 +654,9 @@ size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Plans of one call: rows beyond one launch's (launch_rows) are processed in
 // chunks of that many rows (each streaming the weights once more), so a call
-// has at most two distinct chunk sizes.  Also the workspace it needs: the plans' counters and partials,
-// then, when the norm prologue runs as its own launch, the normalised
-// activations [M, K] at offset `norm_off`.
+// has at most two distinct chunk sizes.  Also the workspace it needs: the
+// plans' counters and partials, then, when the norm prologue runs as its own
+// launch, the normalised activations [M, K] at offset `norm_off`.
 struct CallPlan {
   Plan plans[2];
   int chunk = 0;                // rows per launch
