@@ -300,7 +300,7 @@ def test_ring_half_slab_in_flight(M, grid):
     assert_parity(out, _oracle_gemm(x, w), f"gemm half ring M={M} grid={grid}")
 
 
-@pytest.mark.parametrize("M,groups", [(33, 2), (50, 3), (61, 4), (64, 2)])
+@pytest.mark.parametrize("M,groups", [(33, 2), (50, 3), (61, 4), (64, 2), (100, 4), (128, 4), (128, 8)])
 @pytest.mark.parametrize("split", [1, 2])
 def test_ring_row_groups(M, groups, split):
     """Row groups: the rows split into `groups` independent GEMMs launched side
@@ -334,7 +334,7 @@ def test_ring_row_groups(M, groups, split):
         assert torch.equal(K.gemm(rows, _gpu(w), config=plain), out[g0:g0 + rows.shape[0]]), f"{what} rows {g0}+"
 
 
-@pytest.mark.parametrize("M,groups,grid", [(64, 2, 640), (49, 3, 96), (40, 2, 8)])
+@pytest.mark.parametrize("M,groups,grid", [(64, 2, 640), (49, 3, 96), (40, 2, 8), (128, 4, 256), (97, 4, 8)])
 def test_lm_argmax_row_groups(M, groups, grid):
     """The fused argmax with row groups: one arrival counter per group, every
     row's candidate in one table; a ragged vocabulary at one grid."""
