@@ -113,7 +113,8 @@ struct Plan {
   int tm = 0, tn = 0, tku = 0;  // template parameters: MT|MR, NT|R, KU bound
   int nrb = 0;                  // tiles along N
   int slice_units = 0;
-  int out_rows = 0;             // output columns per tile
+  int out_rows = 0;             // staged output columns per tile (the kernel's OUT_ROWS)
+  int tr = 0;                   // output columns per tile (<= out_rows; fewer on the ring path)
   size_t pre_lds = 0;           // per-wave weight staging (LDS-transposed MFMA path)
   size_t parts_lds = 0;         // fp32 partial tiles (pbuf buffers)
   int pbuf = 2;                 // partial tile buffers (1 only on the ring path when 2 do not fit)
@@ -232,14 +233,22 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     if (pl->tku < 0 || c.waves > sk::instance_waves(sk::KIND_MFMA, pl->tm, pl->tn, pl->tku, pl->epi))
       return SK_ERR_CONFIG;
   } else if (c.path == SK_PATH_MFMA_LDS) {
-    // One K range of KW = 32*ku columns per wave: 256 or 1024 (one or four
-    // 256-column chunks, ring-streamed) or 512 (whole tiles in flight).
-    if (gateup ? c.rows != 16 : (c.rows != 16 && c.rows != 32)) return SK_ERR_CONFIG;
-    if (c.ku != 8 && c.ku != 16 && c.ku != 32) return SK_ERR_CONFIG;
+    // One K range of KW = 32*ku columns per wave: 256, 1024 or 1280 (one,
+    // four or five 256-column chunks, ring-streamed) or 512 (whole tiles in
+    // flight).
+    // The ring path takes any tile height up to 32 rows (48 for gate/up):
+    // its slabs are 16 rows and the rows past `rows` are not loaded, so a
+    // tile of N / 256 rows gives every CU one tile.  The whole-tile body and
+    // the residual hand-off take 16 or 32 (gate/up: 16).
+    if (c.ku != 8 && c.ku != 16 && c.ku != 32 && c.ku != 40) return SK_ERR_CONFIG;
+    const bool any_rows = c.ku != 16 && variant == 0;
+    if (any_rows ? (c.rows < 1 || c.rows > (gateup ? 48 : 32))
+                 : (gateup ? c.rows != 16 : (c.rows != 16 && c.rows != 32)))
+      return SK_ERR_CONFIG;
     const int KW = 32 * c.ku;
     units = cdiv(K, KW);
     pl->tm = cdiv(M, 16);
-    pl->tn = gateup ? 2 : c.rows / 16;
+    pl->tn = gateup ? 2 * cdiv(c.rows, 16) : cdiv(c.rows, 16);
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
     if (c.waves > sk::instance_waves(sk::KIND_MFMT, pl->tm, pl->tn, KW, pl->epi)) return SK_ERR_CONFIG;
@@ -264,9 +273,12 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   const long per_wave = c.path == SK_PATH_MFMA_LDS ? 1 : c.ku;
   if ((long)c.waves * per_wave < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
   if (c.split > 1 && (c.split - 1) * pl->slice_units >= units) return SK_ERR_CONFIG;  // empty split
-  const int out_rows = (c.path == SK_PATH_MFMA) ? (gateup ? 16 : c.rows) : c.rows;
+  const int out_rows = c.path == SK_PATH_MFMA       ? (gateup ? 16 : c.rows)
+                       : c.path == SK_PATH_MFMA_LDS ? (gateup ? 8 * pl->tn : 16 * pl->tn)
+                                                    : c.rows;
   pl->out_rows = out_rows;
-  pl->nrb = cdiv(N, out_rows);
+  pl->tr = c.path == SK_PATH_MFMA_LDS ? c.rows : out_rows;
+  pl->nrb = cdiv(N, pl->tr);
   if (c.path == SK_PATH_MFMA_LDS) partial_rows = sk::lds_part_stride(pl->tm, pl->tn, pl->tku);
   pl->parts_lds = (size_t)2 * c.waves * M * partial_rows * sizeof(float);
   pl->stage_elem = stage_bytes(pl->epi) * (size_t)M * out_rows;
@@ -359,10 +371,13 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 6144, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // qkv       12.30 us  2558 GB/s (two row groups; 18.7 without)
     {SK_OP_GEMM, 6144, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // qkv       16.6 us  (four row groups, one launch; 24.9 as two 64-row launches)
     {SK_OP_GEMM, 2560, 4096, 1, {2, 4, 2, 2, 1, 0}},  // o_proj     5.94 us  3531 GB/s
-    {SK_OP_GEMM, 2560, 4096, 2, {2, 1, 8, 2, 1, 0}},  // o_proj     7.02 us  2991 GB/s
-    {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 16, 1, 0}},  // o_proj     6.95 us  3024 GB/s
-    {SK_OP_GEMM, 2560, 4096, 8, {3, 4, 32, 16, 1, 0}},  // o_proj     7.09 us  2971 GB/s
-    {SK_OP_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj     7.47 us  2834 GB/s
+    // o_proj at M = 2-16: 12- or 10-row tiles, one per CU (214 or 256
+    // workgroups of 16 waves; 16-row tiles leave 96 CUs idle): M = 8
+    // 7.13 -> 6.86 us, M = 2 6.76 (GEMV) -> 6.68 us.
+    {SK_OP_GEMM, 2560, 4096, 2, {3, 16, 8, 12, 1, 0}},  // o_proj     6.68 us  3144 GB/s
+    {SK_OP_GEMM, 2560, 4096, 4, {3, 16, 8, 12, 1, 0}},  // o_proj     6.68 us  3145 GB/s
+    {SK_OP_GEMM, 2560, 4096, 8, {3, 16, 8, 10, 1, 0}},  // o_proj     6.86 us  3066 GB/s
+    {SK_OP_GEMM, 2560, 4096, 16, {3, 16, 8, 10, 1, 0}},  // o_proj     7.34 us  2870 GB/s
     {SK_OP_GEMM, 2560, 4096, 32, {3, 4, 32, 16, 1, 0}},  // o_proj     9.13 us  2343 GB/s
     {SK_OP_GEMM, 2560, 4096, 40, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.96 us  2106 GB/s (three row groups; 11.6 without)
     {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.92 us  2114 GB/s (three row groups; 11.5 without)
@@ -383,15 +398,22 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 58.7 us (67.3 at grid 64)
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
-    {SK_OP_GEMM, 2560, 9728, 2, {3, 13, 8, 32, 3, 240}},  // down      12.53 us  3979 GB/s
-    {SK_OP_GEMM, 2560, 9728, 4, {3, 13, 8, 32, 3, 0}},  // down      12.60 us  3962 GB/s
-    {SK_OP_GEMM, 2560, 9728, 8, {3, 13, 8, 32, 3, 240}},  // down      12.78 us  3913 GB/s
+    // down at M = 2-8: eight waves of five 256-column chunks cover K = 9728
+    // without a global split (13.1 -> 12.6 us at M = 8).
+    {SK_OP_GEMM, 2560, 9728, 2, {3, 8, 40, 16, 1, 0}},  // down      12.08 us  4124 GB/s
+    {SK_OP_GEMM, 2560, 9728, 4, {3, 8, 40, 12, 1, 0}},  // down      12.16 us  4098 GB/s
+    {SK_OP_GEMM, 2560, 9728, 8, {3, 8, 40, 12, 1, 0}},  // down      12.59 us  3962 GB/s
     {SK_OP_GEMM, 2560, 9728, 16, {3, 13, 8, 32, 3, 240}},  // down      13.5 us  3717 GB/s (with partial rows padded; 14.0 with four-chunk waves)
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
     {SK_OP_GEMM, 2560, 9728, 128, {3, 10, 8, 16, 4, 64, 4}},  // down      38.0 us  (four row groups; 47.3 as two 64-row launches)
+    // Residual hand-off producers at decode row counts (the projection's
+    // entries above use tile heights the hand-off cannot take).
+    {SK_OP_RESID_GEMM, 2560, 4096, 8, {3, 16, 8, 16, 1, 0}},   // o_proj producer  7.46 us
+    {SK_OP_RESID_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj producer  7.91 us
+    {SK_OP_RESID_GEMM, 2560, 9728, 8, {3, 8, 40, 16, 1, 0}},   // down producer   13.18 us (16.24 with three splits)
     {SK_OP_RESID_GEMM, 2560, 9728, 64, {3, 10, 8, 16, 4, 128, 2}},  // down producer: its plain plan has no residual instance (64-row tiles)
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
@@ -821,6 +843,7 @@ int run_gemm_family(int op, const sk_bf16* A, int64_t lda, const NormIn* nrm, co
     a.slice_units = pl.slice_units;
     a.ku = pl.cfg.ku;
     a.nrb = pl.nrb;
+    a.tr = pl.tr;
     a.nw = pl.cfg.waves;
     a.grid = grid;
     a.rbstep = grid / pl.cfg.split;
@@ -991,6 +1014,7 @@ int run_handoff(int op, const sk_bf16* A, int64_t lda, const Handoff& h, const s
   a.slice_units = pl.slice_units;
   a.ku = pl.cfg.ku;
   a.nrb = pl.nrb;
+  a.tr = pl.tr;
   a.nw = pl.cfg.waves;
   a.grid = grid;
   a.rbstep = grid / pl.cfg.split;

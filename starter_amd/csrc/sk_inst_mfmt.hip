@@ -41,12 +41,22 @@ KernelFn mfmt_grouped_ptr() {
 #define SK_LIST(NT) \
   SK_C(1, NT, 512) SK_C(2, NT, 512) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(3, NT, 256) SK_C(4, NT, 256) \
   SK_C(1, NT, 1024) SK_C(2, NT, 1024) SK_C(3, NT, 1024) SK_C(4, NT, 1024)
+// Five 256-column chunks per wave (up to 32 rows): K = 9728 in eight waves
+// without a global split.
+#define SK_LONG_LIST(NT) SK_C(1, NT, 1280) SK_C(2, NT, 1280)
+
+// Gate/up tiles taller than 16 rows (ring path, up to 32 rows of activations):
+// two or three 16-row slabs of gate rows and as many of up rows, for tile
+// heights such as 38 = 9728 / 256 that give every CU one tile.
+#define SK_TALL_GU_LIST \
+  SK_C(1, 4, 256) SK_C(2, 4, 256) SK_C(1, 6, 256) SK_C(2, 6, 256)
 
 // Residual hand-off epilogues exist on the ring path only: the consumers
 // (EPI 8-10) with one 256-column chunk per wave, the producers (EPI 11-12)
 // with one or four.
 #define SK_PRE_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256)
-#define SK_RESID_LIST(NT) SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(1, NT, 1024) SK_C(2, NT, 1024)
+#define SK_RESID_LIST(NT) \
+  SK_C(1, NT, 256) SK_C(2, NT, 256) SK_C(1, NT, 1024) SK_C(2, NT, 1024) SK_C(1, NT, 1280) SK_C(2, NT, 1280)
 
 // Row groups: groups of up to 32 rows on the ring path, for the plain
 // projections and the residual hand-off producers (256- and 1024-column
@@ -84,11 +94,16 @@ KernelFn SK_CAT(mfmt_for_epi, SK_EPI)(int MT, int NT, int KW) {
 #elif SK_EPI == 11 || SK_EPI == 12
     SK_RESID_LIST(1)
     SK_RESID_LIST(2)
-#elif SK_EPI == 1 || SK_EPI == 4   // gate/up: 16 gate rows + 16 up rows
+#elif SK_EPI == 1 || SK_EPI == 4   // gate/up: NT/2 slabs of gate rows + NT/2 of up rows
     SK_LIST(2)
+    SK_TALL_GU_LIST
 #else
     SK_LIST(1)
     SK_LIST(2)
+#if SK_EPI == 0 || SK_EPI == 3
+    SK_LONG_LIST(1)
+    SK_LONG_LIST(2)
+#endif
 #endif
     default: break;
   }

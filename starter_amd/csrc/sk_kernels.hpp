@@ -86,6 +86,9 @@ struct Args {
   int slice_units;        // K units per global split
   int ku;                 // K units per wave
   int nrb;                // row blocks (tiles) along N
+  int tr;                 // output columns per tile: tile rb covers [rb*tr, rb*tr + tr); at most the
+                          // compile-time OUT_ROWS (the ring path takes fewer: the loads of a slab's
+                          // rows past tr read the zero line, their MFMA rows are never read)
   int nw;                 // waves per workgroup (blockDim.x / 64)
   int grid;               // workgroups launched (gridDim.x)
   int rbstep;             // grid / S: tile stride of one workgroup
@@ -333,8 +336,10 @@ __device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int n
   const int M = p.M;
   const int tid = threadIdx.x, nthr = 64 * p.nw;
   const int nout = M * OUT_ROWS;
+  const int TR = p.tr;
   for (int idx = tid; idx < nout; idx += nthr) {
     const int m = idx / OUT_ROWS, r = idx - (idx / OUT_ROWS) * OUT_ROWS;
+    if (r >= TR) continue;   // tile rows past tr: nothing to finish
     // Four waves' partials per step are read together (independent LDS loads
     // in flight), then added in wave order 0..nw-1; slots past nw-1 read wave
     // nw-1's slot (in bounds) and are masked to +0.
@@ -365,7 +370,7 @@ __device__ __forceinline__ void tile_reduce(const Args& p, const float* P, int n
       static_cast<float*>(stage)[2 * sidx] = g;
       static_cast<float*>(stage)[2 * sidx + 1] = u;
     } else {   // EPI_ARGMAX
-      const int n = rb * OUT_ROWS + r;
+      const int n = rb * TR + r;
       if (n < p.N) atomicMax(&lds_best[m], argmax_key(f2bf(g), n));
     }
   }
@@ -415,13 +420,14 @@ __device__ __forceinline__ void flush_stage(const Args& p, const void* stage, in
     const int r = idx % OUT_ROWS;
     const int jm = idx / OUT_ROWS;
     const int m = jm % M, j = jm / M;
-    const int n = (rb0 + j * p.rbstep) * OUT_ROWS + r;
+    // (the residual hand-off runs with tr = OUT_ROWS: 16-column groups of one tile)
+    const int n = (rb0 + j * p.rbstep) * p.tr + r;
     if constexpr (RESID) {
       static_assert(EPI == EPI_STORE, "the residual follows a finished projection");
       resid_out(p, m, n, n < p.N, static_cast<const uint16_t*>(stage)[idx], resid_in(p, m, n, n < p.N));
       continue;
     }
-    if (n >= p.N) continue;
+    if (r >= p.tr || n >= p.N) continue;
     if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
       p.C[(int64_t)m * p.ldc + n] = static_cast<const uint16_t*>(stage)[idx];
     } else if constexpr (EPI == EPI_PART) {
@@ -482,7 +488,7 @@ __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0,
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int idx = min(base + (int)threadIdx.x + i * nthr, M * OUT_ROWS - 1);
-          const int m = idx / OUT_ROWS, n = rb * OUT_ROWS + idx % OUT_ROWS;
+          const int m = idx / OUT_ROWS, n = rb * p.tr + idx % OUT_ROWS;
           e[i] = (int64_t)m * p.N + (n < p.N ? n : 0);   // clamped in bounds; stored only if real
           if constexpr (RESID) rres[i] = resid_in(p, m, n, n < p.N);
         }
@@ -509,7 +515,7 @@ __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0,
         for (int i = 0; i < 4; ++i) {
           const int idx = base + (int)threadIdx.x + i * nthr;
           const int m = idx / OUT_ROWS, r = idx % OUT_ROWS;
-          const int n = rb * OUT_ROWS + r;
+          const int n = rb * p.tr + r;
           if constexpr (RESID) {
             // every lane of a 16-column group takes part in the group sum
             // (idx < M*OUT_ROWS is uniform over each 16-lane group)
@@ -517,7 +523,7 @@ __device__ __forceinline__ void splitk_fixup(const Args& p, int ntiles, int rb0,
             if (idx < M * OUT_ROWS) resid_out(p, m, n, n < p.N, f2bf(n < p.N ? g[i] : 0.f), rres[i]);
             continue;
           }
-          if (idx >= M * OUT_ROWS || n >= p.N) continue;
+          if (idx >= M * OUT_ROWS || r >= p.tr || n >= p.N) continue;
           p.C[(int64_t)m * p.ldc + n] = (EPI == EPI_PART_GU) ? swiglu_bf(g[i], u[i]) : f2bf(g[i]);
         }
       }
@@ -974,7 +980,7 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int BASE = EpiTraits<EPI>::base;
   static_assert(!EpiTraits<EPI>::norm, "the LDS-fed MFMA path has no norm prologue");
-  static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
+  static_assert(!GATEUP || NT % 2 == 0, "gate/up tiles pair NT/2 slabs of gate rows with NT/2 of up rows");
   static_assert(CPW >= 1, "chunks per wave");
   constexpr bool PRE = EpiTraits<EPI>::pre;       // finish the RMSNorm from the producer's partials
   constexpr bool RESID = EpiTraits<EPI>::resid;   // hand the residual and its partials on
@@ -982,7 +988,7 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
   constexpr int CW = 256;                        // columns per chunk (slab width)
   constexpr int KW = CW * CPW;                   // columns per wave
   constexpr int ROWS = 16 * NT;                  // weight rows per tile
-  constexpr int OUT_ROWS = GATEUP ? 16 : ROWS;   // output columns per tile
+  constexpr int OUT_ROWS = GATEUP ? ROWS / 2 : ROWS;   // staged output columns per tile
   constexpr int UNITS = CW / 32;                 // MFMA K steps per slab
   constexpr int RING = 8;                        // load instructions per 16-row slab
   constexpr int RSLOTS = ring_slots(MT, CPW);    // of which in flight (ring registers)
@@ -1087,17 +1093,26 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
   }
 
   // Instruction q of slab (rb, c, nt): rows 2q + lane/32 of the 16-row group nt,
-  // 8 columns at kw0 + 256c + 8*(lane%32) (rows clamped in bounds).
+  // 8 columns at kw0 + 256c + 8*(lane%32) (rows clamped in bounds).  Tile rb
+  // holds weight rows rb*tr .. rb*tr + tr - 1 (gate/up: that many gate rows in
+  // slabs 0..NT/2-1 and up rows in the rest); slab rows past tr load the zero
+  // line (one broadcast line, no HBM traffic), so tr need not be a multiple
+  // of 16 and the host can give every CU the same number of rows.
   const int lrow = lane >> 5;
   auto col_of = [&](int c) { return kw0 + CW * c + 8 * (lane & 31); };
   auto wsrc_col = [&](int rb, int col, int nt, int q) -> const uint16_t* {
     const int t = 2 * q + lrow;
     if (!(has_unit && col < p.K)) return zero16;
     if constexpr (GATEUP) {
-      const int row = min(rb * 16 + t, p.N - 1);
-      return (nt == 0 ? p.W0 : p.W1) + (int64_t)row * p.ldw + col;
+      constexpr int H = NT / 2;
+      const int lr = 16 * (nt % H) + t;
+      if (lr >= p.tr) return zero16;
+      const int row = min(rb * p.tr + lr, p.N - 1);
+      return (nt < H ? p.W0 : p.W1) + (int64_t)row * p.ldw + col;
     } else {
-      const int row = min(rb * ROWS + 16 * nt + t, p.N - 1);
+      const int lr = 16 * nt + t;
+      if (lr >= p.tr) return zero16;
+      const int row = min(rb * p.tr + lr, p.N - 1);
       return p.W0 + (int64_t)row * p.ldw + col;
     }
   };

@@ -398,25 +398,28 @@ HANDOFF = {  # decode-step call sites at Qwen3-4B shapes
 }
 
 
-OWN_ENTRY = {"qkv_pre": (8, 16)}   # hand-off ops with table entries of their own at these M (<= 16)
+# hand-off ops with table entries of their own at these M (<= 16)
+OWN_ENTRY = {"qkv_pre": (8, 16), "o_resid": (8, 16), "d_resid": (8,)}
 
 
 @pytest.mark.parametrize("name", list(HANDOFF))
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
 def test_handoff_default_config_is_a_ring_config(name, M):
-    """Hand-off ops run on the ring-streamed LDS-fed MFMA path: their own
-    tuned entry where the table has one at the nearest row count (the qkv
-    consumer at M = 8 and 16: 16-row tiles), else the tuned projection
-    configuration where it is a ring configuration (M >= 2 at these shapes),
-    else a ring configuration; the workspace is the projection's own."""
+    """Hand-off ops run on the ring-streamed LDS-fed MFMA path with tiles of
+    16 or 32 rows: their own tuned entry where the table has one at the
+    nearest row count (the qkv consumer at M = 8 and 16, the producers at
+    decode row counts), else the tuned projection configuration where the
+    hand-off can take it (a ring configuration with such tiles), else a ring
+    configuration; the workspace is the projection's own."""
     op, N, K, base = HANDOFF[name]
+    kus = (8, 32, 40) if op == SK_OP_RESID_GEMM else (8,)
     cfg = _lib.default_config(op, M, N, K)
-    assert cfg.path == _LDS and cfg.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,))
+    assert cfg.path == _LDS and cfg.ku in kus and cfg.rows in (16, 32)
     assert _lib.check_config(op, M, N, K, cfg) == SK_OK
     b = _lib.default_config(base, M, N, K)
     if M in OWN_ENTRY.get(name, ()):
         assert cfg.rows == 16
-    elif b.path == _LDS and b.ku in ((8, 32) if op == SK_OP_RESID_GEMM else (8,)):
+    elif b.path == _LDS and b.ku in kus and b.rows in (16, 32):
         assert cfg.as_dict() == b.as_dict()
     assert _lib.workspace_bytes(op, M, N, K, cfg) == _lib.workspace_bytes(base, M, N, K, cfg)
 
