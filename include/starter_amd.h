@@ -85,13 +85,19 @@ typedef enum sk_path {
  * from an offline-tuned table (sk_default_config) and an explicit config can
  * be passed to any op (NULL = default) to test or time one candidate.
  *
- *   path   : SK_PATH_MFMA or SK_PATH_GEMV
+ *   path   : SK_PATH_MFMA, SK_PATH_MFMA_LDS or SK_PATH_GEMV
  *   waves  : wavefronts per workgroup; they split the workgroup's K slice and
  *            their fp32 partials are summed in LDS in fixed wave order
  *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns;
- *            MFMA_LDS: 8, 16 or 32, i.e. 256, 512 or 1024 columns per wave;
- *            256 and 1024 stream 256-column chunks through an 8-load ring)
- *   rows   : weight rows per workgroup tile (MFMA: 16 or 32; GEMV: 1..8)
+ *            MFMA_LDS: 8, 16, 32 or 40, i.e. 256, 512, 1024 or 1280 columns
+ *            per wave; all but 512 stream 256-column chunks through an
+ *            8-load ring)
+ *   rows   : weight rows per workgroup tile (MFMA: 16 or 32; GEMV: 1..8;
+ *            MFMA_LDS ring, i.e. ku != 16: any height 1..32, for gate/up
+ *            1..48 gate rows and as many up rows, loaded as 16-row slabs
+ *            whose rows past the tile are not read, so a height of N / 256
+ *            gives every CU one tile; the whole-tile body (ku 16) and the
+ *            residual hand-off ops take 16 or 32, gate/up 16)
  *   split  : global K splits; >1 writes fp32 partials to the workspace and
  *            the last workgroup to finish a tile sums them in fixed split
  *            order (no floating-point atomics, no second kernel)
@@ -114,7 +120,10 @@ typedef enum sk_path {
  * 128 when the configuration for 128 rows has groups) plus the remainder,
  * each streaming the weights again (the hand-off ops take one launch's rows).
  * An explicit configuration applies to every launch of a call, the shorter
- * last one included; sk_check_config checks them all.
+ * last one included; sk_check_config checks them all.  A shorter last launch
+ * with fewer rows than the configuration has groups can give each one (e.g.
+ * the one row left of 129) runs with as many groups as hold a row, so the
+ * configuration sk_default_config returns for M rows suits every launch.
  */
 typedef struct sk_config {
   int32_t path;

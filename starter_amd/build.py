@@ -134,8 +134,11 @@ def build(jobs: int | None = None, verbose: bool = False, incremental: bool = Fa
     return LIB
 
 
-_INSTANCE = re.compile(r"_ZN2sk10(gemv|mfma|mfmt)_entryILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)EEEvNS_4ArgsE")
-_KINDS = {"gemv": 0, "mfma": 1, "mfmt": 2}
+_INSTANCE = re.compile(
+    r"_ZN2sk(?:10|18)(gemv|mfma|mfmt|mfmt_grouped)_entryILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)EEEvNS_4ArgsE")
+# The row-group entry of an LDS-fed MFMA instance is compiled for the plain
+# instance's tier (one table key): a spill in either moves both down.
+_KINDS = {"gemv": 0, "mfma": 1, "mfmt": 2, "mfmt_grouped": 2}
 # (waves per workgroup, VGPRs + AGPRs per lane the compiler may then use)
 _TIERS = ((16, 128), (12, 168), (8, 256), (4, 512))
 

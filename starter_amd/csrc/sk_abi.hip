@@ -712,6 +712,17 @@ int plan_call(int op, int M, int N, int K, const sk_config* cfg, CallPlan* cp) {
     sk_config c;
     int st = resolve_config(op, cp->chunk_rows[i], N, K, cfg, &c);
     if (st) return st;
+    // A configuration with row groups applies to every launch of the call; a
+    // launch with too few rows to give each group one (the remainder after
+    // 128-row launches, e.g. one row of 129) runs with as many groups as
+    // hold a row, so the configuration default_config returns for the whole
+    // call is accepted for every launch.
+    if (cp->nplans == 2 && i == 1 && c.groups > 1) {
+      const int rows = cp->chunk_rows[i];
+      int g = c.groups;
+      while (g > 1 && (g - 1) * cdiv(rows, g) >= rows) --g;
+      c.groups = g > 1 ? g : 0;
+    }
     st = plan_shape(op, cp->chunk_rows[i], N, K, c, &cp->plans[i]);
     if (st) return st;
   }

@@ -36,6 +36,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -590,15 +591,23 @@ class DecodeAttention:
 
 
 def ancestor_masks(parent: list[int]) -> list[int]:
-    """Per-node int64 bit mask of the node and its ancestors (engine/kernels/attention.py:245-254)."""
-    masks = []
-    for i in range(len(parent)):
-        m, n = 0, i
-        while n >= 0:
-            m |= 1 << n
-            n = parent[n]
-        masks.append(m - (1 << 64) if m >= (1 << 63) else m)
-    return masks
+    """Per-node int64 bit mask of the node and its ancestors: bit j of node
+    i's mask is set when j is i or on i's path to the root, the format the
+    tree attention consumes (engine/kernels/attention.py:245-254).
+
+    A draft tree lists every parent before its children (parent[i] < i, -1
+    for a root), so one pass in node order builds each mask from its parent's:
+    mask[i] = mask[parent[i]] | bit i.  The masks are formed as uint64 and
+    reinterpreted as int64, so node 63 gives the sign bit."""
+    n = len(parent)
+    if n > 64:
+        raise ValueError(f"a draft tree of {n} nodes does not fit 64-bit masks")
+    masks = np.zeros(n, dtype=np.uint64)
+    for i, p in enumerate(parent):
+        if not -1 <= p < i:
+            raise ValueError(f"node {i}: parent {p} must be -1 or an earlier node")
+        masks[i] = (masks[p] if p >= 0 else np.uint64(0)) | (np.uint64(1) << np.uint64(i))
+    return masks.view(np.int64).tolist()
 
 
 def chain_tree(R: int, device) -> torch.Tensor:

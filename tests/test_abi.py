@@ -98,6 +98,22 @@ def test_heuristic_for_untuned_shapes():
     assert _lib.check_config(SK_OP_GEMM, 8, 777, 96, c) == SK_OK
 
 
+@pytest.mark.parametrize("name", list(QWEN) + ["rms_qkv", "rms_gu", "rms_lm"])
+def test_default_config_suits_every_launch_of_the_call(name):
+    """The configuration default_config returns for M rows, passed back
+    explicitly, is accepted for every launch of the call at every M up to 256
+    (above 128 rows the call runs as 128-row launches plus the remainder,
+    which runs with as many row groups as hold a row)."""
+    from starter_amd._lib import SK_OP_RMSNORM_GATEUP, SK_OP_RMSNORM_GEMM, SK_OP_RMSNORM_LM_ARGMAX
+
+    op, N, K = {"rms_qkv": (SK_OP_RMSNORM_GEMM, 6144, 2560), "rms_gu": (SK_OP_RMSNORM_GATEUP, 9728, 2560),
+                "rms_lm": (SK_OP_RMSNORM_LM_ARGMAX, 151936, 2560)}.get(name) or QWEN[name]
+    for M in range(1, 257):
+        cfg = _lib.default_config(op, M, N, K)
+        assert _lib.check_config(op, M, N, K, cfg) == SK_OK, (name, M, cfg)
+        assert _lib.workspace_bytes(op, M, N, K, cfg) == _lib.workspace_bytes(op, M, N, K, None), (name, M)
+
+
 def test_default_config_prefers_no_global_split_at_decode_m():
     for name in ("qkv", "gu", "lm_argmax"):
         op, N, K = QWEN[name]
@@ -250,12 +266,16 @@ def test_wide_calls_plan_one_launch_of_row_groups():
     # row groups hold at most 64 rows each, launches at most 128
     ring = SkConfig.make(_LDS, 10, 8, 16, 1, 64, 2)
     assert _lib.check_config(SK_OP_GEMM, 128, 6144, 2560, ring) == SK_OK   # two 64-row launches of 2 x 32
-    # an explicit configuration must suit every launch: 129 rows leave a
-    # one-row launch, where four groups would leave three empty
+    # an explicit configuration applies to every launch: 129 rows leave a
+    # one-row launch, which runs without groups (four would leave three
+    # empty), 130 two groups of one row, 132 four
     four = SkConfig.make(_LDS, 10, 8, 16, 1, 64, 4)
     assert _lib.check_config(SK_OP_GEMM, 128, 6144, 2560, four) == SK_OK
-    assert _lib.check_config(SK_OP_GEMM, 129, 6144, 2560, four) == SK_ERR_CONFIG
+    assert _lib.check_config(SK_OP_GEMM, 129, 6144, 2560, four) == SK_OK
+    assert _lib.check_config(SK_OP_GEMM, 130, 6144, 2560, four) == SK_OK
     assert _lib.check_config(SK_OP_GEMM, 132, 6144, 2560, four) == SK_OK     # 128 + 4: four one-row groups
+    # a single launch must still give every group a row
+    assert _lib.check_config(SK_OP_GEMM, 3, 6144, 2560, four) == SK_ERR_CONFIG
 
     # the hand-off ops take up to 128 rows in one launch
     for op, N, K in ((SK_OP_PRE_GEMM, 6144, 2560), (SK_OP_RESID_GEMM, 2560, 9728), (SK_OP_RESID_GEMM, 2560, 4096)):

@@ -22,6 +22,24 @@ def test_instance_names_parse():
     m = B._INSTANCE.fullmatch("_ZN2sk10gemv_entryILi8ELi8ELi10ELi7EEEvNS_4ArgsE")
     assert m and m.group(1) == "gemv" and tuple(map(int, m.groups()[1:])) == (8, 8, 10, 7)
     assert B._INSTANCE.fullmatch("_ZN2sk18decode_attn_kernelILi4ELi8ELb0ELb1EEEvNS_8AttnArgsE") is None
+    m = B._INSTANCE.fullmatch("_ZN2sk18mfmt_grouped_entryILi2ELi1ELi256ELi3EEEvNS_4ArgsE")
+    assert m and B._KINDS[m.group(1)] == 2 and tuple(map(int, m.groups()[1:])) == (2, 1, 256, 3)
+
+
+def test_retier_moves_a_spilling_row_group_entry_with_its_plain_instance(tmp_path, monkeypatch):
+    """The row-group entry shares its plain instance's tier: when only the
+    grouped entry spills, the shared key moves one tier down."""
+    monkeypatch.setattr(B, "TIERS_INC", tmp_path / "sk_tiers.inc")
+    budget = dict(B._TIERS)
+
+    def fake_compile(units, jobs, incremental=False, verbose=False):
+        waves = B._read_tiers().get((2, 2, 1, 256, 3), 16)
+        need = 150   # the grouped entry needs 150 registers: spills at 16 waves (128), fits at 12 (168)
+        spills = [("_ZN2sk18mfmt_grouped_entryILi2ELi1ELi256ELi3EEEvNS_4ArgsE", need - budget[waves], budget[waves])]
+        return [(None, spills if need > budget[waves] else [])]
+
+    monkeypatch.setattr(B, "_compile", fake_compile)
+    assert B.retier(jobs=1, fresh=True) == {(2, 2, 1, 256, 3): 12}
 
 
 def test_tier_table_round_trip(tmp_path, monkeypatch):

@@ -127,6 +127,42 @@ def test_wide_calls_default_config(name, M):
     assert_parity(out, _oracle_gemm(x, w), f"gemm {name} M={M}")
 
 
+@pytest.mark.parametrize("M", [129, 130])
+@pytest.mark.parametrize("name", ["qkv", "gate_up", "lm_argmax"])
+def test_wide_calls_with_the_default_config_passed_explicitly(name, M):
+    """default_config(op, M) passed back explicitly: the 128-row launch runs
+    its row groups, the one- or two-row remainder as many groups as hold a row."""
+    from starter_amd._lib import SK_OP_LM_ARGMAX, default_config
+
+    if name == "gate_up":
+        I2, Kd = GU
+        I = I2 // 2
+        wgu = _weights(I2, Kd, seed=17)
+        x = _acts(M, Kd, seed=23)
+        wd = _gpu(wgu)
+        cfg = default_config(SK_OP_GATEUP, M, I, Kd)
+        out = K.gateup_swiglu(x.to(DEV), wd[:I], wd[I:], config=cfg)
+        assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"gateup M={M} {cfg}")
+        return
+    if name == "lm_argmax":
+        V, Kd = LM
+        w = _weights(V, Kd, seed=7)
+        x = _acts(M, Kd, seed=29)
+        cfg = default_config(SK_OP_LM_ARGMAX, M, V, Kd)
+        ids, maxv = K.lm_argmax(x.to(DEV), _gpu(w), config=cfg)
+        logits = oracle.gemm(bits(x), bits(w))
+        o_ids, o_maxv = oracle.argmax(logits)
+        check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax M={M} {cfg}")
+        return
+    N, Kd = QKV
+    w = _weights(N, Kd, seed=N + Kd)
+    x = _acts(M, Kd, seed=31)
+    cfg = default_config(SK_OP_GEMM, M, N, Kd)
+    out = K.gemm(x.to(DEV), _gpu(w), config=cfg)
+    torch.cuda.synchronize()
+    assert_parity(out, _oracle_gemm(x, w), f"qkv M={M} {cfg}")
+
+
 @pytest.mark.parametrize("M", [100, 128, 129])
 def test_wide_lm_head(M):
     """lm_head at up to 128 rows in one launch, more as a second launch: the

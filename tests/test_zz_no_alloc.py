@@ -97,10 +97,11 @@ def test_noalloc_unsplit_plan_and_graph_replay():
     ad, wd = a.to(DEV), w.to(DEV)
     out = torch.empty(M, N, dtype=BF16, device=DEV)
     stream = torch.cuda.Stream()
+    assert _lib.workspace_bytes(_lib.SK_OP_GEMM, M, N, K, SPLIT3) > 0
 
     def call():
         st = _lib.lib().sk_gemm_bf16_noalloc(ad.data_ptr(), ad.stride(0), wd.data_ptr(), wd.stride(0),
-                                             out.data_ptr(), out.stride(0), M, N, K, None,
+                                             out.data_ptr(), out.stride(0), M, N, K, _lib.cfg_ptr(SPLIT3),
                                              torch.cuda.current_stream().cuda_stream)
         assert st == SK_OK
 
@@ -116,10 +117,60 @@ def test_noalloc_unsplit_plan_and_graph_replay():
     for _ in range(3):
         out.zero_()
         # eager work between replays, also through the shared scratch (a smaller split call)
-        small = _noalloc(ad[:3], wd, None)
+        small = _noalloc(ad[:3], wd, SPLIT3)
         torch.cuda.synchronize()
-        assert torch.equal(small, _with_workspace(ad[:3], wd, None))
+        assert torch.equal(small, _with_workspace(ad[:3], wd, SPLIT3))
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
-    assert torch.equal(eager, _with_workspace(ad, wd, None))
+    assert torch.equal(eager, _with_workspace(ad, wd, SPLIT3))
+
+
+_FIRST_CALL_IN_CAPTURE = r'''
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from starter_amd import _lib
+from starter_amd._lib import SK_OK, SK_PATH_MFMA_LDS, SkConfig
+dev = "cuda:0"
+torch.cuda.set_device(0)
+M, N, K = 8, 2560, 9728
+cfg = SkConfig.make(SK_PATH_MFMA_LDS, waves=13, ku=8, rows=32, split=3)   # uses the scratch
+g = torch.Generator().manual_seed(5)
+a = (torch.randn(M, K, generator=g)).to(torch.bfloat16).to(dev)
+w = (0.02 * torch.randn(N, K, generator=g)).to(torch.bfloat16).to(dev)
+out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+L = _lib.lib()
+def noalloc():
+    return L.sk_gemm_bf16_noalloc(a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(),
+                                  out.stride(0), M, N, K, _lib.cfg_ptr(cfg), torch.cuda.current_stream().cuda_stream)
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    st = noalloc()      # the process's first call of the entry point
+assert st == SK_OK, _lib.strerror(st)
+ref = torch.empty_like(out)
+n = _lib.workspace_bytes(_lib.SK_OP_GEMM, M, N, K, cfg)
+ws = torch.zeros(n, dtype=torch.uint8, device=dev)
+assert L.sk_gemm_bf16(a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), ref.data_ptr(), ref.stride(0), M, N, K,
+                      _lib.cfg_ptr(cfg), ws.data_ptr(), n, torch.cuda.current_stream().cuda_stream) == SK_OK
+for i in range(3):
+    out.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {i}"
+print("first-call-in-capture ok", flush=True)
+'''
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """A fresh process whose first sk_gemm_bf16_noalloc call is made under
+    HIP graph capture: the scratch address is looked up there, and every
+    replay equals sk_gemm_bf16 with a workspace."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, root], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "first-call-in-capture ok" in r.stdout
