@@ -601,6 +601,89 @@ def verify_benchmark(plan, R: int = 8, parents=TREE8, replays: int = 20) -> dict
 _KEEP: list = []   # attention workloads stay allocated until the process ends (no device frees)
 
 
+def verify_recycle_benchmark(B: int = 16, R: int = 8, k: int = 8, chains: int = 8, reps: int = 7) -> dict:
+    """The reference's production verify chain at batch 16 (recycle mode,
+    engine/model.py:370-373, engine/recycle.py:164-184): the lm_head call
+    ``mm["lm"](x, y, w_norm, xout, w)`` producing the full logits of the
+    M = B x R verify rows ([128, 151936] bf16: add + RMSNorm, then the logits
+    GEMM, sk_gemm_bf16), then ``fast_topk(logits, k)`` (sk_topk_bf16).  A graph of
+    ``chains`` chains over two rotating lm_head weight copies (1.56 GB, beyond
+    the 256 MB Infinity Cache); HIP events on the replay stream, median of
+    ``reps`` replays.  The logits GEMM and the top-k are also timed alone, and
+    the library's logits GEMM (torch.mm on hipBLASLt) beside them."""
+    import statistics
+
+    import torch
+
+    from starter_amd import kernels as K
+    from starter_amd._lib import SK_OP_RMSNORM_GEMM
+
+    dev = "cuda:0"
+    M, H, V = B * R, 2560, 151936
+    g = torch.Generator(device=dev).manual_seed(21)
+    ws_ = [torch.empty(V, H, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=g) for _ in range(2)]
+    x = torch.empty(M, H, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    y = torch.empty(M, H, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    wn = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    xout = torch.empty_like(x)
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    lib_logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    n = K._lib.workspace_bytes(SK_OP_RMSNORM_GEMM, M, V, H)
+    ws = torch.zeros(max(n, 1), dtype=torch.uint8, device=dev)
+    _KEEP.extend([ws_, x, y, wn, xout, logits, lib_logits, ws])
+    res: dict = {}
+
+    def chain(i):
+        K.rmsnorm_gemm(x, y, wn, 1e-6, xout, ws_[i % 2], out=logits, ws=ws)
+        res["topk"] = K.fast_topk(logits, k)
+
+    def logits_only(i):
+        K.rmsnorm_gemm(x, y, wn, 1e-6, xout, ws_[i % 2], out=logits, ws=ws)
+
+    def topk_only(i):
+        K.fast_topk(logits, k)
+
+    def library(i):
+        torch.mm(x, ws_[i % 2].t(), out=lib_logits)
+
+    def time_us(fn, n_calls):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn(0)
+            fn(1)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n_calls):
+                fn(i)
+        graph.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / n_calls)
+        _KEEP.append(graph)
+        return statistics.median(ts)
+
+    chain_us = time_us(chain, chains)
+    logits_us = time_us(logits_only, chains)
+    topk_us = time_us(topk_only, 4 * chains)
+    lib_us = time_us(library, chains)
+    log(f"verify recycle chain (M={M}): {chain_us:.1f} us per chain; logits {logits_us:.1f} us "
+        f"(hipBLASLt GEMM alone {lib_us:.1f} us), top-{k} {topk_us:.1f} us")
+    return {"M": M, "B": B, "R": R, "k": k, "us_per_chain": round(chain_us, 2), "logits_us": round(logits_us, 2),
+            "topk_us": round(topk_us, 2), "hipblaslt_logits_us": round(lib_us, 2),
+            "logits_GB/s": round((V * H * 2 + M * H * 2 + M * V * 2) / (logits_us * 1e-6) / 1e9, 1),
+            "workload": f"mm['lm'] (add + RMSNorm + logits GEMM [{M}, {H}] x [{V}, {H}]) then fast_topk k={k}, "
+                        f"two rotating weight copies"}
+
+
 ATTN_POS = 1088
 
 
@@ -693,6 +776,8 @@ def main() -> int:
                     help="C5: greedy decode steps timed after a B=16, T=1024 prefill (0 skips it)")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the decode-attention measurement and print its JSON object")
+    ap.add_argument("--recycle-only", action="store_true",
+                    help="run only the verify recycle-chain measurement (logits at M = 128 + top-k)")
     ap.add_argument("--decode-only", action="store_true",
                     help="run only the C5 decode measurement and print its JSON object")
     ap.add_argument("--probe", action="store_true",
@@ -738,6 +823,9 @@ def main() -> int:
     if args.decode_only:
         print(json.dumps({"decode": decode_benchmark(max(1, args.decode_steps))}), flush=True)
         return 0
+    if args.recycle_only:
+        print(json.dumps({"verify_recycle": verify_recycle_benchmark()}), flush=True)
+        return 0
     log(f"device {torch.cuda.get_device_name(0)}; building workload (36 layers of weights)")
     wl = Workload(args.layers, args.M)
 
@@ -754,9 +842,11 @@ def main() -> int:
     g.replay()   # untimed replay of the captured graph (first-touch of its pool)
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
-    ms = min(wl.time_graph(g, 3))   # best of three replays of the K-step graph
+    times = wl.time_graph(g, 5)   # five replays of the K-step graph: the median is the value
+    ms = statistics.median(times)
     ms_per_step = ms / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    value_best = step_bytes / (min(times) / args.steps * 1e-3) / 1e9
     del g
 
     # Per-kernel timing: the dominant kernel of the step (gate_up) and the
@@ -814,6 +904,7 @@ def main() -> int:
     # attention before the decode measurement, whose model and caches (~11 GB)
     # leave the process in a state where the isolated launch reads ~1 us slower
     attention = attention_benchmark()
+    recycle = verify_recycle_benchmark()
     decode = None
     if args.decode_steps > 0:
         decode = decode_benchmark(args.decode_steps)
@@ -840,6 +931,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations)",
+        "value_best_of_5": round(value_best, 1),
         "config": {"workload": "qwen3-4b decoder-layer decode GEMMs: qkv 6144x2560, o_proj 2560x4096, "
                                "gate_up 19456x2560+swiglu, down 2560x9728",
                    "M": args.M, "layers_rotated": args.layers, "step_bytes": step_bytes,
@@ -848,6 +940,7 @@ def main() -> int:
         "roofline": roofline,
         "decode": decode,
         "attention": attention,
+        "verify_recycle": recycle,
         "cpu_baseline": cpu,
         "cpu_port": port,
         "cpu_config1": cpu1,

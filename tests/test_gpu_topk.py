@@ -16,8 +16,8 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-@pytest.mark.parametrize("N,V,k", [(16, 151936, 8), (64, 151936, 4), (3, 1000, 8), (5, 2048, 1), (2, 7, 7),
-                                   (4, 151935, 16)])
+@pytest.mark.parametrize("N,V,k", [(16, 151936, 8), (64, 151936, 4), (128, 151936, 8), (3, 1000, 8), (5, 2048, 1),
+                                   (2, 7, 7), (4, 151935, 16)])
 def test_topk_matches_oracle(N, V, k):
     g = torch.Generator().manual_seed(N * V + k)
     L = randn_bf16((N, V), 2.0, g)
