@@ -9,10 +9,17 @@
 // Rank 0 is the exact argmax with torch's lowest-index tie rule; ranks >= 1
 // miss a true top-k value only when two of them share a lane.
 //
-// MI355X mapping: one workgroup of 256 threads per row; thread t owns lanes
-// 8t .. 8t+7, so one 16-byte load per thread reads 1 KiB contiguous per wave
-// (4 KiB per workgroup and sweep step).  The final selection is K rounds of a
-// workgroup (max value, min column) reduction through LDS.
+// MI355X mapping: one workgroup of 1024 threads per row, four sweep groups of
+// 256.  Thread t of a group owns lanes 8t .. 8t+7, so one 16-byte load per
+// thread reads 1 KiB contiguous per wave; group g takes the sweep steps
+// g, g + 4, g + 8, ... and issues up to 20 of them before using any, so a
+// row of the Qwen3 vocabulary (75 steps, 297 KiB) is requested in one round.  A group keeps, per
+// lane, the largest value of its steps and the first column holding it; the
+// four groups are merged per lane (larger value, then lower column), which is
+// the single sweep's result: within a lane a later column replaces only a
+// strictly larger value, i.e. the first occurrence of the lane maximum wins.
+// The final selection is K rounds of a one-wave (max value, min column)
+// reduction over the merged lane maxima.
 #include "starter_amd.h"
 
 #include <hip/hip_runtime.h>
@@ -24,16 +31,19 @@
 namespace sk {
 
 constexpr int TOPK_LANES = 2048;   // the reference's BLOCK
-constexpr int TOPK_THREADS = 256;
+constexpr int TOPK_THREADS = 256;  // one sweep group
+constexpr int TOPK_GROUPS = 4;     // sweep groups per row
+constexpr int TOPK_UNROLL = 20;    // sweep steps a thread requests together
 constexpr int TOPK_PER_THREAD = TOPK_LANES / TOPK_THREADS;   // 8 lanes per thread
 constexpr int TOPK_MAX_K = 64;
 
-__global__ void __launch_bounds__(TOPK_THREADS) topk_kernel(const uint16_t* __restrict__ L, int64_t ld, int V,
-                                                             int K, int vec, float* __restrict__ vals,
-                                                             int32_t* __restrict__ idxs) {
-  __shared__ float s_v[TOPK_THREADS / 64];
-  __shared__ int s_i[TOPK_THREADS / 64];
-  const int row = blockIdx.x, t = threadIdx.x;
+__global__ void __launch_bounds__(TOPK_THREADS * TOPK_GROUPS)
+topk_kernel(const uint16_t* __restrict__ L, int64_t ld, int V, int K, int vec, float* __restrict__ vals,
+            int32_t* __restrict__ idxs) {
+  __shared__ float s_gv[TOPK_GROUPS - 1][TOPK_LANES];   // lane maxima of groups 1..3
+  __shared__ int s_gi[TOPK_GROUPS - 1][TOPK_LANES];
+  const int row = blockIdx.x;
+  const int t = threadIdx.x % TOPK_THREADS, grp = threadIdx.x / TOPK_THREADS;
   const uint16_t* x = L + (int64_t)row * ld;
   float best[TOPK_PER_THREAD];
   int bidx[TOPK_PER_THREAD];
@@ -43,39 +53,106 @@ __global__ void __launch_bounds__(TOPK_THREADS) topk_kernel(const uint16_t* __re
     bidx[e] = 0;
   }
   const int lane0 = TOPK_PER_THREAD * t;
-  for (int start = 0; start < V; start += TOPK_LANES) {
-    const int c0 = start + lane0;
-    float v[TOPK_PER_THREAD];
-    if (vec && c0 + TOPK_PER_THREAD <= V) {
-      const u32x4 w = ld16(x + c0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        v[2 * q] = bf2f(w[q] & 0xFFFFu);
-        v[2 * q + 1] = bf2f(w[q] >> 16);
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < TOPK_PER_THREAD; ++e) v[e] = c0 + e < V ? bf2f(x[c0 + e]) : -INFINITY;
+  const int nsteps = (V + TOPK_LANES - 1) / TOPK_LANES;
+  // one lane's update with the value at column c (strictly larger replaces)
+  auto take = [&](int e, float v, int c) {
+    if (v > best[e]) {
+      best[e] = v;
+      bidx[e] = c;
     }
+  };
+  if (vec) {
+    // Aligned rows: up to TOPK_UNROLL of this group's steps are requested at
+    // once (a row of the Qwen3 vocabulary, 75 steps, in one round), then
+    // used in column order.  A step past the row, or the partial last step,
+    // reads nothing here and is handled below.
+    const int full = V / TOPK_LANES;   // steps whose 2048 columns all exist
+    for (int s0 = grp; s0 < full; s0 += TOPK_GROUPS * TOPK_UNROLL) {
+      u32x4 raw[TOPK_UNROLL];
 #pragma unroll
-    for (int e = 0; e < TOPK_PER_THREAD; ++e) {
-      if (v[e] > best[e]) {   // strict: the first occurrence of a value keeps its lane
-        best[e] = v[e];
-        bidx[e] = c0 + e;
+      for (int u = 0; u < TOPK_UNROLL; ++u) {
+        const int st = s0 + u * TOPK_GROUPS;
+        raw[u] = st < full ? ld16(x + st * TOPK_LANES + lane0) : u32x4{0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u, 0xFF80FF80u};
       }
+#pragma unroll
+      for (int u = 0; u < TOPK_UNROLL; ++u) {
+        const int c0 = (s0 + u * TOPK_GROUPS) * TOPK_LANES + lane0;   // -inf padding never replaces
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          take(2 * q, bf2f(raw[u][q] & 0xFFFFu), c0 + 2 * q);
+          take(2 * q + 1, bf2f(raw[u][q] >> 16), c0 + 2 * q + 1);
+        }
+      }
+    }
+    if (full < nsteps && full % TOPK_GROUPS == grp) {   // the partial last step, element by element
+      const int c0 = full * TOPK_LANES + lane0;
+#pragma unroll
+      for (int e = 0; e < TOPK_PER_THREAD; ++e)
+        if (c0 + e < V) take(e, bf2f(x[c0 + e]), c0 + e);
+    }
+  } else {
+    for (int st = grp; st < nsteps; st += TOPK_GROUPS) {
+      const int c0 = st * TOPK_LANES + lane0;
+#pragma unroll
+      for (int e = 0; e < TOPK_PER_THREAD; ++e)
+        if (c0 + e < V) take(e, bf2f(x[c0 + e]), c0 + e);
     }
   }
-  const int lane = t & 63, wave = t >> 6;
+  // Merge the groups' lane maxima into group 0: larger value, then the lower
+  // column (a lane with no value above -inf keeps column 0 in every group).
+  if (grp > 0) {
+#pragma unroll
+    for (int e = 0; e < TOPK_PER_THREAD; ++e) {
+      s_gv[grp - 1][lane0 + e] = best[e];
+      s_gi[grp - 1][lane0 + e] = bidx[e];
+    }
+  }
+  __syncthreads();
+  if (grp == 0) {
+#pragma unroll
+    for (int g = 0; g < TOPK_GROUPS - 1; ++g)
+#pragma unroll
+      for (int e = 0; e < TOPK_PER_THREAD; ++e) {
+        const float ov = s_gv[g][lane0 + e];
+        const int oi = s_gi[g][lane0 + e];
+        if (ov > best[e] || (ov == best[e] && oi < bidx[e])) {
+          best[e] = ov;
+          bidx[e] = oi;
+        }
+      }
+  }
+  // Selection by one wave, without workgroup barriers: the 2048 lane maxima go
+  // to LDS, lane l of wave 0 takes lanes l, l + 64, ..., and each round is a
+  // wave (max value, min column) reduction followed by removing the chosen
+  // column's lane (every entry holding that column: a lane that saw no value
+  // above -inf keeps column 0).
+  __syncthreads();   // group 0 has read the other groups' maxima
+  if (grp == 0) {
+#pragma unroll
+    for (int e = 0; e < TOPK_PER_THREAD; ++e) {
+      s_gv[0][lane0 + e] = best[e];
+      s_gi[0][lane0 + e] = bidx[e];
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x >= 64) return;   // no barrier follows
+  constexpr int PER = TOPK_LANES / 64;
+  const int lane = threadIdx.x;
+  float bv[PER];
+  int bi[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    bv[i] = s_gv[0][lane + 64 * i];
+    bi[i] = s_gi[0][lane + 64 * i];
+  }
   for (int k = 0; k < K; ++k) {
-    // Thread candidate: max value, lowest column among its lanes holding it.
     float m = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < TOPK_PER_THREAD; ++e) m = fmaxf(m, best[e]);
+    for (int i = 0; i < PER; ++i) m = fmaxf(m, bv[i]);
     int ci = 0x7FFFFFFF;
 #pragma unroll
-    for (int e = 0; e < TOPK_PER_THREAD; ++e)
-      if (best[e] == m && bidx[e] < ci) ci = bidx[e];
-    // Wave, then workgroup: larger value wins, then the lower column.
+    for (int i = 0; i < PER; ++i)
+      if (bv[i] == m && bi[i] < ci) ci = bi[i];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
       const float om = __shfl_xor(m, off);
@@ -86,26 +163,12 @@ __global__ void __launch_bounds__(TOPK_THREADS) topk_kernel(const uint16_t* __re
       }
     }
     if (lane == 0) {
-      s_v[wave] = m;
-      s_i[wave] = ci;
-    }
-    __syncthreads();
-    float M = s_v[0];
-    int I = s_i[0];
-#pragma unroll
-    for (int w = 1; w < TOPK_THREADS / 64; ++w)
-      if (s_v[w] > M || (s_v[w] == M && s_i[w] < I)) {
-        M = s_v[w];
-        I = s_i[w];
-      }
-    __syncthreads();   // s_v / s_i are rewritten by the next round
-    if (t == 0) {
-      vals[(int64_t)row * K + k] = M;
-      idxs[(int64_t)row * K + k] = I;
+      vals[(int64_t)row * K + k] = m;
+      idxs[(int64_t)row * K + k] = ci;
     }
 #pragma unroll
-    for (int e = 0; e < TOPK_PER_THREAD; ++e)
-      if (bidx[e] == I) best[e] = -INFINITY;
+    for (int i = 0; i < PER; ++i)
+      if (bi[i] == ci) bv[i] = -INFINITY;
   }
 }
 
@@ -122,6 +185,6 @@ extern "C" int sk_topk_bf16(const sk_bf16* L, int64_t ld, int N, int V, int K, f
       strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return SK_ERR_DEVICE;
   const int vec = ((reinterpret_cast<uintptr_t>(L) & 15u) == 0 && (ld & 7) == 0) ? 1 : 0;
-  sk::topk_kernel<<<dim3((unsigned)N), dim3(sk::TOPK_THREADS), 0, stream>>>(L, ld, V, K, vec, vals, idxs);
+  sk::topk_kernel<<<dim3((unsigned)N), dim3(sk::TOPK_THREADS * sk::TOPK_GROUPS), 0, stream>>>(L, ld, V, K, vec, vals, idxs);
   return hipGetLastError() == hipSuccess ? SK_OK : SK_ERR_LAUNCH;
 }
