@@ -348,12 +348,13 @@ PROBE_LAUNCHES = 24
 PROBE_COPY_BYTES = 512 << 20
 
 
-def probe(M: int, name: str = "gate_up") -> int:
+def probe(M: int, name: str = "gate_up", config: str | None = None) -> int:
     """Untimed launches for the hardware-counter passes: PROBE_LAUNCHES
     launches of one projection (default gate_up+SwiGLU) at M rows over rotating
     weights (12 layers, or the two lm_head copies: no launch finds its weights
     in the MALL), then three copies of PROBE_COPY_BYTES with torch's copy
-    kernel as the calibration of known size."""
+    kernel as the calibration of known size.  ``config`` ("path,waves,ku,rows,
+    split,grid,groups") replaces the projection's default configuration."""
     import torch
 
     if name == "attention":   # the decode step's fused rope + attention launch (B = 16, position 1088)
@@ -361,6 +362,14 @@ def probe(M: int, name: str = "gate_up") -> int:
         attention_benchmark(launches=PROBE_LAUNCHES, timed=False)
     else:
         wl = Workload(12, M)
+        if config:
+            from starter_amd import kernels as Kn
+            from starter_amd._lib import SkConfig
+
+            mm = wl.mm[name]
+            mm.config = SkConfig.make(*[int(v) for v in config.split(",")])
+            mm.ws = Kn._workspace(mm.op, M, mm.N, mm.K, mm.config, wl.dev)
+            log(f"probe: {name} at M={M} with {mm.config}")
         nl = 2 if name == "lm_head" else wl.L
         wl.launch(name, 0)
         torch.cuda.synchronize()
@@ -477,6 +486,7 @@ def counters_summary(folder: str) -> int:
 
     for pr in probes:
         op, m = pr.rsplit("_m", 1)
+        m, _, tag = m.partition("-")   # <op>_m<M>[-<tag>]: a probe of an explicit configuration
         M = int(m)
         sets = {x: _dispatches(root / f"{pr}_{x}", "counter_collection.csv") for x in "ABCD"}
         lib = {x: [r for r in rs if "sk::" in r["_name"]][1:] for x, rs in sets.items()}
@@ -495,7 +505,7 @@ def counters_summary(folder: str) -> int:
         waves = med(A, "SQ_WAVES")
         name = A[0]["_name"].replace("void ", "").split("(")[0]
         hits, miss = med(D, "TCC_HIT_sum"), med(D, "TCC_MISS_sum")
-        print(f"| {op} | {M if op != 'attention' else 16} | `{name}` | {A[0]['_grid']} x {A[0]['_wg']} | {us:.2f} "
+        print(f"| {op}{f' ({tag})' if tag else ''} | {M if op != 'attention' else 16} | `{name}` | {A[0]['_grid']} x {A[0]['_wg']} | {us:.2f} "
               f"| {100 * alg / us / 1e3 / PEAK_HBM_GBS:.1f} "
               f"| {flops / us / 1e6:.1f} ({100 * flops / us / 1e6 / PEAK_BF16_TFLOPS:.2f}) "
               f"| {100 * med(B, 'SQ_VALU_MFMA_BUSY_CYCLES') / (cycles * MI355X_SIMDS):.2f} "
@@ -784,6 +794,8 @@ def main() -> int:
                     help="launch --probe-op at --M (untimed) and a 512 MiB copy, for rocprofv3 --pmc passes")
     ap.add_argument("--probe-op", default="gate_up", choices=list(SHAPES) + ["attention"],
                     help="the projection --probe launches (default gate_up)")
+    ap.add_argument("--probe-config", metavar="P,W,KU,ROWS,SPLIT,GRID,GROUPS",
+                    help="with --probe: launch this configuration instead of the default one")
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders of --probe (FETCH_SIZE, WRITE_SIZE) into "
                          "profiles/traffic_<probe-op>_m<M>.json and exit")
@@ -816,7 +828,7 @@ def main() -> int:
         return 1
     torch.cuda.set_device(0)
     if args.probe:
-        return probe(args.M, args.probe_op)
+        return probe(args.M, args.probe_op, args.probe_config)
     if args.attention_only:
         print(json.dumps({"attention": attention_benchmark()}), flush=True)
         return 0

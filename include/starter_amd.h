@@ -76,7 +76,8 @@ typedef enum sk_path {
   SK_PATH_AUTO = 0,
   SK_PATH_MFMA = 1,       /* v_mfma_f32_16x16x32_bf16 tiles, 16 weight rows per wave tile */
   SK_PATH_GEMV = 2,       /* VALU v_dot2_f32_bf16, lanes span K, DPP/shuffle lane reduction */
-  SK_PATH_MFMA_LDS = 3    /* MFMA fed from LDS: weight rows loaded 1 KiB-contiguous, transposed in LDS */
+  SK_PATH_MFMA_LDS = 3,   /* MFMA fed from LDS: weight rows loaded 1 KiB-contiguous, transposed in LDS */
+  SK_PATH_WIDE = 4        /* up to 128 rows per workgroup: weight tile staged once in LDS for all rows */
 } sk_path;
 
 /*
@@ -88,7 +89,8 @@ typedef enum sk_path {
  *   path   : SK_PATH_MFMA, SK_PATH_MFMA_LDS or SK_PATH_GEMV
  *   waves  : wavefronts per workgroup; they split the workgroup's K slice and
  *            their fp32 partials are summed in LDS in fixed wave order
- *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns;
+ *   ku     : K units per wave (MFMA: 32 columns; GEMV: 512 columns; WIDE: 8,
+ *            every wave walks its slice in 256-column steps;
  *            MFMA_LDS: 8, 16, 32 or 40, i.e. 256, 512, 1024 or 1280 columns
  *            per wave; all but 512 stream 256-column chunks through an
  *            8-load ring)
@@ -97,7 +99,8 @@ typedef enum sk_path {
  *            1..48 gate rows and as many up rows, loaded as 16-row slabs
  *            whose rows past the tile are not read, so a height of N / 256
  *            gives every CU one tile; the whole-tile body (ku 16) and the
- *            residual hand-off ops take 16 or 32, gate/up 16)
+ *            residual hand-off ops take 16 or 32, gate/up 16; SK_PATH_WIDE:
+ *            1..96 rows, gate/up 1..48, with WN = 2 gate/up 1..32)
  *   split  : global K splits; >1 writes fp32 partials to the workspace and
  *            the last workgroup to finish a tile sums them in fixed split
  *            order (no floating-point atomics, no second kernel)
@@ -112,6 +115,10 @@ typedef enum sk_path {
  *            serves the later groups' reads.  Every group must hold a row.
  *            For M where one group of all rows would need more registers per
  *            wave than a ten-wave workgroup allows (M > 48 at K = 2560).
+ *            SK_PATH_WIDE reads it as WN, the groups its waves form along
+ *            the tile's weight slabs: 1 (every wave multiplies the whole
+ *            tile for its activation tiles) or 2 (eight waves: two groups of
+ *            slabs x four groups of activation tiles).
  *
  * Rows per launch: at most 64 without row groups; with a configuration that
  * splits them into groups (compiled for groups of up to 32 rows), up to 128

@@ -43,6 +43,7 @@ SK_PATH_AUTO = 0
 SK_PATH_MFMA = 1
 SK_PATH_GEMV = 2
 SK_PATH_MFMA_LDS = 3
+SK_PATH_WIDE = 4
 
 # Every symbol include/starter_amd.h declares (checked by the CPU tests).
 EXPORTS = (

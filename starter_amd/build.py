@@ -48,6 +48,7 @@ def _units() -> list[tuple[Path, list[str], Path]]:
         units.append((CSRC / "sk_inst_mfma.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfma_{epi}.o"))
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
         units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
+        units.append((CSRC / "sk_inst_wide.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_wide_{epi}.o"))
     for epi in NORM_EPIS:
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
     for epi in HANDOFF_EPIS:

@@ -165,6 +165,8 @@ size_t plan_lds(const Plan& pl, int M, int tiles_per) {
 // that instance is not built).
 sk::KernelFn plan_kernel(const Plan& pl) {
   if (pl.cfg.path == SK_PATH_MFMA) return sk::mfma_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku);
+  if (pl.cfg.path == SK_PATH_WIDE)
+    return sk::wide_kernel_for(pl.epi, pl.cfg.waves, pl.cfg.groups > 1 ? pl.cfg.groups : 1, pl.tn);
   if (pl.cfg.path == SK_PATH_MFMA_LDS)
     return pl.groups > 1 ? sk::mfmt_grouped_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku)
                          : sk::mfmt_kernel_for(pl.epi, pl.tm, pl.tn, pl.tku);
@@ -196,7 +198,9 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   // Row groups: ring path (no norm prologue), an explicit grid that keeps
   // sibling workgroups on one XCD, and a row in every group; the rest of the
   // plan is that of one group.
-  const int groups = c.groups > 1 ? c.groups : 1;
+  // (the wide path reads `groups` as the wave groups along the tile's weight
+  // slabs, not as row groups)
+  const int groups = c.groups > 1 && c.path != SK_PATH_WIDE ? c.groups : 1;
   if (groups > 1) {
     if (fused || c.path != SK_PATH_MFMA_LDS || (c.ku != 8 && c.ku != 32)) return SK_ERR_CONFIG;
     if (c.grid <= 0 || (c.grid % 8) != 0) return SK_ERR_CONFIG;
@@ -204,7 +208,9 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     if ((groups - 1) * mrows >= M) return SK_ERR_CONFIG;
     M = mrows;
   }
-  if (M > kMaxM) return SK_ERR_SHAPE;   // more rows than an instance holds: chunked, or row groups
+  // more rows than an instance holds: chunked, or row groups (the wide path
+  // holds up to kMaxLaunchM rows in one workgroup)
+  if (M > (c.path == SK_PATH_WIDE && groups == 1 ? kMaxLaunchM : kMaxM)) return SK_ERR_SHAPE;
   pl->groups = groups;
   pl->mrows = M;
   const bool gateup = (op == SK_OP_GATEUP);
@@ -253,6 +259,25 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     partial_rows = 16 * pl->tn;
     if (c.waves > sk::instance_waves(sk::KIND_MFMT, pl->tm, pl->tn, KW, pl->epi)) return SK_ERR_CONFIG;
     pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
+  } else if (c.path == SK_PATH_WIDE) {
+    // All rows in one workgroup: W = 4 or 8 waves split the (up to 8)
+    // 16-row activation tiles, every wave multiplies the whole weight tile
+    // of `rows` rows (gate/up: rows gate + rows up), staged in LDS in
+    // 256-column steps (ku = 8).
+    // `groups` (1 or 2) = WN, the wave groups along the tile's slabs.
+    const int wn = c.groups > 1 ? c.groups : 1;
+    if (variant != 0 || wn > 2 || (wn == 2 && c.waves != 8)) return SK_ERR_CONFIG;
+    if ((c.waves != 4 && c.waves != 8) || c.ku != 8) return SK_ERR_CONFIG;
+    if (c.rows < 1 || c.rows > (gateup ? (wn == 2 ? 32 : 48) : 96)) return SK_ERR_CONFIG;
+    units = cdiv(K, sk::kWideChunk);
+    pl->tm = cdiv(M, 16);
+    const int half = cdiv(c.rows, 16);                    // slabs per half (gate/up) or per tile
+    const int hw = cdiv(half, wn) * wn;                   // rounded to whole slabs per wave group
+    pl->tn = gateup ? 2 * hw : hw;
+    if (pl->tn < 2) pl->tn = 2;   // the smallest instance stages two slabs
+    pl->tku = sk::kWideChunk;
+    partial_rows = 0;
+    pl->pre_lds = sk::wide_weight_lds(pl->tn);
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
     if (M > 8) return SK_ERR_CONFIG;
@@ -271,23 +296,29 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   if (!plan_kernel(*pl)) return SK_ERR_CONFIG;
   pl->slice_units = cdiv(units, c.split);
   const long per_wave = c.path == SK_PATH_MFMA_LDS ? 1 : c.ku;
-  if ((long)c.waves * per_wave < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
+  // (the wide path's waves all walk the whole slice)
+  if (c.path != SK_PATH_WIDE && (long)c.waves * per_wave < pl->slice_units) return SK_ERR_CONFIG;   // K slice not covered
   if (c.split > 1 && (c.split - 1) * pl->slice_units >= units) return SK_ERR_CONFIG;  // empty split
-  const int out_rows = c.path == SK_PATH_MFMA       ? (gateup ? 16 : c.rows)
-                       : c.path == SK_PATH_MFMA_LDS ? (gateup ? 8 * pl->tn : 16 * pl->tn)
-                                                    : c.rows;
+  const bool lds_fed = c.path == SK_PATH_MFMA_LDS || c.path == SK_PATH_WIDE;
+  const int out_rows = c.path == SK_PATH_MFMA ? (gateup ? 16 : c.rows)
+                       : lds_fed             ? (gateup ? 8 * pl->tn : 16 * pl->tn)
+                                             : c.rows;
   pl->out_rows = out_rows;
-  pl->tr = c.path == SK_PATH_MFMA_LDS ? c.rows : out_rows;
+  pl->tr = lds_fed ? c.rows : out_rows;
   pl->nrb = cdiv(N, pl->tr);
   if (c.path == SK_PATH_MFMA_LDS) partial_rows = sk::lds_part_stride(pl->tm, pl->tn, pl->tku);
   pl->parts_lds = (size_t)2 * c.waves * M * partial_rows * sizeof(float);
   pl->stage_elem = stage_bytes(pl->epi) * (size_t)M * out_rows;
+  if (c.path == SK_PATH_WIDE) {   // outputs go straight from registers; the split-K finish's flags
+    pl->parts_lds = (size_t)64 * c.waves * sizeof(int);
+    pl->stage_elem = 0;
+  }
   if (c.grid > 0 && (c.grid % c.split) != 0) return SK_ERR_CONFIG;
   const int tiles_per = c.grid > 0 ? cdiv(pl->nrb, c.grid / c.split) : 1;
   pl->lds = plan_lds(*pl, M, tiles_per);
   // The ring path can work with one partial tile buffer (one more barrier per
   // tile) where two would not fit.
-  const bool ring = c.path == SK_PATH_MFMA_LDS && pl->tku != 512;
+  const bool ring = c.path == SK_PATH_MFMA_LDS && pl->tku != 512;   // (not the wide path)
   if (ring && (pl->lds > kMaxLds || (c.grid == 0 && plan_lds(*pl, M, cdiv(pl->nrb, kMaxGrid)) > kMaxLds))) {
     pl->pbuf = 1;
     pl->parts_lds /= 2;
@@ -424,7 +455,10 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
-    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // lm_head  ~290-310 us (four row groups; 362 as two 64-row launches)
+    // lm_head + argmax at 65-128 rows: the wide path, every row in one
+    // workgroup of eight waves over 96-row weight tiles (291-295 us at 128
+    // rows against 306-309 for four row groups; 362 as two 64-row launches)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 96, 1, 0, 0}},
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer, as for qkv
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
@@ -543,7 +577,8 @@ int default_config(int op, int M, int N, int K, int num_cu, sk_config* out) {
     const int Ml = M < kMaxLaunchM ? M : kMaxLaunchM;
     const int bo = base_op(op);
     if (const Tuned* t = tuned_lookup(bo, Ml, N, K, bo == SK_OP_GEMM ? SK_OP_LM_ARGMAX : -1)) {
-      if (t->cfg.groups > 1 && t->M > kMaxM && plan_shape(op, Ml, N, K, t->cfg, &pl) == SK_OK) {
+      if ((t->cfg.groups > 1 || t->cfg.path == SK_PATH_WIDE) && t->M > kMaxM &&
+          plan_shape(op, Ml, N, K, t->cfg, &pl) == SK_OK) {
         *out = t->cfg;
         return SK_OK;
       }
@@ -697,7 +732,8 @@ int launch_rows(int op, int M, int N, int K, const sk_config* cfg) {
   const int R = M < kMaxLaunchM ? M : kMaxLaunchM;
   sk_config c;
   Plan pl;
-  if (resolve_config(op, R, N, K, cfg, &c) == SK_OK && c.groups > 1 && plan_shape(op, R, N, K, c, &pl) == SK_OK)
+  if (resolve_config(op, R, N, K, cfg, &c) == SK_OK && (c.groups > 1 || c.path == SK_PATH_WIDE) &&
+      plan_shape(op, R, N, K, c, &pl) == SK_OK)
     return kMaxLaunchM;
   return kMaxM;
 }
@@ -717,7 +753,7 @@ int plan_call(int op, int M, int N, int K, const sk_config* cfg, CallPlan* cp) {
     // 128-row launches, e.g. one row of 129) runs with as many groups as
     // hold a row, so the configuration default_config returns for the whole
     // call is accepted for every launch.
-    if (cp->nplans == 2 && i == 1 && c.groups > 1) {
+    if (cp->nplans == 2 && i == 1 && c.groups > 1 && c.path != SK_PATH_WIDE) {
       const int rows = cp->chunk_rows[i];
       int g = c.groups;
       while (g > 1 && (g - 1) * cdiv(rows, g) >= rows) --g;

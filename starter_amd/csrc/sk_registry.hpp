@@ -10,6 +10,7 @@
 #pragma once
 
 #include "sk_kernels.hpp"
+#include "sk_wide.hpp"
 
 namespace sk {
 
@@ -104,6 +105,11 @@ KernelFn mfmt_grouped_for_epi9(int MT, int NT, int KW);
 KernelFn mfmt_grouped_for_epi10(int MT, int NT, int KW);
 KernelFn mfmt_grouped_for_epi11(int MT, int NT, int KW);
 KernelFn mfmt_grouped_for_epi12(int MT, int NT, int KW);
+KernelFn wide_for_epi0(int W, int WN, int NT);
+KernelFn wide_for_epi1(int W, int WN, int NT);
+KernelFn wide_for_epi2(int W, int WN, int NT);
+KernelFn wide_for_epi3(int W, int WN, int NT);
+KernelFn wide_for_epi4(int W, int WN, int NT);
 KernelFn gemv_for_epi0(int MR, int R, int KU);
 KernelFn gemv_for_epi1(int MR, int R, int KU);
 KernelFn gemv_for_epi2(int MR, int R, int KU);
@@ -153,6 +159,19 @@ inline KernelFn mfmt_grouped_kernel_for(int epi, int MT, int NT, int KW) {
     case EPI_ARGMAX_PRE: return mfmt_grouped_for_epi10(MT, NT, KW);
     case EPI_STORE_RESID: return mfmt_grouped_for_epi11(MT, NT, KW);
     case EPI_PART_RESID: return mfmt_grouped_for_epi12(MT, NT, KW);
+  }
+  return nullptr;
+}
+
+// Wide-M instances: W waves (4 or 8) in WN groups along the tile's weight
+// slabs, NT 16-row weight slabs per tile.
+inline KernelFn wide_kernel_for(int epi, int W, int WN, int NT) {
+  switch (epi) {
+    case EPI_STORE: return wide_for_epi0(W, WN, NT);
+    case EPI_SWIGLU: return wide_for_epi1(W, WN, NT);
+    case EPI_ARGMAX: return wide_for_epi2(W, WN, NT);
+    case EPI_PART: return wide_for_epi3(W, WN, NT);
+    case EPI_PART_GU: return wide_for_epi4(W, WN, NT);
   }
   return nullptr;
 }

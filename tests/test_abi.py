@@ -59,12 +59,15 @@ def test_default_config_is_valid_for_every_decode_shape(name, M):
         assert cfg.waves * cfg.ku * cfg.split >= K // 32
     elif cfg.path == SK_PATH_GEMV:
         assert cfg.waves * cfg.ku * cfg.split >= -(-K // 512)
+    elif cfg.path == _lib.SK_PATH_WIDE:
+        assert cfg.ku == 8 and cfg.waves in (4, 8)   # every wave walks the whole K slice
     else:
         assert cfg.path == SK_PATH_MFMA_LDS
         assert cfg.waves * cfg.split >= -(-K // (32 * cfg.ku))
     ws = _lib.workspace_bytes(op, M, N, K, cfg)
     # row groups: counters and partials per group of ceil(M / groups) rows
-    g = max(cfg.groups, 1)
+    # (the wide path's `groups` are wave groups, not row groups)
+    g = max(cfg.groups, 1) if cfg.path != _lib.SK_PATH_WIDE else 1
     if op == SK_OP_LM_ARGMAX:
         assert ws == _tickets(g) + 8 * M
     elif cfg.split == 1:
@@ -242,13 +245,18 @@ def test_row_groups_planning():
 def test_wide_calls_plan_one_launch_of_row_groups():
     """Up to 128 rows run as one launch when the configuration splits them
     into row groups of at most 64 (the tuned entries do, for every Qwen3-4B
-    projection); more rows run as 128-row launches plus the remainder.  An
-    ungrouped configuration keeps 64-row launches."""
+    projection but lm_head + argmax) or runs them on the wide path (lm_head +
+    argmax: every row in one workgroup); more rows run as 128-row launches
+    plus the remainder.  An ungrouped configuration keeps 64-row launches."""
     for name in ("qkv", "o", "gu", "d", "lm_argmax", "lm"):
         op, N, K = QWEN[name]
         for M in (65, 100, 128):
             cfg = _lib.default_config(op, M, N, K)
-            assert cfg.groups > 1 and -(-M // cfg.groups) <= 32, (name, M, cfg)
+            if name == "lm_argmax":
+                assert cfg.path == _lib.SK_PATH_WIDE, (name, M, cfg)
+                assert _lib.workspace_bytes(op, M, N, K, cfg) == _tickets(1) + 8 * M   # one launch
+            else:
+                assert cfg.groups > 1 and -(-M // cfg.groups) <= 32, (name, M, cfg)
             assert _lib.check_config(op, M, N, K, cfg) == SK_OK, (name, M)
     # one launch of four 32-row groups: the split-K partials of every group,
     # once; 129 rows take one more launch, which reuses that workspace
