@@ -17,6 +17,16 @@ namespace sk {
 
 constexpr int HEAD_D = 128;   // head width of Qwen3 (the only one compiled)
 
+// K/V blocks a wave keeps in flight beyond the one it processes (1 or 2).
+// One: with two the first round of requests of the whole grid (24 MB at
+// B = 16, position 1088) was served in no particular order and the last waves
+// started late (B = 16 with two key splits: 17.6 us with two blocks ahead,
+// 16.9 with one; pure streaming reads of the same 71 MB by 128 workgroups of
+// 512 threads: 14.6 us with 8 loads per thread in flight, 19.1 with 16).
+#ifndef SK_ATTN_AHEAD
+#define SK_ATTN_AHEAD 1
+#endif
+
 // ---------------------------------------------------------------------------
 // q/k RMSNorm + RoPE + cache write (rope.py:94-188 cast placement):
 //   n = bf16(x * rsqrt(mean(x^2) + eps)); y = bf16(w * n)
@@ -383,15 +393,31 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
       }
   };
   u32x4 kA[4], vA[4], kB[4], vB[4], kC[4], vC[4];   // the 4 K and 4 V loads of a block
-  if (start < end) {
-    load_block(start, kA, vA);
-    load_block(start + step, kB, vB);
-  }
   const int unmasked_end = min(end, pos);   // blocks wholly below it skip the masks
   auto run = [&](int nb, const u32x4* kf, const u32x4* vv) {
     if (nb + step <= unmasked_end) process(nb, kf, vv, std::false_type{});   // uniform
     else process(nb, kf, vv, std::true_type{});
   };
+#if SK_ATTN_AHEAD == 1
+  // One block in flight beyond the one being processed (two buffers).
+  (void)kC;
+  (void)vC;
+  if (start < end) load_block(start, kA, vA);
+  for (int n0 = start; n0 < end; n0 += 2 * step) {
+    load_block(n0 + step, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    run(n0, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    load_block(n0 + 2 * step, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    run(n0 + step, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#else
+  if (start < end) {
+    load_block(start, kA, vA);
+    load_block(start + step, kB, vB);
+  }
   // The scheduling fences keep every prefetch ahead of the block it overlaps.
   for (int n0 = start; n0 < end; n0 += 3 * step) {
     load_block(n0 + 2 * step, kC, vC);
@@ -407,6 +433,7 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
     run(n0 + 2 * step, kC, vC);
     __builtin_amdgcn_sched_barrier(0);
   }
+#endif
 
   // Per wave: the row sums of the 4 lanes of each row, then the waves'
   // results merge in LDS in wave order.
@@ -552,11 +579,14 @@ int attn_plan(int B, int HQ, int HKV, int D, int R, int cap, int max_len, int ns
   const int blocks = cdiv(work, block);
   int S = nsplit;
   if (S <= 0) {
-    // About one workgroup per two CUs of an MI355X: the cross-workgroup merge
-    // of the splits costs more than the compute units left idle (B = 16,
-    // 8 KV heads, ~1.1k keys: one split 15.4 us, two 16.3 us, eight 24 us).
+    // Decode (one query row per sequence): about one workgroup per CU of an
+    // MI355X (B = 16, 8 KV heads, 1089 keys: 17.4 us in one split per pair,
+    // 16.8 in two; B = 4: 10.9 -> 9.6 us; decode step 5896 -> 5978 tok/s).
+    // Verify rows (R > 1, one or more 16-row blocks per pair): about one per
+    // two CUs, where a second split cost the 16 x 8 verify pass 10%.
     const long pairs = (long)B * HKV;
-    S = (int)((128 + pairs - 1) / pairs);
+    const long target = R == 1 ? 256 : 128;
+    S = (int)((target + pairs - 1) / pairs);
     if (S > 32) S = 32;
   }
   if (S > blocks) S = blocks;
