@@ -429,9 +429,10 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 58.7 us (67.3 at grid 64)
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
-    // down at M = 2-8: eight waves of five 256-column chunks cover K = 9728
-    // without a global split (13.1 -> 12.6 us at M = 8).
-    {SK_OP_GEMM, 2560, 9728, 2, {3, 8, 40, 16, 1, 0}},  // down      12.08 us  4124 GB/s
+    // down at M = 3-8: eight waves of five 256-column chunks cover K = 9728
+    // without a global split (13.1 -> 12.6 us at M = 8); at M = 2 the GEMV
+    // of M = 1 is still ahead (11.33 us against 12.09).
+    {SK_OP_GEMM, 2560, 9728, 2, {2, 2, 10, 2, 1, 0}},  // down      11.33 us  4398 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {3, 8, 40, 12, 1, 0}},  // down      12.16 us  4098 GB/s
     {SK_OP_GEMM, 2560, 9728, 8, {3, 8, 40, 12, 1, 0}},  // down      12.59 us  3962 GB/s
     {SK_OP_GEMM, 2560, 9728, 16, {3, 13, 8, 32, 3, 240}},  // down      13.5 us  3717 GB/s (with partial rows padded; 14.0 with four-chunk waves)
