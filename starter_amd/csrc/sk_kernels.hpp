@@ -1533,14 +1533,27 @@ __global__ void __launch_bounds__(RMS_THREADS) add_rmsnorm_kernel(const uint16_t
   uint16_t* xo = xout + (int64_t)m * ld;
   uint16_t* orow = out + (int64_t)m * ld_out;
   const int nchunk = K >> 3;
-  u32x4 sv[RMS_MAX_CHUNKS];
+  // Every load of the row (x, y and the norm weights) is requested before
+  // the first is used: the weights are not left for after the reduction,
+  // where they would add a memory round trip to the launch.
+  u32x4 sv[RMS_MAX_CHUNKS], xv[RMS_MAX_CHUNKS], yv[RMS_MAX_CHUNKS], wv[RMS_MAX_CHUNKS];
+#pragma unroll
+  for (int j = 0; j < RMS_MAX_CHUNKS; ++j) {
+    const int c = threadIdx.x + j * RMS_THREADS;
+    xv[j] = yv[j] = wv[j] = u32x4{0u, 0u, 0u, 0u};
+    if (c < nchunk) {
+      xv[j] = ld16(xr + 8 * c);
+      yv[j] = ld16(yr + 8 * c);
+      wv[j] = ld16(w + 8 * c);
+    }
+  }
   float sq = 0.f;
 #pragma unroll
   for (int j = 0; j < RMS_MAX_CHUNKS; ++j) {
     const int c = threadIdx.x + j * RMS_THREADS;
     sv[j] = u32x4{0u, 0u, 0u, 0u};
     if (c < nchunk) {
-      sv[j] = add_bf16x8(ld16(xr + 8 * c), ld16(yr + 8 * c), sq);
+      sv[j] = add_bf16x8(xv[j], yv[j], sq);
       *reinterpret_cast<u32x4*>(xo + 8 * c) = sv[j];
     }
   }
@@ -1554,7 +1567,7 @@ __global__ void __launch_bounds__(RMS_THREADS) add_rmsnorm_kernel(const uint16_t
 #pragma unroll
   for (int j = 0; j < RMS_MAX_CHUNKS; ++j) {
     const int c = threadIdx.x + j * RMS_THREADS;
-    if (c < nchunk) *reinterpret_cast<u32x4*>(orow + 8 * c) = norm_bf16x8(sv[j], ld16(w + 8 * c), rstd);
+    if (c < nchunk) *reinterpret_cast<u32x4*>(orow + 8 * c) = norm_bf16x8(sv[j], wv[j], rstd);
   }
 }
 
