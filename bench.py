@@ -463,6 +463,43 @@ def _dispatches(folder: Path, csv_name: str) -> list[dict]:
     return [per[k] for k in sorted(per)]
 
 
+def trace_summary(folder: str, regex: str = "sk::", per: int = 0) -> int:
+    """One markdown row per kernel launch shape in the rocprofv3 kernel trace(s)
+    under ``folder``: kernels whose name matches ``regex``, grouped by (name,
+    workgroups, workgroup size) in order of first appearance, with launch
+    count, kernel-only average / median / min / max duration and, when ``per``
+    is given, the launches and microseconds per unit (e.g. per decode step)."""
+    import csv
+    import re
+
+    pat = re.compile(regex)
+    groups: dict = {}
+    for f in sorted(Path(folder).rglob("*kernel_trace.csv")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"]
+                if not pat.search(name):
+                    continue
+                wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+                grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]) // max(wg, 1)
+                key = (name.replace("void ", "").split("(")[0], grid, wg, r.get("VGPR_Count", ""))
+                groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    head = "| kernel | workgroups | threads | VGPR | launches | avg us | median us | min us | max us |"
+    print(head + (" launches per unit | us per unit |" if per else ""))
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|" + ("---:|---:|" if per else ""))
+    total = 0.0
+    for (name, grid, wg, vgpr), us in groups.items():
+        line = (f"| `{name}` | {grid} | {wg} | {vgpr} | {len(us)} | {statistics.mean(us):.2f} | "
+                f"{statistics.median(us):.2f} | {min(us):.2f} | {max(us):.2f} |")
+        if per:
+            line += f" {len(us) / per:.1f} | {sum(us) / per:.1f} |"
+            total += sum(us) / per
+        print(line)
+    if per:
+        print(f"\nSum of the listed kernels per unit: {total:.1f} us ({per} units).")
+    return 0
+
+
 def counters_summary(folder: str) -> int:
     """One markdown row per probe from the counter passes of ``--probe`` runs
     laid out as <folder>/<op>_m<M>_{kt,A,B,C,D} (kernel trace, then the four
@@ -799,12 +836,19 @@ def main() -> int:
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc output folders of --probe (FETCH_SIZE, WRITE_SIZE) into "
                          "profiles/traffic_<probe-op>_m<M>.json and exit")
+    ap.add_argument("--trace-from", metavar="FOLDER",
+                    help="print a markdown table of the library's kernels in the rocprofv3 kernel trace under "
+                         "FOLDER and exit (--trace-regex, --trace-per)")
+    ap.add_argument("--trace-regex", default="sk::", help="kernel-name pattern for --trace-from")
+    ap.add_argument("--trace-per", type=int, default=0, help="with --trace-from: units to divide totals by")
     ap.add_argument("--counters-from", metavar="FOLDER",
                     help="print a markdown row per probe from the rocprofv3 passes under FOLDER "
                          "(<op>_m<M>_kt, _A, _B, _C, _D) and exit")
     args = ap.parse_args()
     if args.counters_from:
         return counters_summary(args.counters_from)
+    if args.trace_from:
+        return trace_summary(args.trace_from, args.trace_regex, args.trace_per)
     if args.traffic_from:
         return traffic_summary(args.traffic_from[0], args.traffic_from[1], args.M, args.probe_op)
 
