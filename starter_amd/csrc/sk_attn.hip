@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int dg = lane & 15, kr = lane >> 4;
   // Workgroup (b, kv head, row block, split): query rows rbk*QR .. +QR-1 of
   // the KV head's G*R rows (row = t*G + g), keys of split s.
@@ -393,9 +393,15 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
       }
   };
   u32x4 kA[4], vA[4], kB[4], vB[4], kC[4], vC[4];   // the 4 K and 4 V loads of a block
-  const int unmasked_end = min(end, pos);   // blocks wholly below it skip the masks
+  const int unmasked_end = min(end, pos);   // keys below it need no masks
+  // Per wave (uniform): its 16 keys of block nb are nb + 16*wave .. +15.  A
+  // wave whose keys all lie at or past `end` skips the block (every score
+  // would be masked: p = 0, m and l unchanged, so skipping is exact); one
+  // whose keys all lie below `unmasked_end` takes the body without masks.
   auto run = [&](int nb, const u32x4* kf, const u32x4* vv) {
-    if (nb + step <= unmasked_end) process(nb, kf, vv, std::false_type{});   // uniform
+    const int wk = nb + 16 * wave;
+    if (wk >= end) return;
+    if (wk + 16 <= unmasked_end) process(nb, kf, vv, std::false_type{});
     else process(nb, kf, vv, std::true_type{});
   };
 #if SK_ATTN_AHEAD == 1

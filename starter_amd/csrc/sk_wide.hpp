@@ -144,8 +144,12 @@ __device__ __forceinline__ void wide_body(Args p) {
   };
   static_assert(PF >= 1 && PF < D, "prefetch distance within the register slots");
   if (G > 0) issue_w(std::integral_constant<int, 0>{}, 0);
-  if (PF > 1 && G > 1) issue_w(std::integral_constant<int, 1>{}, 1);
-  if (PF > 2 && G > 2) issue_w(std::integral_constant<int, 2>{}, 2);
+  if constexpr (PF > 1) {
+    if (G > 1) issue_w(std::integral_constant<int, 1>{}, 1);
+  }
+  if constexpr (PF > 2) {
+    if (G > 2) issue_w(std::integral_constant<int, 2>{}, 2);
+  }
   if (G > 0) issue_acts(std::integral_constant<int, 0>{}, c_lo);
 
   f32x4 acc[NL][MTW];
