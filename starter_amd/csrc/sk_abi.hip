@@ -264,20 +264,24 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     // 16-row activation tiles, every wave multiplies the whole weight tile
     // of `rows` rows (gate/up: rows gate + rows up), staged in LDS in
     // 256-column steps (ku = 8).
-    // `groups` (1 or 2) = WN, the wave groups along the tile's slabs.
+    // `groups` (1 or 2) = WN, the wave groups along the tile's slabs;
+    // groups = 4 selects the body that stages the activation rows in LDS too
+    // (four waves, two activation tiles each, every wave on the whole tile).
     const int wn = c.groups > 1 ? c.groups : 1;
-    if (variant != 0 || wn > 2 || (wn == 2 && c.waves != 8)) return SK_ERR_CONFIG;
+    if (variant != 0 || (wn != 1 && wn != 2 && wn != 4) || (wn == 2 && c.waves != 8)) return SK_ERR_CONFIG;
     if ((c.waves != 4 && c.waves != 8) || c.ku != 8) return SK_ERR_CONFIG;
-    if (c.rows < 1 || c.rows > (gateup ? (wn == 2 ? 32 : 48) : 96)) return SK_ERR_CONFIG;
+    const int max_rows = wn == 4 ? (gateup ? 64 : 128) : (gateup ? (wn == 2 ? 32 : 48) : 96);
+    if (c.rows < 1 || c.rows > max_rows) return SK_ERR_CONFIG;
     units = cdiv(K, sk::kWideChunk);
     pl->tm = cdiv(M, 16);
     const int half = cdiv(c.rows, 16);                    // slabs per half (gate/up) or per tile
-    const int hw = cdiv(half, wn) * wn;                   // rounded to whole slabs per wave group
+    const int hw = wn == 4 ? half : cdiv(half, wn) * wn;  // rounded to whole slabs per wave group
     pl->tn = gateup ? 2 * hw : hw;
     if (pl->tn < 2) pl->tn = 2;   // the smallest instance stages two slabs
+    if (wn == 4 && (pl->tn == 7 || (c.waves == 8 && (pl->tn & 1)))) pl->tn += 1;   // compiled slab counts
     pl->tku = sk::kWideChunk;
     partial_rows = 0;
-    pl->pre_lds = sk::wide_weight_lds(pl->tn);
+    pl->pre_lds = wn == 4 ? sk::wide2_lds(pl->tn) : sk::wide_weight_lds(pl->tn);
   } else if (c.path == SK_PATH_GEMV) {
     if (c.rows != 2 && c.rows != 4 && c.rows != 8) return SK_ERR_CONFIG;
     if (M > 8) return SK_ERR_CONFIG;
@@ -414,7 +418,10 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 4096, 48, {3, 4, 32, 32, 1, 80, 3}},  // o_proj     9.92 us  2114 GB/s (three row groups; 11.5 without)
     {SK_OP_GEMM, 2560, 4096, 64, {3, 4, 32, 32, 1, 80, 3}},  // o_proj    12.37 us  1696 GB/s (three row groups; 14.8 without)
     {SK_OP_GEMM, 2560, 4096, 96, {3, 4, 32, 32, 1, 80, 3}},  // o_proj    12.7 us  (three 32-row groups; 14.8 with six)
-    {SK_OP_GEMM, 2560, 4096, 128, {3, 4, 32, 32, 1, 80, 8}},  // o_proj    20.1 us  (eight row groups; 24.9 as two 64-row launches)
+    // 97-128 rows on the two-operand wide path (activation rows and weight
+    // tile both staged in LDS, eight waves): 21.4 us against 22.1 for eight
+    // row groups (24.9 as two 64-row launches).
+    {SK_OP_GEMM, 2560, 4096, 128, {4, 8, 8, 32, 3, 0, 4}},  // o_proj    21.4 us
     {SK_OP_GATEUP, 9728, 2560, 1, {3, 10, 8, 16, 1, 203}},  // gate_up   17.31 us  5755 GB/s
     {SK_OP_RMSNORM_GATEUP, 9728, 2560, 1, {2, 4, 2, 2, 1, 0}},  // fused prologue beats 17.31 + a norm launch
     {SK_OP_GATEUP, 9728, 2560, 2, {3, 10, 8, 16, 1, 203}},  // gate_up   17.35 us  5746 GB/s
@@ -425,7 +432,10 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   24.7 us  4080 GB/s (two row groups; 25.8 half ring)
     {SK_OP_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   30.0 us  3373 GB/s (two row groups; 45.0 without)
-    {SK_OP_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 64, 4}},  // gate_up   40.7 us  (four row groups; 55.9 as two 64-row launches)
+    // 65-128 rows: the two-operand wide path, 40 + 40-row tiles (244
+    // workgroups of eight waves): 36.1 us at 128 rows, 34.7 at 96, against
+    // 42.9 and 38.1 for four row groups (55.9 as two 64-row launches).
+    {SK_OP_GATEUP, 9728, 2560, 128, {4, 8, 8, 40, 1, 0, 4}},  // gate_up   36.1 us
     {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 58.7 us (67.3 at grid 64)
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
@@ -440,7 +450,11 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
-    {SK_OP_GEMM, 2560, 9728, 128, {3, 10, 8, 16, 4, 64, 4}},  // down      38.0 us  (four row groups; 47.3 as two 64-row launches)
+    // 65-128 rows: the two-operand wide path, three K splits of 32-row tiles:
+    // 34.4 us at 128 rows, 30.7 at 96 (four row groups with four splits 38.5
+    // and 35.7; six splits of 64-row tiles within 0.4 us at twice the
+    // partials).
+    {SK_OP_GEMM, 2560, 9728, 128, {4, 8, 8, 32, 3, 0, 4}},  // down      34.4 us
     // Residual hand-off producers at decode row counts (the projection's
     // entries above use tile heights the hand-off cannot take).
     {SK_OP_RESID_GEMM, 2560, 4096, 8, {3, 16, 8, 16, 1, 0}},   // o_proj producer  7.46 us
@@ -456,14 +470,15 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
-    // lm_head + argmax at 65-128 rows: the wide path, every row in one
-    // workgroup of eight waves over 96-row weight tiles (291-295 us at 128
-    // rows against 306-309 for four row groups; 362 as two 64-row launches)
-    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 96, 1, 0, 0}},
+    // lm_head + argmax at 65-128 rows: the two-operand wide path, every row
+    // in one workgroup of eight waves over 96-row weight tiles (241 us at 128
+    // rows, 235 at 96; the weights-only-in-LDS wide body 281 and 269, four
+    // row groups 306-309, two 64-row launches 362)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 96, 1, 0, 4}},
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer, as for qkv
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
-    {SK_OP_GEMM, 151936, 2560, 128, {3, 10, 8, 16, 1, 256, 4}},  // lm_head logits 306-342 us (four row groups; 512-workgroup grid 318)
+    {SK_OP_GEMM, 151936, 2560, 128, {4, 8, 8, 96, 1, 0, 4}},  // lm_head logits 256 us (two-operand wide path; four row groups 304-342)
 };
 
 // Tuned entry for op/N/K at the smallest tuned row count >= M among op's own

@@ -15,20 +15,33 @@ __global__ void __launch_bounds__(64 * W) wide_entry(Args p) {
   wide_body<W, WN, NT, EPI>(p);
 }
 
+// Both operands staged in LDS (sk_wide2.hpp): four or eight waves, keyed as
+// WN = 4.
+template <int W, int NT, int EPI>
+__global__ void __launch_bounds__(64 * W) wide2_entry(Args p) {
+  wide2_body<W, NT, EPI>(p);
+}
+
 #define SK_W(W, WN, NT) \
   case W * 1000 + WN * 100 + NT: return &wide_entry<W, WN, NT, SK_EPI>;
+#define SK_W2(W, NT) \
+  case W * 1000 + 4 * 100 + NT: return &wide2_entry<W, NT, SK_EPI>;
 
-// (W waves, WN groups of them along the tile's weight slabs, NT slabs)
+// (W waves, WN groups of them along the tile's weight slabs, NT slabs; W = 4,
+// WN = 4: the two-operand body)
 KernelFn SK_CAT(wide_for_epi, SK_EPI)(int W, int WN, int NT) {
   switch (W * 1000 + WN * 100 + NT) {
 #if SK_EPI == 1 || SK_EPI == 4   // gate/up: NT/2 gate slabs + NT/2 up slabs
     SK_W(4, 1, 2) SK_W(4, 1, 4) SK_W(4, 1, 6)
     SK_W(8, 1, 2) SK_W(8, 1, 4) SK_W(8, 1, 6)
     SK_W(8, 2, 4)
+    SK_W2(4, 4) SK_W2(4, 6) SK_W2(4, 8) SK_W2(8, 4) SK_W2(8, 6)
 #else
     SK_W(4, 1, 2) SK_W(4, 1, 3) SK_W(4, 1, 4) SK_W(4, 1, 5) SK_W(4, 1, 6)
     SK_W(8, 1, 2) SK_W(8, 1, 3) SK_W(8, 1, 4) SK_W(8, 1, 5) SK_W(8, 1, 6)
     SK_W(8, 2, 2) SK_W(8, 2, 4) SK_W(8, 2, 6)
+    SK_W2(4, 2) SK_W2(4, 3) SK_W2(4, 4) SK_W2(4, 5) SK_W2(4, 6) SK_W2(4, 8)
+    SK_W2(8, 2) SK_W2(8, 4) SK_W2(8, 6)
 #endif
     default: break;
   }

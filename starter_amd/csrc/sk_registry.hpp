@@ -11,6 +11,7 @@
 
 #include "sk_kernels.hpp"
 #include "sk_wide.hpp"
+#include "sk_wide2.hpp"
 
 namespace sk {
 

@@ -1,0 +1,259 @@
+// sk_wide2.hpp - the wide-M body with both operands staged in LDS: up to 128
+// activation rows and a tile of weight rows per workgroup, four waves, each
+// wave multiplying the whole weight tile against its own 32 activation rows.
+//
+// Why a second wide body: in sk_wide.hpp every wave fetches its activation
+// fragments from L2 itself (16 rows x 64 B per instruction) and reads every
+// staged weight fragment once per 16 activation rows; at 128 rows those two
+// streams, not HBM, set its time.  Here:
+//
+//  * Each 128-column step stages the tile's weight rows AND the 128
+//    activation rows in LDS (one 272-byte row per staged row: fragment reads
+//    of 16 consecutive rows are conflict-free), loaded row-contiguous by all
+//    four waves (one instruction = 256 B of each of four rows).
+//  * Wave w holds the fp32 accumulators of activation tiles 2w and 2w + 1
+//    against every weight slab: per 32-column MFMA step it reads NT weight
+//    fragments and two activation fragments for 2 NT MFMAs, i.e. each weight
+//    fragment read from LDS feeds two MFMAs and each activation fragment NT.
+//  * Global loads run two steps ahead in a three-slot register ring (the
+//    steps of successive tiles form one sequence), LDS is double-buffered with
+//    one barrier per step: a wave writes buffer g & 1 only after every wave
+//    passed step g - 1's barrier, i.e. finished reading it at step g - 2.
+//
+// Epilogues and the cross-workgroup finishes are those of sk_wide.hpp: bf16
+// store, SwiGLU, fused argmax (per-row LDS bests, then argmax_fixup), split-K
+// partials finished in-kernel by the last workgroup of each tile.
+#pragma once
+
+#include "sk_wide.hpp"
+
+namespace sk {
+
+constexpr int kW2Step = 128;                  // K columns per step
+constexpr int kW2Pitch = 2 * kW2Step + 16;    // LDS bytes per staged row
+constexpr int kW2Rows = 128;                  // activation rows staged per step (M <= 128)
+
+// LDS bytes of a two-operand wide instance: two buffers of the weight tile's
+// 16 NT rows and 128 activation rows; the argmax bests or split-K flags follow.
+constexpr size_t wide2_lds(int NT) { return (size_t)2 * (16 * NT + kW2Rows) * kW2Pitch; }
+
+template <int W, int NT, int EPI>
+__device__ __forceinline__ void wide2_body(Args p) {
+  constexpr bool GATEUP = EpiTraits<EPI>::gateup;
+  constexpr int BASE = EpiTraits<EPI>::base;
+  static_assert(!EpiTraits<EPI>::norm && !EpiTraits<EPI>::pre && !EpiTraits<EPI>::resid, "plain epilogues only");
+  static_assert(!GATEUP || NT % 2 == 0, "gate/up tiles pair NT/2 gate slabs with NT/2 up slabs");
+  static_assert(W == 4 || W == 8, "four waves, or eight splitting each step's K units in two");
+  constexpr int KH = W / 4;                  // K halves of a step (waves w and w + 4 share tiles)
+  constexpr int MTW = 2;                     // 16-row activation tiles per wave
+  constexpr int ROWS = 16 * NT;              // staged weight rows
+  constexpr int SROWS = ROWS + kW2Rows;      // staged rows per buffer
+  constexpr int H = GATEUP ? NT / 2 : NT;    // slabs per half
+  constexpr int HROWS = 16 * H;              // output columns a tile can hold (the finish's stride)
+  constexpr int UNITS = kW2Step / 32;        // MFMA K steps per step
+  constexpr int WLD = ROWS / (4 * W);        // weight load instructions per wave and step
+  constexpr int ALD = kW2Rows / (4 * W);     // activation load instructions per wave and step
+  static_assert(ROWS % (4 * W) == 0, "weight loads split evenly over the waves");
+  constexpr int UW = UNITS / KH;             // MFMA K steps of one wave per step
+  constexpr int D = 3, PF = 2;               // register slots, steps requested ahead
+
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  char* const buf = reinterpret_cast<char*>(lds);
+  char* const tail = buf + wide2_lds(NT);
+  unsigned long long* const lds_best = reinterpret_cast<unsigned long long*>(tail);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int mw = wave % 4, kh = wave / 4;     // activation tiles 2 mw, 2 mw + 1; K half kh
+  const int M = p.M, TR = p.tr;
+  const int S = p.S;
+  const int slice = blockIdx.x % (unsigned)S;
+  const int rbstep = p.rbstep;
+  const int rb0 = blockIdx.x / (unsigned)S;
+  const int ntiles = wg_tiles(rb0, rbstep, p.nrb);
+  // The planner's K units are 256-column chunks; a step is half of one.
+  const int nchunks = (p.K + kWideChunk - 1) / kWideChunk;
+  const int s_lo = 2 * slice * p.slice_units;
+  const int s_hi = min(2 * min((slice + 1) * p.slice_units, nchunks), (p.K + kW2Step - 1) / kW2Step);
+  const int nsteps = max(s_hi - s_lo, 0);
+  const int G = ntiles * nsteps;
+  auto tile_of = [&](int g) { return rb0 + (g / nsteps) * rbstep; };
+  auto step_of = [&](int g) { return s_lo + g % nsteps; };
+  const uint16_t* const zero16 = reinterpret_cast<const uint16_t*>(kZeroLine);
+  if constexpr (BASE == EPI_ARGMAX) {
+    for (int i = tid; i < M; i += 64 * W) lds_best[i] = 0ull;   // ordered by the first step's barrier
+  }
+
+  // Load instruction i of this wave covers staged rows 4*(wave + W*i) + g4
+  // (lane: 16 bytes at column 8*r16 of the step).  The row addresses are
+  // formed once (activations) or once per tile (weights); weight rows past
+  // the tile or past N (clamped), activation rows past M and columns past K
+  // read the zero line.
+  const uint16_t* abase[ALD];
+  bool aok[ALD];
+#pragma unroll
+  for (int i = 0; i < ALD; ++i) {
+    const int ar = 4 * (wave + W * i) + g4;
+    aok[i] = ar < M;
+    abase[i] = p.A + (int64_t)min(ar, M - 1) * p.lda + 8 * r16;
+  }
+  const uint16_t* wbase[WLD];
+  bool wok[WLD];
+  auto set_tile = [&](int rb) {
+#pragma unroll
+    for (int i = 0; i < WLD; ++i) {
+      const int sr = 4 * (wave + W * i) + g4;
+      const int half = sr / HROWS, hr = sr - half * HROWS;
+      wok[i] = hr < TR;
+      const int row = min(rb * TR + hr, p.N - 1);
+      wbase[i] = ((GATEUP && half) ? p.W1 : p.W0) + (int64_t)row * p.ldw + 8 * r16;
+    }
+  };
+
+  u32x4 wreg[D][WLD];
+  u32x4 areg[D][ALD];
+  // Requests are made in step order, so the weight row addresses follow the
+  // tile of the step being requested.
+  auto issue = [&](auto slot, int g) {
+    constexpr int SL = decltype(slot)::value;
+    const int st = step_of(g);
+    if (st == s_lo) set_tile(tile_of(g));   // uniform: the first step of a tile
+    const int col0 = st * kW2Step;
+    const bool colok = col0 + 8 * r16 < p.K;
+#pragma unroll
+    for (int i = 0; i < WLD; ++i) wreg[SL][i] = ld16_stream(wok[i] && colok ? wbase[i] + col0 : zero16);
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) areg[SL][i] = ld16(aok[i] && colok ? abase[i] + col0 : zero16);
+  };
+  if (G > 0) issue(std::integral_constant<int, 0>{}, 0);
+  if (G > 1) issue(std::integral_constant<int, 1>{}, 1);
+
+  f32x4 acc[NT][MTW];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int i = 0; i < MTW; ++i) acc[nt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  // Tile epilogue.  Lane holds, for activation row m = 16*(MTW*mw + i) + r16,
+  // the tile's output columns hr = 16*h + 4*g4 + e (e < 4) of slab h (and,
+  // for gate/up, the up value of the same column in slab h + H).
+  auto epilogue = [&](int rb) {
+#pragma unroll
+    for (int i = 0; i < MTW; ++i) {
+      const int m = 16 * (MTW * mw + i) + r16;
+      unsigned long long key = 0ull;
+#pragma unroll
+      for (int h = 0; h < H; ++h)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int hr = 16 * h + 4 * g4 + e;
+          const int n = rb * TR + hr;
+          const bool ok = m < M && hr < TR && n < p.N;
+          if constexpr (BASE == EPI_STORE) {
+            if (ok) p.C[(int64_t)m * p.ldc + n] = f2bf(acc[h][i][e]);
+          } else if constexpr (BASE == EPI_SWIGLU) {
+            if (ok) p.C[(int64_t)m * p.ldc + n] = swiglu_bf(acc[h][i][e], acc[h + H][i][e]);
+          } else if constexpr (BASE == EPI_PART) {
+            if (ok) store_agent(&p.part[((int64_t)slice * M + m) * p.N + n], acc[h][i][e]);
+          } else if constexpr (BASE == EPI_PART_GU) {
+            if (ok) {
+              store_agent(&p.part[((int64_t)slice * M + m) * p.N + n], acc[h][i][e]);
+              store_agent(&p.part[((int64_t)(S + slice) * M + m) * p.N + n], acc[h + H][i][e]);
+            }
+          } else {   // EPI_ARGMAX
+            if (ok) {
+              const unsigned long long k = argmax_key(f2bf(acc[h][i][e]), n);
+              key = k > key ? k : key;
+            }
+          }
+        }
+      if constexpr (BASE == EPI_ARGMAX) {
+        // the four lanes of row m (g4 = 0..3), then one LDS atomic per row
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+          const unsigned long long o = ((unsigned long long)(uint32_t)__shfl_xor((int)(key >> 32), off) << 32) |
+                                       (uint32_t)__shfl_xor((int)(key & 0xFFFFFFFFu), off);
+          key = o > key ? o : key;
+        }
+        if (g4 == 0 && m < M && key) atomicMax(&lds_best[m], key);
+      }
+    }
+  };
+
+  auto step = [&](auto slot, int g) {
+    constexpr int SL = decltype(slot)::value;   // g % D
+    char* const sb = buf + (g & 1) * (SROWS * kW2Pitch);
+    // Stage step g's rows, then request step g + PF's into the slot that held
+    // step g + PF - D (already staged).
+#pragma unroll
+    for (int i = 0; i < WLD; ++i)
+      *reinterpret_cast<u32x4*>(sb + (4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = wreg[SL][i];
+#pragma unroll
+    for (int i = 0; i < ALD; ++i)
+      *reinterpret_cast<u32x4*>(sb + (ROWS + 4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = areg[SL][i];
+    if (g + PF < G) issue(std::integral_constant<int, (SL + PF) % D>{}, g + PF);
+    lds_barrier();
+#pragma unroll
+    for (int uu = 0; uu < UW; ++uu) {
+      const int u = kh * UW + uu;
+      bf16x8 af[MTW];
+#pragma unroll
+      for (int i = 0; i < MTW; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(sb + (ROWS + 16 * (MTW * mw + i) + r16) * kW2Pitch + 64 * u +
+                                                 16 * g4);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const bf16x8 wv = *reinterpret_cast<const bf16x8*>(sb + (16 * nt + r16) * kW2Pitch + 64 * u + 16 * g4);
+#pragma unroll
+        for (int i = 0; i < MTW; ++i) acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[i], acc[nt][i], 0, 0, 0);
+      }
+    }
+    if ((g + 1) % nsteps == 0) {   // the tile's last step
+      if constexpr (KH == 2) {
+        // Waves 4-7 hand their K half to waves 4 below through this step's
+        // buffer: every wave has finished reading it after the barrier, and
+        // it is written again only at step g + 2, after step g + 1's barrier,
+        // which waves 0-3 reach only once they have read it.
+        float* const red = reinterpret_cast<float*>(sb);
+        lds_barrier();
+        if (kh == 1) {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < MTW; ++i)
+              *reinterpret_cast<f32x4*>(red + ((mw * NT + nt) * MTW + i) * 256 + 4 * lane) = acc[nt][i];
+        }
+        lds_barrier();
+        if (kh == 0) {
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < MTW; ++i)
+              acc[nt][i] += *reinterpret_cast<const f32x4*>(red + ((mw * NT + nt) * MTW + i) * 256 + 4 * lane);
+          epilogue(tile_of(g));
+        }
+      } else {
+        epilogue(tile_of(g));
+      }
+      zero_acc();
+    }
+  };
+  for (int g0 = 0; g0 < G; g0 += D) {
+    step(std::integral_constant<int, 0>{}, g0);
+    if (g0 + 1 < G) step(std::integral_constant<int, 1>{}, g0 + 1);
+    if (g0 + 2 < G) step(std::integral_constant<int, 2>{}, g0 + 2);
+  }
+
+  if constexpr (BASE == EPI_ARGMAX) {
+    lds_barrier();
+    argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
+  } else if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU) {
+    splitk_fixup<HROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(tail));
+  }
+}
+
+}  // namespace sk

@@ -76,7 +76,8 @@ def test_default_config_is_valid_for_every_decode_shape(name, M):
         # output columns per tile: 16 for MFMA gate/up (16 gate + 16 up rows), else `rows`
         out_rows = 16 if (op == SK_OP_GATEUP and cfg.path != SK_PATH_GEMV) else cfg.rows
         tiles = -(-N // out_rows)
-        rows = g * -(-M // g) if g > 1 else min(M, 64)
+        # partial rows: one group's rows x groups; a wide launch holds up to 128
+        rows = g * -(-M // g) if g > 1 else (min(M, 128) if cfg.path == _lib.SK_PATH_WIDE else min(M, 64))
         assert ws == _tickets(g * tiles) + (2 if op == SK_OP_GATEUP else 1) * cfg.split * rows * N * 4
 
 
@@ -244,27 +245,31 @@ def test_row_groups_planning():
 
 def test_wide_calls_plan_one_launch_of_row_groups():
     """Up to 128 rows run as one launch when the configuration splits them
-    into row groups of at most 64 (the tuned entries do, for every Qwen3-4B
-    projection but lm_head + argmax) or runs them on the wide path (lm_head +
-    argmax: every row in one workgroup); more rows run as 128-row launches
-    plus the remainder.  An ungrouped configuration keeps 64-row launches."""
+    into row groups of at most 64 (the tuned entries do for qkv, and for
+    o_proj up to 96 rows) or runs them on the wide path (every row in one
+    workgroup: gate_up, down, lm_head and lm_head + argmax at 65-128 rows,
+    o_proj at 97-128); more rows run as 128-row launches plus the remainder.
+    An ungrouped configuration keeps 64-row launches."""
+    wide = {"gu": (65, 100, 128), "d": (65, 100, 128), "lm_argmax": (65, 100, 128), "lm": (65, 100, 128),
+            "o": (100, 128)}
     for name in ("qkv", "o", "gu", "d", "lm_argmax", "lm"):
         op, N, K = QWEN[name]
         for M in (65, 100, 128):
             cfg = _lib.default_config(op, M, N, K)
-            if name == "lm_argmax":
+            if M in wide.get(name, ()):
                 assert cfg.path == _lib.SK_PATH_WIDE, (name, M, cfg)
-                assert _lib.workspace_bytes(op, M, N, K, cfg) == _tickets(1) + 8 * M   # one launch
+                if op == SK_OP_LM_ARGMAX:
+                    assert _lib.workspace_bytes(op, M, N, K, cfg) == _tickets(1) + 8 * M   # one launch
             else:
                 assert cfg.groups > 1 and -(-M // cfg.groups) <= 32, (name, M, cfg)
             assert _lib.check_config(op, M, N, K, cfg) == SK_OK, (name, M)
-    # one launch of four 32-row groups: the split-K partials of every group,
+    # one wide launch of all 128 rows: the split-K partials of every row,
     # once; 129 rows take one more launch, which reuses that workspace
     op, N, K = QWEN["d"]
     cfg = _lib.default_config(op, 128, N, K)
-    assert cfg.split > 1
+    assert cfg.split > 1 and cfg.path == _lib.SK_PATH_WIDE
     one = _lib.workspace_bytes(op, 128, N, K)
-    assert one == _tickets(cfg.groups * (N // 16)) + cfg.groups * cfg.split * 32 * N * 4
+    assert one == _tickets(-(-N // cfg.rows)) + cfg.split * 128 * N * 4
     assert _lib.workspace_bytes(op, 129, N, K) == one
     assert _lib.workspace_bytes(op, 256, N, K) == one
     # an explicit ungrouped configuration: 64-row launches

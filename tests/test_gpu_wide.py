@@ -2,7 +2,8 @@
 
 Up to 128 activation rows run in one workgroup: four or eight waves split
 the 16-row activation tiles and every wave multiplies the whole weight tile,
-staged once per 256-column step in LDS.  Checked with every epilogue (bf16
+staged once per 256-column step in LDS (groups = 4: weight tile and
+activation rows both staged in LDS per 128-column step, csrc/sk_wide2.hpp).  Checked with every epilogue (bf16
 store, SwiGLU, fused argmax, split-K partials and their in-kernel finish for
 the plain and the gate/up GEMM), at the verify row counts of the reference
 (B x R = 64 and 128; engine/engine.py:451) and ragged ones, with tile heights
@@ -53,6 +54,18 @@ GEMM_CASES = [
     (6144, 2560, wide(8, 48, wn=2)),        # waves in two groups of slabs x four of activation tiles
     (2560, 9728, wide(8, 96, split=4, wn=2)),
     (777, 2560, wide(8, 20, wn=2, grid=16)),
+    # groups = 4: activation rows staged in LDS too (four waves, 32 rows each)
+    (6144, 2560, wide(4, 48, wn=4)),
+    (6144, 2560, wide(4, 64, split=2, wn=4)),
+    (2560, 4096, wide(4, 40, split=3, wn=4)),   # K slices of 6, 6, 4 chunks
+    (2560, 9728, wide(4, 80, split=4, wn=4)),
+    (777, 2560, wide(4, 13, wn=4)),             # one slab, ragged N
+    (777, 2560, wide(4, 128, grid=4, wn=4)),    # eight slabs, several tiles per workgroup
+    (1000, 2336, wide(4, 20, split=2, wn=4)),   # K = 18 * 128 + 32: the last step is partial
+    (6144, 2560, wide(8, 48, wn=4)),            # eight waves: each step's K units split in two
+    (2560, 9728, wide(8, 32, split=3, wn=4)),
+    (777, 2560, wide(8, 90, grid=4, wn=4)),
+    (1000, 2336, wide(8, 20, split=2, wn=4)),
 ]
 
 
@@ -73,6 +86,12 @@ GATEUP_CASES = [
     (1000, wide(8, 24, grid=8)),            # ragged I, several tiles per workgroup
     (9728, wide(8, 32, wn=2)),              # two groups of slabs: gate and up slab of each group
     (9728, wide(8, 24, split=2, wn=2)),
+    (9728, wide(4, 38, wn=4)),                  # 256 tiles of 38 gate + 38 up rows
+    (9728, wide(4, 64, wn=4)),
+    (9728, wide(4, 24, split=2, wn=4)),
+    (1000, wide(4, 40, grid=8, wn=4)),
+    (9728, wide(8, 38, wn=4)),
+    (9728, wide(8, 24, split=2, wn=4)),
 ]
 
 
@@ -88,7 +107,8 @@ def test_wide_gateup(case, M):
     assert_gateup_parity(out, bits(x), bits(wgu[:I]), bits(wgu[I:]), f"I={I} {cfg} M={M}")
 
 
-@pytest.mark.parametrize("cfg", [wide(4, 64), wide(8, 96), wide(4, 27, grid=64), wide(8, 96, wn=2)], ids=_ids)
+@pytest.mark.parametrize("cfg", [wide(4, 64), wide(8, 96), wide(4, 27, grid=64), wide(8, 96, wn=2), wide(4, 128, wn=4),
+                                 wide(4, 27, grid=64, wn=4), wide(8, 96, wn=4)], ids=_ids)
 @pytest.mark.parametrize("M", [1, 64, 128])
 def test_wide_lm_argmax(cfg, M):
     """Fused argmax over a 30000-token vocabulary (many tiles per workgroup)."""
