@@ -100,7 +100,9 @@ typedef enum sk_path {
  *            whose rows past the tile are not read, so a height of N / 256
  *            gives every CU one tile; the whole-tile body (ku 16) and the
  *            residual hand-off ops take 16 or 32, gate/up 16; SK_PATH_WIDE:
- *            1..96 rows, gate/up 1..48, with WN = 2 gate/up 1..32)
+ *            1..96 rows, gate/up 1..48, with WN = 2 gate/up 1..32, with
+ *            WN = 4 1..128 rows (eight waves 1..96), gate/up 17..64 (eight
+ *            waves 17..48))
  *   split  : global K splits; >1 writes fp32 partials to the workspace and
  *            the last workgroup to finish a tile sums them in fixed split
  *            order (no floating-point atomics, no second kernel)
@@ -118,7 +120,10 @@ typedef enum sk_path {
  *            SK_PATH_WIDE reads it as WN, the groups its waves form along
  *            the tile's weight slabs: 1 (every wave multiplies the whole
  *            tile for its activation tiles) or 2 (eight waves: two groups of
- *            slabs x four groups of activation tiles).
+ *            slabs x four groups of activation tiles); 4 selects the body
+ *            that stages the activation rows in LDS beside the weight tile
+ *            (128-column steps; four waves of 32 activation rows, or eight
+ *            whose pairs split each step's K columns).
  *
  * Rows per launch: at most 64 without row groups; with a configuration that
  * splits them into groups (compiled for groups of up to 32 rows), up to 128
