@@ -21,10 +21,10 @@
 //    4-7 hand their sums to waves 0-3 through LDS: two waves per SIMD hide
 //    each other's LDS and MFMA latencies (one wave per SIMD with four waves:
 //    gate_up at 128 rows 47.5 us against 36.1 with eight).
-//  * Global loads run two steps ahead in a three-slot register ring (the
-//    steps of successive tiles form one sequence), LDS is double-buffered with
-//    one barrier per step: a wave writes buffer g & 1 only after every wave
-//    passed step g - 1's barrier, i.e. finished reading it at step g - 2.
+//  * Global loads run ahead in a two-slot register ring (the steps of
+//    successive tiles form one sequence), LDS is double-buffered with one
+//    barrier per step: right after step g's barrier a wave stages step g + 1
+//    into the other buffer, which every wave finished reading at step g - 1.
 //
 // Epilogues and the cross-workgroup finishes are those of sk_wide.hpp: bf16
 // store, SwiGLU, fused argmax (per-row LDS bests, then argmax_fixup), split-K
@@ -61,7 +61,12 @@ __device__ __forceinline__ void wide2_body(Args p) {
   constexpr int ALD = kW2Rows / (4 * W);     // activation load instructions per wave and step
   static_assert(ROWS % (4 * W) == 0, "weight loads split evenly over the waves");
   constexpr int UW = UNITS / KH;             // MFMA K steps of one wave per step
-  constexpr int D = 3, PF = 2;               // register slots, steps requested ahead
+  // Step g + 1 is staged right after step g's barrier, beside step g's
+  // MFMAs (staging before the barrier, as sk_wide.hpp does, left the LDS
+  // writes and the MFMAs of a step in separate phases: gate_up at 128 rows
+  // 36.0 against 34.0 us); two register slots, each step's loads requested
+  // while the step three ahead of it is multiplied.
+  constexpr int D = 2, PF = 3;
 
   extern __shared__ __attribute__((aligned(16))) float lds[];
   char* const buf = reinterpret_cast<char*>(lds);
@@ -134,6 +139,20 @@ __device__ __forceinline__ void wide2_body(Args p) {
   };
   if (G > 0) issue(std::integral_constant<int, 0>{}, 0);
   if (G > 1) issue(std::integral_constant<int, 1>{}, 1);
+  auto stage = [&](auto slot, int g) {
+    constexpr int SL = decltype(slot)::value;
+    char* const sb = buf + (g & 1) * (SROWS * kW2Pitch);
+#pragma unroll
+    for (int i = 0; i < WLD; ++i)
+      *reinterpret_cast<u32x4*>(sb + (4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = wreg[SL][i];
+#pragma unroll
+    for (int i = 0; i < ALD; ++i)
+      *reinterpret_cast<u32x4*>(sb + (ROWS + 4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = areg[SL][i];
+  };
+  if (G > 0) {
+    stage(std::integral_constant<int, 0>{}, 0);
+    if (G > 2) issue(std::integral_constant<int, 0>{}, 2);
+  }
 
   f32x4 acc[NT][MTW];
   auto zero_acc = [&]() {
@@ -193,16 +212,13 @@ __device__ __forceinline__ void wide2_body(Args p) {
   auto step = [&](auto slot, int g) {
     constexpr int SL = decltype(slot)::value;   // g % D
     char* const sb = buf + (g & 1) * (SROWS * kW2Pitch);
-    // Stage step g's rows, then request step g + PF's into the slot that held
-    // step g + PF - D (already staged).
-#pragma unroll
-    for (int i = 0; i < WLD; ++i)
-      *reinterpret_cast<u32x4*>(sb + (4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = wreg[SL][i];
-#pragma unroll
-    for (int i = 0; i < ALD; ++i)
-      *reinterpret_cast<u32x4*>(sb + (ROWS + 4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = areg[SL][i];
-    if (g + PF < G) issue(std::integral_constant<int, (SL + PF) % D>{}, g + PF);
+    // Step g's rows are staged (by the previous step or the prologue).  After
+    // the barrier every wave has finished step g - 1's reads of the other
+    // buffer, so step g + 1 is staged there beside this step's MFMAs, and
+    // its register slot takes the loads of step g + 3.
     lds_barrier();
+    if (g + 1 < G) stage(std::integral_constant<int, (SL + 1) % D>{}, g + 1);
+    if (g + PF < G) issue(std::integral_constant<int, (SL + 1) % D>{}, g + PF);
 #pragma unroll
     for (int uu = 0; uu < UW; ++uu) {
       const int u = kh * UW + uu;
@@ -248,10 +264,10 @@ __device__ __forceinline__ void wide2_body(Args p) {
       zero_acc();
     }
   };
+  static_assert(D == 2, "the loop below is unrolled for two slots");
   for (int g0 = 0; g0 < G; g0 += D) {
     step(std::integral_constant<int, 0>{}, g0);
     if (g0 + 1 < G) step(std::integral_constant<int, 1>{}, g0 + 1);
-    if (g0 + 2 < G) step(std::integral_constant<int, 2>{}, g0 + 2);
   }
 
   if constexpr (BASE == EPI_ARGMAX) {
