@@ -219,6 +219,8 @@ __device__ __forceinline__ void wide2_body(Args p) {
     lds_barrier();
     if (g + 1 < G) stage(std::integral_constant<int, (SL + 1) % D>{}, g + 1);
     if (g + PF < G) issue(std::integral_constant<int, (SL + 1) % D>{}, g + PF);
+    // (a wave whose 32 activation rows all lie past M has nothing to multiply)
+    if (16 * MTW * mw < M) {
 #pragma unroll
     for (int uu = 0; uu < UW; ++uu) {
       const int u = kh * UW + uu;
@@ -234,12 +236,13 @@ __device__ __forceinline__ void wide2_body(Args p) {
         for (int i = 0; i < MTW; ++i) acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[i], acc[nt][i], 0, 0, 0);
       }
     }
+    }
     if ((g + 1) % nsteps == 0) {   // the tile's last step
       if constexpr (KH == 2) {
         // Waves 4-7 hand their K half to waves 4 below through this step's
         // buffer: every wave has finished reading it after the barrier, and
-        // it is written again only at step g + 2, after step g + 1's barrier,
-        // which waves 0-3 reach only once they have read it.
+        // it is written again only after step g + 1's barrier (staging step
+        // g + 2), which waves 0-3 reach only once they have read it.
         float* const red = reinterpret_cast<float*>(sb);
         lds_barrier();
         if (kh == 1) {
