@@ -271,20 +271,21 @@ __device__ __forceinline__ void wide2_body(Args p) {
     // (a wave whose 32 activation rows all lie past M has nothing to multiply)
     if (16 * MTW * mw < M) {
 #pragma unroll
-    for (int uu = 0; uu < UW; ++uu) {
-      const int u = kh * UW + uu;
-      bf16x8 af[MTW];
+      for (int uu = 0; uu < UW; ++uu) {
+        const int u = kh * UW + uu;
+        bf16x8 af[MTW];
 #pragma unroll
-      for (int i = 0; i < MTW; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(sb + (ROWS + 16 * (MTW * mw + i) + r16) * kW2Pitch + 64 * u +
-                                                 16 * g4);
+        for (int i = 0; i < MTW; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(sb + (ROWS + 16 * (MTW * mw + i) + r16) * kW2Pitch + 64 * u +
+                                                   16 * g4);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const bf16x8 wv = *reinterpret_cast<const bf16x8*>(sb + (16 * nt + r16) * kW2Pitch + 64 * u + 16 * g4);
+        for (int nt = 0; nt < NT; ++nt) {
+          const bf16x8 wv = *reinterpret_cast<const bf16x8*>(sb + (16 * nt + r16) * kW2Pitch + 64 * u + 16 * g4);
 #pragma unroll
-        for (int i = 0; i < MTW; ++i) acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[i], acc[nt][i], 0, 0, 0);
+          for (int i = 0; i < MTW; ++i)
+            acc[nt][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, af[i], acc[nt][i], 0, 0, 0);
+        }
       }
-    }
     }
     if ((g + 1) % nsteps == 0) {   // the tile's last step
       if constexpr (KH == 2) {
