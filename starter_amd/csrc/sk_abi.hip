@@ -471,14 +471,16 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
     // lm_head + argmax at 65-128 rows: the two-operand wide path, every row
-    // in one workgroup of eight waves over 96-row weight tiles (241 us at 128
-    // rows, 235 at 96; the weights-only-in-LDS wide body 281 and 269, four
-    // row groups 306-309, two 64-row launches 362)
-    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 96, 1, 0, 4}},
+    // in one workgroup of eight waves over 128-row weight tiles (218 us at
+    // 128 rows, 212 at 96; 96-row tiles 242 and 234, the weights-only-in-LDS
+    // wide body 281 and 269, four row groups 306-309, two 64-row launches 362)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 128, 1, 0, 4}},
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer, as for qkv
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
-    {SK_OP_GEMM, 151936, 2560, 128, {4, 8, 8, 96, 1, 0, 4}},  // lm_head logits 256 us (two-operand wide path; four row groups 304-342)
+    // lm_head logits at 65-128 rows: as for the fused argmax, 209 us at 128
+    // rows and 193 at 96 (96-row tiles 243 and 229, four row groups 304-342)
+    {SK_OP_GEMM, 151936, 2560, 128, {4, 8, 8, 128, 1, 0, 4}},
 };
 
 // Tuned entry for op/N/K at the smallest tuned row count >= M among op's own

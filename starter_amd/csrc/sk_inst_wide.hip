@@ -41,7 +41,7 @@ KernelFn SK_CAT(wide_for_epi, SK_EPI)(int W, int WN, int NT) {
     SK_W(8, 1, 2) SK_W(8, 1, 3) SK_W(8, 1, 4) SK_W(8, 1, 5) SK_W(8, 1, 6)
     SK_W(8, 2, 2) SK_W(8, 2, 4) SK_W(8, 2, 6)
     SK_W2(4, 2) SK_W2(4, 3) SK_W2(4, 4) SK_W2(4, 5) SK_W2(4, 6) SK_W2(4, 8)
-    SK_W2(8, 2) SK_W2(8, 4) SK_W2(8, 6)
+    SK_W2(8, 2) SK_W2(8, 4) SK_W2(8, 6) SK_W2(8, 8)
 #endif
     default: break;
   }

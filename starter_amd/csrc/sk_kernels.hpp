@@ -155,6 +155,13 @@ __device__ __forceinline__ unsigned long long argmax_key(uint16_t h, int n) {
   return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)n);
 }
 
+// The key's halves on their own: the value's order (1 .. 0x10001) and the
+// packing of an order with its column.
+__device__ __forceinline__ uint32_t argmax_ord(uint16_t h) { return (uint32_t)(argmax_key(h, 0) >> 32); }
+__device__ __forceinline__ unsigned long long argmax_pack(uint32_t ord, int n) {
+  return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)n);
+}
+
 __device__ __forceinline__ float argmax_key_value(unsigned long long key) {
   const uint32_t ord = (uint32_t)(key >> 32);
   if (ord == 0x10001u) return __uint_as_float(0x7FC00000u);

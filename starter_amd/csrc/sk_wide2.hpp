@@ -215,7 +215,13 @@ __device__ __forceinline__ void wide2_body(Args p) {
   // of sixteen rows (at 128 rows: o_proj's split-K partials 21.0 -> 18.3 us,
   // down 33.4 -> 29.9, the lm_head logits 249 -> 242).  The SwiGLU tile of
   // gate_up keeps the direct stores (36.5 against 38.9 us through LDS).
-  constexpr bool LDS_OUT = BASE == EPI_STORE || BASE == EPI_PART || BASE == EPI_PART_GU;
+  //
+  // The argmax tile of the eight-slab, eight-wave instance goes the same way
+  // (its per-lane epilogue does not fit the register file beside the
+  // pipeline): bf16 values to LDS, then four threads per row scan a quarter
+  // of the row's columns each.
+  constexpr bool LDS_ARGMAX = BASE == EPI_ARGMAX && W == 8 && NT == 8;
+  constexpr bool LDS_OUT = BASE == EPI_STORE || BASE == EPI_PART || BASE == EPI_PART_GU || LDS_ARGMAX;
   constexpr bool F32OUT = BASE == EPI_PART || BASE == EPI_PART_GU;
   constexpr int TP = HROWS + (F32OUT ? 4 : 8);
   constexpr int NMAT = BASE == EPI_PART_GU ? 2 : 1;
@@ -255,6 +261,41 @@ __device__ __forceinline__ void wide2_body(Args p) {
       } else {
         p.C[(int64_t)m * p.ldc + n] = reinterpret_cast<const uint16_t*>(sb)[m * TP + hr];
       }
+    }
+  };
+
+  auto argmax_tile = [&](int rb, const char* sb) {
+    constexpr int QC = HROWS / 4;   // columns per thread
+    static_assert(!LDS_ARGMAX || QC % 8 == 0, "16-byte LDS reads");
+    const uint16_t* const T = reinterpret_cast<const uint16_t*>(sb);
+    // a row's four threads are consecutive lanes, so the loop bound and the
+    // exchanges below are uniform over each group of four
+    for (int idx = tid; idx < 4 * M; idx += 64 * W) {
+      const int m = idx >> 2, q = idx & 3;
+      uint32_t bo = 0u;
+      int bn = 0;
+#pragma unroll
+      for (int v = 0; v < QC / 8; ++v) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(T + m * TP + q * QC + 8 * v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int hr = q * QC + 8 * v + k;
+          const int n = rb * TR + hr;
+          const uint32_t o = argmax_ord((uint16_t)(x[k >> 1] >> (16 * (k & 1))));
+          if (hr < TR && n < p.N && o > bo) {   // increasing columns: ties keep the lowest
+            bo = o;
+            bn = n;
+          }
+        }
+      }
+      unsigned long long key = bo ? argmax_pack(bo, bn) : 0ull;
+#pragma unroll
+      for (int off = 1; off <= 2; off <<= 1) {
+        const unsigned long long o = ((unsigned long long)(uint32_t)__shfl_xor((int)(key >> 32), off) << 32) |
+                                     (uint32_t)__shfl_xor((int)(key & 0xFFFFFFFFu), off);
+        key = o > key ? o : key;
+      }
+      if (q == 0 && key) atomicMax(&lds_best[m], key);
     }
   };
 
@@ -320,7 +361,10 @@ __device__ __forceinline__ void wide2_body(Args p) {
         lds_barrier();
         if (kh == 0) write_tile(sb);
         lds_barrier();
-        store_tile(tile_of(g), sb);
+        if constexpr (LDS_ARGMAX)
+          argmax_tile(tile_of(g), sb);
+        else
+          store_tile(tile_of(g), sb);
       }
       zero_acc();
     }

@@ -66,6 +66,7 @@ GEMM_CASES = [
     (2560, 9728, wide(8, 32, split=3, wn=4)),
     (777, 2560, wide(8, 90, grid=4, wn=4)),
     (1000, 2336, wide(8, 20, split=2, wn=4)),
+    (777, 2560, wide(8, 128, grid=3, wn=4)),    # eight slabs at eight waves
 ]
 
 
@@ -108,7 +109,8 @@ def test_wide_gateup(case, M):
 
 
 @pytest.mark.parametrize("cfg", [wide(4, 64), wide(8, 96), wide(4, 27, grid=64), wide(8, 96, wn=2), wide(4, 128, wn=4),
-                                 wide(4, 27, grid=64, wn=4), wide(8, 96, wn=4)], ids=_ids)
+                                 wide(4, 27, grid=64, wn=4), wide(8, 96, wn=4), wide(8, 128, wn=4),
+                                 wide(8, 128, grid=40, wn=4)], ids=_ids)
 @pytest.mark.parametrize("M", [1, 64, 128])
 def test_wide_lm_argmax(cfg, M):
     """Fused argmax over a 30000-token vocabulary (many tiles per workgroup)."""
@@ -119,3 +121,24 @@ def test_wide_lm_argmax(cfg, M):
     logits = oracle.gemm(bits(x), bits(w))
     o_ids, o_maxv = oracle.argmax(logits)
     check_argmax_rows(ids, maxv, logits, o_ids, o_maxv, f"lm_argmax {cfg} M={M}")
+
+
+@pytest.mark.parametrize("cfg", [wide(4, 128, wn=4), wide(8, 96, wn=4), wide(8, 128, wn=4),
+                                 wide(8, 128, grid=40, wn=4)], ids=_ids)
+def test_wide_lm_argmax_exact_ties(cfg):
+    """Duplicate weight rows give bit-identical logits; the lowest column must
+    win when the copies share a lane's columns, sit in different quarters or
+    slabs of one tile, in adjacent tiles, or in different workgroups."""
+    V, Kd, M = 40_000, 2560, 8
+    w, x = _w(V, Kd, 5), _x(M, Kd, 5)
+    pairs = [(100, 39_000), (7, 8), (20_000, 30_000), (0, V - 1), (45, 110), (130, 131), (31, 33), (255, 256)]
+    for m, (lo, hi) in enumerate(pairs):
+        hot = (x[m].float() * 0.05).to(torch.bfloat16)   # strongly aligned with row m's activations
+        w[lo] = hot
+        w[hi] = hot
+    ids, maxv = K.lm_argmax(x.to(DEV), w.to(DEV), config=cfg)
+    torch.cuda.synchronize()
+    assert ids.cpu().tolist() == [lo for lo, _ in pairs]
+    o_ids, o_maxv = oracle.lm_argmax(bits(x), bits(w))
+    assert (ids.cpu().numpy() == o_ids).all()
+    assert (maxv.cpu().numpy() == o_maxv).all()
