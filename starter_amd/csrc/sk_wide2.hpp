@@ -125,20 +125,23 @@ __device__ __forceinline__ void wide2_body(Args p) {
   u32x4 wreg[D][WLD];
   u32x4 areg[D][ALD];
   // Requests are made in step order, so the weight row addresses follow the
-  // tile of the step being requested.
+  // tile of the step being requested.  Steps past the last (g >= G) request
+  // the zero line: the loop below stages and requests without branches, so
+  // the compiler's wait for a slot's loads leaves the other slot's in flight
+  // (around conditional requests it waited for every load before the next
+  // requests, one step of look-ahead instead of two).
   auto issue = [&](auto slot, int g) {
     constexpr int SL = decltype(slot)::value;
+    const bool live = g < G;
     const int st = step_of(g);
-    if (st == s_lo) set_tile(tile_of(g));   // uniform: the first step of a tile
+    if (live && st == s_lo) set_tile(tile_of(g));   // uniform: the first step of a tile
     const int col0 = st * kW2Step;
-    const bool colok = col0 + 8 * r16 < p.K;
+    const bool colok = live && col0 + 8 * r16 < p.K;
 #pragma unroll
     for (int i = 0; i < WLD; ++i) wreg[SL][i] = ld16_stream(wok[i] && colok ? wbase[i] + col0 : zero16);
 #pragma unroll
     for (int i = 0; i < ALD; ++i) areg[SL][i] = ld16(aok[i] && colok ? abase[i] + col0 : zero16);
   };
-  if (G > 0) issue(std::integral_constant<int, 0>{}, 0);
-  if (G > 1) issue(std::integral_constant<int, 1>{}, 1);
   auto stage = [&](auto slot, int g) {
     constexpr int SL = decltype(slot)::value;
     char* const sb = buf + (g & 1) * (SROWS * kW2Pitch);
@@ -150,8 +153,10 @@ __device__ __forceinline__ void wide2_body(Args p) {
       *reinterpret_cast<u32x4*>(sb + (ROWS + 4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = areg[SL][i];
   };
   if (G > 0) {
+    issue(std::integral_constant<int, 0>{}, 0);
+    issue(std::integral_constant<int, 1>{}, 1);
     stage(std::integral_constant<int, 0>{}, 0);
-    if (G > 2) issue(std::integral_constant<int, 0>{}, 2);
+    issue(std::integral_constant<int, 0>{}, 2);
   }
 
   f32x4 acc[NT][MTW];
@@ -307,10 +312,11 @@ __device__ __forceinline__ void wide2_body(Args p) {
     // buffer, so step g + 1 is staged there beside this step's MFMAs, and
     // its register slot takes the loads of step g + 3.
     lds_barrier();
-    if (g + 1 < G) stage(std::integral_constant<int, (SL + 1) % D>{}, g + 1);
-    if (g + PF < G) issue(std::integral_constant<int, (SL + 1) % D>{}, g + PF);
-    // (a wave whose 32 activation rows all lie past M has nothing to multiply)
-    if (16 * MTW * mw < M) {
+    stage(std::integral_constant<int, (SL + 1) % D>{}, g + 1);
+    issue(std::integral_constant<int, (SL + 1) % D>{}, g + PF);
+    // (a wave whose 32 activation rows all lie past M has nothing to
+    // multiply; step G, run when G is odd, only stages and requests)
+    if (g < G && 16 * MTW * mw < M) {
 #pragma unroll
       for (int uu = 0; uu < UW; ++uu) {
         const int u = kh * UW + uu;
@@ -328,7 +334,7 @@ __device__ __forceinline__ void wide2_body(Args p) {
         }
       }
     }
-    if ((g + 1) % nsteps == 0) {   // the tile's last step
+    if (g < G && (g + 1) % nsteps == 0) {   // the tile's last step
       if constexpr (KH == 2) {
         // Waves 4-7 hand their K half to waves 4 below through this step's
         // buffer: every wave has finished reading it after the barrier, and
@@ -372,7 +378,7 @@ __device__ __forceinline__ void wide2_body(Args p) {
   static_assert(D == 2, "the loop below is unrolled for two slots");
   for (int g0 = 0; g0 < G; g0 += D) {
     step(std::integral_constant<int, 0>{}, g0);
-    if (g0 + 1 < G) step(std::integral_constant<int, 1>{}, g0 + 1);
+    step(std::integral_constant<int, 1>{}, g0 + 1);
   }
 
   if constexpr (BASE == EPI_ARGMAX) {
