@@ -38,7 +38,8 @@ COMMON = [
 
 N_EPI = 5       # EPI_STORE, EPI_SWIGLU, EPI_ARGMAX, EPI_PART, EPI_PART_GU
 NORM_EPIS = (5, 6, 7)   # the first three with the norm prologue (GEMV path only)
-HANDOFF_EPIS = (8, 9, 10, 11, 12)   # residual hand-off consumers and producers (LDS-fed ring path only)
+HANDOFF_EPIS = (8, 9, 10, 11, 12)   # residual hand-off consumers and producers (LDS-fed ring path)
+WIDE_HANDOFF_EPIS = (8, 9, 10, 12)   # the same on the two-operand wide path (no bf16-store producer)
 
 
 def _units() -> list[tuple[Path, list[str], Path]]:
@@ -53,6 +54,8 @@ def _units() -> list[tuple[Path, list[str], Path]]:
         units.append((CSRC / "sk_inst_gemv.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_gemv_{epi}.o"))
     for epi in HANDOFF_EPIS:
         units.append((CSRC / "sk_inst_mfmt.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_mfmt_{epi}.o"))
+    for epi in WIDE_HANDOFF_EPIS:
+        units.append((CSRC / "sk_inst_wide.hip", [f"-DSK_EPI={epi}"], BUILD / f"sk_inst_wide_{epi}.o"))
     return units
 
 

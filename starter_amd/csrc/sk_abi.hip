@@ -189,7 +189,8 @@ int epi_for(int op, int split) {
 // projection (GEMM / GATEUP / LM_ARGMAX); `fused` selects the instances with
 // the norm prologue.
 // variant: 0 plain, 1 residual hand-off consumer (EPI_*_PRE), 2 producer
-// (EPI_*_RESID); both run on the ring-streamed LDS-fed MFMA path only.
+// (EPI_*_RESID); both run on the ring-streamed LDS-fed MFMA path or the
+// two-operand wide path.
 int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused, Plan* pl, int variant = 0) {
   if (!is_gemm_family(op)) return SK_ERR_CONFIG;
   if (M < 1 || M > kMaxLaunchM || N < 1 || K < 32 || (K & 31) != 0) return SK_ERR_SHAPE;
@@ -216,12 +217,22 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
   const bool gateup = (op == SK_OP_GATEUP);
   if (fused && (c.split != 1 || c.path != SK_PATH_GEMV)) return SK_ERR_CONFIG;
   if (variant != 0) {
-    if (fused || c.path != SK_PATH_MFMA_LDS || c.ku == 16) return SK_ERR_CONFIG;
-    // consumers: one K split; the prologue loads each wave's share of the
-    // partial sums in one pass (rows <= 4 per wave, <= 256 groups per row)
-    if (variant == 1 && (c.ku != 8 || c.split != 1 || (K & 15) != 0 || M > 4 * c.waves || K > 4096))
-      return SK_ERR_CONFIG;
+    if (fused) return SK_ERR_CONFIG;
     if (variant == 2 && op != SK_OP_GEMM) return SK_ERR_CONFIG;
+    if (c.path == SK_PATH_WIDE) {
+      // the two-operand wide body: consumers with one K split (whole 16-column
+      // groups of partial sums), the producer after split-K partials (its
+      // tiles are whole 16-column groups, checked below)
+      if (c.groups != 4) return SK_ERR_CONFIG;
+      if (variant == 1 && (c.split != 1 || (K & 15) != 0)) return SK_ERR_CONFIG;
+      if (variant == 2 && (c.split < 2 || (c.rows & 15) != 0)) return SK_ERR_CONFIG;
+    } else {
+      if (c.path != SK_PATH_MFMA_LDS || c.ku == 16) return SK_ERR_CONFIG;
+      // consumers: one K split; the prologue loads each wave's share of the
+      // partial sums in one pass (rows <= 4 per wave, <= 256 groups per row)
+      if (variant == 1 && (c.ku != 8 || c.split != 1 || (K & 15) != 0 || M > 4 * c.waves || K > 4096))
+        return SK_ERR_CONFIG;
+    }
   }
   pl->cfg = c;
   pl->epi = epi_for(op, c.split) + (fused ? sk::EPI_STORE_NORM : 0);
@@ -268,7 +279,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     // groups = 4 selects the body that stages the activation rows in LDS too
     // (four waves, two activation tiles each, every wave on the whole tile).
     const int wn = c.groups > 1 ? c.groups : 1;
-    if (variant != 0 || (wn != 1 && wn != 2 && wn != 4) || (wn == 2 && c.waves != 8)) return SK_ERR_CONFIG;
+    if ((variant != 0 && wn != 4) || (wn != 1 && wn != 2 && wn != 4) || (wn == 2 && c.waves != 8)) return SK_ERR_CONFIG;
     if ((c.waves != 4 && c.waves != 8) || c.ku != 8) return SK_ERR_CONFIG;
     const int max_rows = wn == 4 ? (gateup ? 64 : 128) : (gateup ? (wn == 2 ? 32 : 48) : 96);
     if (c.rows < 1 || c.rows > max_rows) return SK_ERR_CONFIG;
@@ -279,6 +290,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tn = gateup ? 2 * hw : hw;
     if (pl->tn < 2) pl->tn = 2;   // the smallest instance stages two slabs
     if (wn == 4 && (pl->tn == 7 || (c.waves == 8 && (pl->tn & 1)))) pl->tn += 1;   // compiled slab counts
+    if (variant == 2 && 16 * pl->tn != c.rows) return SK_ERR_CONFIG;   // the finish's 16-column groups
     pl->tku = sk::kWideChunk;
     partial_rows = 0;
     pl->pre_lds = wn == 4 ? sk::wide2_lds(pl->tn) : sk::wide_weight_lds(pl->tn);
@@ -399,7 +411,7 @@ const Tuned kTuned[] = {
     {SK_OP_PRE_GEMM, 6144, 2560, 8, {3, 10, 8, 16, 1, 192}},  // qkv consumer  9.07 us (32-row tiles 9.21)
     {SK_OP_PRE_GEMM, 6144, 2560, 16, {3, 10, 8, 16, 1, 0}},  // qkv consumer 10.13 us (32-row tiles 10.50)
     {SK_OP_PRE_GEMM, 6144, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer: 16-row groups (32-row consumers have 8 waves, too few for K)
-    {SK_OP_PRE_GEMM, 6144, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 24.0 us (eight 16-row groups; 30.2 at grid 64)
+    {SK_OP_PRE_GEMM, 6144, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 24.0-26.3 us (eight 16-row groups; 30.2 at grid 64; two-operand wide path 31.3)
     {SK_OP_GEMM, 6144, 2560, 32, {3, 10, 8, 32, 1, 0}},  // qkv       10.22 us  3134 GB/s
     {SK_OP_GEMM, 6144, 2560, 40, {3, 10, 8, 16, 1, 0}},  // qkv       11.34 us  2835 GB/s (half ring)
     {SK_OP_GEMM, 6144, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // qkv       11.33 us  2849 GB/s (two row groups; 12.0 half ring)
@@ -437,7 +449,11 @@ const Tuned kTuned[] = {
     // 42.9 and 38.1 for four row groups (55.9 as two 64-row launches).
     {SK_OP_GATEUP, 9728, 2560, 128, {4, 8, 8, 40, 1, 0, 4}},  // gate_up   36.1 us
     {SK_OP_PRE_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
-    {SK_OP_PRE_GATEUP, 9728, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer 58.7 us (67.3 at grid 64)
+    // consumer at 65-128 rows: the two-operand wide path, 44.1 us at 128 rows
+    // (eight 16-row ring groups 58.7-62.3; an add + RMSNorm launch and then
+    // the plain projection 41.4: every workgroup normalises the whole
+    // activation block while staging it, ~7 us of VALU work per launch)
+    {SK_OP_PRE_GATEUP, 9728, 2560, 128, {4, 8, 8, 48, 1, 0, 4}},
     {SK_OP_GEMM, 2560, 9728, 1, {2, 2, 10, 2, 1, 0}},  // down      10.48 us  4754 GB/s
     // down at M = 3-8: eight waves of five 256-column chunks cover K = 9728
     // without a global split (13.1 -> 12.6 us at M = 8); at M = 2 the GEMV
@@ -476,7 +492,10 @@ const Tuned kTuned[] = {
     // wide body 281 and 269, four row groups 306-309, two 64-row launches 362)
     {SK_OP_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 128, 1, 0, 4}},
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 64, 4}},  // consumer, as for qkv
-    {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {3, 10, 8, 16, 1, 32, 8}},  // consumer, as for qkv
+    // consumer at 65-128 rows: the two-operand wide path, 238.7 us at 128 rows
+    // (eight ring groups 412; the add + RMSNorm launch then the plain
+    // projection 214.7)
+    {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 128, 1, 0, 4}},
     {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
     // lm_head logits at 65-128 rows: as for the fused argmax, 209 us at 128
     // rows and 193 at 96 (96-row tiles 243 and 229, four row groups 304-342)

@@ -1,4 +1,5 @@
-// Wide-M kernel instances (sk_wide.hpp) for one epilogue (-DSK_EPI=<0..4>).
+// Wide-M kernel instances (sk_wide.hpp, sk_wide2.hpp) for one epilogue
+// (-DSK_EPI=<0..4, 8..10, 12>).
 #include "sk_registry.hpp"
 
 #ifndef SK_EPI
@@ -31,7 +32,15 @@ __global__ void __launch_bounds__(64 * W) wide2_entry(Args p) {
 // WN = 4: the two-operand body)
 KernelFn SK_CAT(wide_for_epi, SK_EPI)(int W, int WN, int NT) {
   switch (W * 1000 + WN * 100 + NT) {
-#if SK_EPI == 1 || SK_EPI == 4   // gate/up: NT/2 gate slabs + NT/2 up slabs
+#if SK_EPI == 8   // residual hand-off (two-operand body only): consumers, then the producer
+    SK_W2(8, 2) SK_W2(8, 4) SK_W2(8, 6)
+#elif SK_EPI == 9
+    SK_W2(8, 4) SK_W2(8, 6)
+#elif SK_EPI == 10
+    SK_W2(8, 6) SK_W2(8, 8)
+#elif SK_EPI == 12
+    SK_W2(8, 2) SK_W2(8, 4)
+#elif SK_EPI == 1 || SK_EPI == 4   // gate/up: NT/2 gate slabs + NT/2 up slabs
     SK_W(4, 1, 2) SK_W(4, 1, 4) SK_W(4, 1, 6)
     SK_W(8, 1, 2) SK_W(8, 1, 4) SK_W(8, 1, 6)
     SK_W(8, 2, 4)

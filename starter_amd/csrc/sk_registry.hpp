@@ -111,6 +111,10 @@ KernelFn wide_for_epi1(int W, int WN, int NT);
 KernelFn wide_for_epi2(int W, int WN, int NT);
 KernelFn wide_for_epi3(int W, int WN, int NT);
 KernelFn wide_for_epi4(int W, int WN, int NT);
+KernelFn wide_for_epi8(int W, int WN, int NT);
+KernelFn wide_for_epi9(int W, int WN, int NT);
+KernelFn wide_for_epi10(int W, int WN, int NT);
+KernelFn wide_for_epi12(int W, int WN, int NT);
 KernelFn gemv_for_epi0(int MR, int R, int KU);
 KernelFn gemv_for_epi1(int MR, int R, int KU);
 KernelFn gemv_for_epi2(int MR, int R, int KU);
@@ -173,6 +177,10 @@ inline KernelFn wide_kernel_for(int epi, int W, int WN, int NT) {
     case EPI_ARGMAX: return wide_for_epi2(W, WN, NT);
     case EPI_PART: return wide_for_epi3(W, WN, NT);
     case EPI_PART_GU: return wide_for_epi4(W, WN, NT);
+    case EPI_STORE_PRE: return wide_for_epi8(W, WN, NT);
+    case EPI_SWIGLU_PRE: return wide_for_epi9(W, WN, NT);
+    case EPI_ARGMAX_PRE: return wide_for_epi10(W, WN, NT);
+    case EPI_PART_RESID: return wide_for_epi12(W, WN, NT);
   }
   return nullptr;
 }

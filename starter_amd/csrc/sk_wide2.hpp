@@ -28,7 +28,11 @@
 //
 // Epilogues and the cross-workgroup finishes are those of sk_wide.hpp: bf16
 // store, SwiGLU, fused argmax (per-row LDS bests, then argmax_fixup), split-K
-// partials finished in-kernel by the last workgroup of each tile.
+// partials finished in-kernel by the last workgroup of each tile.  The
+// residual hand-off runs here too: a producer (split-K partials) finishes
+// xout = r + y with the per-row partial sums of squares of xout, and a
+// consumer normalises the activation rows as it stages them, with row norms
+// from those partial sums.
 #pragma once
 
 #include "sk_wide.hpp"
@@ -47,7 +51,10 @@ template <int W, int NT, int EPI>
 __device__ __forceinline__ void wide2_body(Args p) {
   constexpr bool GATEUP = EpiTraits<EPI>::gateup;
   constexpr int BASE = EpiTraits<EPI>::base;
-  static_assert(!EpiTraits<EPI>::norm && !EpiTraits<EPI>::pre && !EpiTraits<EPI>::resid, "plain epilogues only");
+  constexpr bool PRE = EpiTraits<EPI>::pre;       // consumer: normalise the rows while staging them
+  constexpr bool RESID = EpiTraits<EPI>::resid;   // producer: the split-K finish hands the residual on
+  static_assert(!EpiTraits<EPI>::norm, "the norm prologue with an add runs on the GEMV path");
+  static_assert(!RESID || BASE == EPI_PART, "the residual hand-off follows split-K partials");
   static_assert(!GATEUP || NT % 2 == 0, "gate/up tiles pair NT/2 gate slabs with NT/2 up slabs");
   static_assert(W == 4 || W == 8, "four waves, or eight splitting each step's K units in two");
   constexpr int KH = W / 4;                  // K halves of a step (waves w and w + 4 share tiles)
@@ -124,6 +131,9 @@ __device__ __forceinline__ void wide2_body(Args p) {
 
   u32x4 wreg[D][WLD];
   u32x4 areg[D][ALD];
+  // PRE: the norm weights of the lane's eight columns of the step (the same
+  // for every row), requested with the step's rows.
+  u32x4 nreg[PRE ? D : 1];
   // Requests are made in step order, so the weight row addresses follow the
   // tile of the step being requested.  Steps past the last (g >= G) request
   // the zero line: the loop below stages and requests without branches, so
@@ -141,6 +151,43 @@ __device__ __forceinline__ void wide2_body(Args p) {
     for (int i = 0; i < WLD; ++i) wreg[SL][i] = ld16_stream(wok[i] && colok ? wbase[i] + col0 : zero16);
 #pragma unroll
     for (int i = 0; i < ALD; ++i) areg[SL][i] = ld16(aok[i] && colok ? abase[i] + col0 : zero16);
+    if constexpr (PRE) nreg[SL] = ld16(colok ? p.NW + col0 + 8 * r16 : zero16);
+  };
+  // PRE: rstd of each staged activation row of this lane, from the
+  // producer's partial sums of squares (K/16 per row, row stride sq_ld): the
+  // row's 16 lanes sum every 16th group each, in increasing group order,
+  // then a butterfly over the 16 lanes (a fixed order); rows past M sum
+  // nothing and are never used.
+  float rst[PRE ? ALD : 1];
+  auto row_norms = [&]() {
+    const int ngrp = p.K >> 4;
+    float t[ALD];
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) t[i] = 0.f;
+    for (int g0 = r16; g0 < ngrp; g0 += 16 * 4) {
+      float v[ALD][4];
+#pragma unroll
+      for (int i = 0; i < ALD; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int gi = g0 + 16 * k;
+          const int ar = 4 * (wave + W * i) + g4;
+          v[i][k] = (aok[i] && gi < ngrp) ? p.SQ[(int64_t)ar * p.sq_ld + gi] : 0.f;
+        }
+#pragma unroll
+      for (int i = 0; i < ALD; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) t[i] += v[i][k];
+    }
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) {
+      float u = t[i];
+      u += __shfl_xor(u, 1);
+      u += __shfl_xor(u, 2);
+      u += __shfl_xor(u, 4);
+      u += __shfl_xor(u, 8);
+      rst[i] = rms_rstd(u, p.K, p.eps);
+    }
   };
   auto stage = [&](auto slot, int g) {
     constexpr int SL = decltype(slot)::value;
@@ -148,13 +195,29 @@ __device__ __forceinline__ void wide2_body(Args p) {
 #pragma unroll
     for (int i = 0; i < WLD; ++i)
       *reinterpret_cast<u32x4*>(sb + (4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = wreg[SL][i];
+    // PRE: A = bf16(w * bf16(x * rstd)) (the cast placement of
+    // engine/kernels/gemm.py:28-56); zero lines stay zero
+    u32x4 wlo, whi;
+    if constexpr (PRE) {
 #pragma unroll
-    for (int i = 0; i < ALD; ++i)
-      *reinterpret_cast<u32x4*>(sb + (ROWS + 4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = areg[SL][i];
+      for (int q = 0; q < 4; ++q) {
+        wlo[q] = nreg[SL][q] & 0xFFFFu;
+        whi[q] = nreg[SL][q] & 0xFFFF0000u;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < ALD; ++i) {
+      u32x4 v = areg[SL][i];
+      if constexpr (PRE) v = norm_line_bf16x8(v, wlo, whi, rst[i]);
+      *reinterpret_cast<u32x4*>(sb + (ROWS + 4 * (wave + W * i) + g4) * kW2Pitch + 16 * r16) = v;
+    }
   };
   if (G > 0) {
     issue(std::integral_constant<int, 0>{}, 0);
     issue(std::integral_constant<int, 1>{}, 1);
+    // (the partial sums are requested after the first two steps' rows: the
+    // first staging waits for those anyway)
+    if constexpr (PRE) row_norms();
     stage(std::integral_constant<int, 0>{}, 0);
     issue(std::integral_constant<int, 0>{}, 2);
   }
@@ -385,7 +448,7 @@ __device__ __forceinline__ void wide2_body(Args p) {
     lds_barrier();
     argmax_fixup(p, lds_best, reinterpret_cast<int*>(lds_best + M));
   } else if constexpr (BASE == EPI_PART || BASE == EPI_PART_GU) {
-    splitk_fixup<HROWS, BASE>(p, ntiles, rb0, reinterpret_cast<int*>(tail));
+    splitk_fixup<HROWS, BASE, RESID>(p, ntiles, rb0, reinterpret_cast<int*>(tail));
   }
 }
 

@@ -468,6 +468,35 @@ def test_handoff_rejects_unsupported_configs():
     assert _lib.check_config(SK_OP_RESID_GEMM, 8, 2560, 9728, SkConfig.make(_LDS, 4, 32, 32, 3)) == SK_OK
 
 
+def test_handoff_on_the_two_operand_wide_path():
+    """Above 64 rows the hand-off ops also run on the two-operand wide path
+    (groups = 4): producers after split-K partials, with tiles of whole
+    16-column groups (the finish writes one partial sum per group), consumers
+    with one K split.  The other wide bodies take no hand-off."""
+    def w2(rows, split=1, waves=8, groups=4):
+        return SkConfig.make(_lib.SK_PATH_WIDE, waves, 8, rows, split, 0, groups)
+    for M in (65, 100, 128):
+        assert _lib.check_config(SK_OP_RESID_GEMM, M, 2560, 4096, w2(32, 3)) == SK_OK
+        assert _lib.check_config(SK_OP_RESID_GEMM, M, 2560, 9728, w2(64, 2)) == SK_OK
+        assert _lib.check_config(SK_OP_RESID_GEMM, M, 2560, 4096, w2(32, 1)) == SK_ERR_CONFIG   # no split-K
+        assert _lib.check_config(SK_OP_RESID_GEMM, M, 2560, 4096, w2(40, 3)) == SK_ERR_CONFIG   # 40-row tiles
+        assert _lib.check_config(SK_OP_RESID_GEMM, M, 2560, 4096, w2(48, 3)) == SK_ERR_CONFIG   # 48 in 4 slabs
+        assert _lib.check_config(SK_OP_RESID_GEMM, M, 2560, 4096, w2(32, 3, groups=1)) == SK_ERR_CONFIG
+        assert _lib.check_config(SK_OP_PRE_GEMM, M, 6144, 2560, w2(32)) == SK_OK
+        assert _lib.check_config(SK_OP_PRE_GEMM, M, 6144, 2560, w2(32, 2)) == SK_ERR_CONFIG    # consumers: one split
+        assert _lib.check_config(SK_OP_PRE_GATEUP, M, 9728, 2560, w2(48)) == SK_OK
+        assert _lib.check_config(SK_OP_PRE_LM_ARGMAX, M, 151936, 2560, w2(128)) == SK_OK
+        assert _lib.check_config(SK_OP_PRE_GEMM, M, 6144, 2560, w2(32, waves=4)) == SK_ERR_CONFIG  # not compiled
+    # defaults at 65-128 rows: the producers take the projection's wide entry,
+    # the gate/up and lm_head consumers their own wide entries
+    for name in ("o_resid", "d_resid", "gu_pre", "lm_pre"):
+        op, N, K, base = HANDOFF[name]
+        cfg = _lib.default_config(op, 128, N, K)
+        assert cfg.path == _lib.SK_PATH_WIDE and cfg.groups == 4, name
+        assert _lib.workspace_bytes(op, 128, N, K, cfg) == _lib.workspace_bytes(base, 128, N, K, cfg)
+    assert _lib.default_config(SK_OP_PRE_GEMM, 128, 6144, 2560).path == _LDS
+
+
 R0, RO0, SQ0 = FAKE + (1 << 29), FAKE + (1 << 29) + (1 << 22), FAKE + (1 << 29) + (2 << 22)
 
 

@@ -142,3 +142,122 @@ def test_wide_lm_argmax_exact_ties(cfg):
     o_ids, o_maxv = oracle.lm_argmax(bits(x), bits(w))
     assert (ids.cpu().numpy() == o_ids).all()
     assert (maxv.cpu().numpy() == o_maxv).all()
+
+
+# ---------------------------------------------------------------------------
+# Residual hand-off on the two-operand wide path (groups = 4): the producer
+# after split-K partials, the consumers normalising rows while staging them.
+# ---------------------------------------------------------------------------
+
+HID, EPS = 2560, 1e-6
+
+
+def _sums16(ro: torch.Tensor) -> torch.Tensor:
+    """fp64 sums of squares over 16-column groups of an [M, N] bf16 tensor."""
+    M, N = ro.shape
+    G = (N + 15) // 16
+    f = torch.zeros((M, G * 16), dtype=torch.float64)
+    f[:, :N] = ro.double()
+    return f.pow(2).view(M, G, 16).sum(-1)
+
+
+def _exact(shape, seed):
+    """Values in {0, +-0.5, ..., +-2}: every partial sum of squares is exact in
+    fp32, so a row's rstd does not depend on the summation order."""
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randint(-4, 5, shape, generator=g).float() * 0.5).to(torch.bfloat16)
+
+
+def _gain(seed):
+    g = torch.Generator().manual_seed(seed)
+    return (1 + 0.1 * torch.randn(HID, generator=g)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("N,Kd,cfg", [
+    (2560, 4096, wide(8, 32, split=3, wn=4)),   # o_proj
+    (2560, 9728, wide(8, 32, split=3, wn=4)),   # down
+    (2560, 4096, wide(8, 64, split=2, wn=4)),   # four slabs per tile
+    (200, 512, wide(8, 32, split=2, wn=4)),     # ragged N: the last tile's columns past N
+], ids=lambda v: v if isinstance(v, int) else _ids(v))
+@pytest.mark.parametrize("M", [128, 100, 33])
+def test_wide_gemm_residual_bit_exact_against_gemm_plus_add(N, Kd, cfg, M):
+    """r_out = bf16(r + y) bit for bit with y the plain wide GEMM of the same
+    configuration (same split-K sum order), sums of squares against fp64."""
+    a, w, r = _x(M, Kd, 80), _w(N, Kd, 81), _x(M, N, 82)
+    ad, wd, rd = a.to(DEV), w.to(DEV), r.to(DEV)
+    y = K.gemm(ad, wd, config=cfg)
+    ro = torch.empty_like(rd)
+    sq = torch.full((M, K.sumsq_groups(M, N)), float("nan"), dtype=torch.float32, device=DEV)
+    K.gemm_residual(ad, wd, rd, ro, sq, config=cfg)
+    torch.cuda.synchronize()
+    assert_parity(y, from_bits(oracle.gemm(bits(a), bits(w))), f"projection N={N} M={M} {cfg}")
+    want = (r.float() + y.cpu().float()).to(torch.bfloat16)
+    assert torch.equal(ro.cpu().view(torch.int16), want.view(torch.int16)), f"residual N={N} M={M}"
+    got, ref = sq.cpu().double(), _sums16(want)
+    assert torch.all(torch.isfinite(got))
+    assert torch.allclose(got, ref, rtol=2e-6, atol=0), (got - ref).abs().max().item()
+
+
+PRE_CASES = [
+    ("qkv", wide(8, 48, wn=4)),       # 48-row tiles in four slabs (two waves per 32 rows)
+    ("qkv", wide(8, 24, wn=4)),
+    ("gate_up", wide(8, 40, wn=4)),
+    ("gate_up", wide(8, 24, wn=4)),
+    ("lm_argmax", wide(8, 128, wn=4)),
+    ("lm_argmax", wide(8, 96, grid=64, wn=4)),
+]
+
+
+def _consume(kind, xd, sq, wnd, wd, cfg, pre: bool):
+    """The consumer (pre=True) or the unfused pipeline: add + RMSNorm launch,
+    then the projection with the same configuration."""
+    if kind == "qkv":
+        if pre:
+            return K.rmsnorm_pre_gemm(xd, sq, wnd, EPS, wd, config=cfg)
+        return K.rmsnorm_gemm(xd, torch.zeros_like(xd), wnd, EPS, torch.empty_like(xd), wd, config=cfg)
+    if kind == "gate_up":
+        I = wd.shape[0] // 2
+        if pre:
+            return K.rmsnorm_pre_gateup_swiglu(xd, sq, wnd, EPS, wd[:I], wd[I:], config=cfg)
+        return K.rmsnorm_gateup_swiglu(xd, torch.zeros_like(xd), wnd, EPS, torch.empty_like(xd), wd[:I], wd[I:],
+                                       config=cfg)
+    if pre:
+        return K.rmsnorm_pre_lm_argmax(xd, sq, wnd, EPS, wd, config=cfg)
+    return K.rmsnorm_lm_argmax(xd, torch.zeros_like(xd), wnd, EPS, torch.empty_like(xd), wd, config=cfg)
+
+
+_PRE_N = {"qkv": 6144, "gate_up": 2 * 9728, "lm_argmax": 30000}
+
+
+@pytest.mark.parametrize("kind,cfg", PRE_CASES, ids=lambda v: v if isinstance(v, str) else _ids(v))
+@pytest.mark.parametrize("M", [128, 77])
+def test_wide_pre_exact_stats_equals_unfused_pipeline(kind, cfg, M):
+    x, wn, w = _exact((M, HID), 90 + M), _gain(91), _w(_PRE_N[kind], HID, 92)
+    xd, wnd, wd = x.to(DEV), wn.to(DEV), w.to(DEV)
+    got = _consume(kind, xd, _sums16(x).float().to(DEV), wnd, wd, cfg, pre=True)
+    ref = _consume(kind, xd, None, wnd, wd, cfg, pre=False)
+    torch.cuda.synchronize()
+    if kind == "lm_argmax":
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1])
+    else:
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("kind,cfg", PRE_CASES, ids=lambda v: v if isinstance(v, str) else _ids(v))
+@pytest.mark.parametrize("M", [128, 50])
+def test_wide_pre_random_against_oracle(kind, cfg, M):
+    import numpy as np
+
+    x, wn, w = _x(M, HID, 95), _gain(96), _w(_PRE_N[kind], HID, 97)
+    got = _consume(kind, x.to(DEV), _sums16(x).float().to(DEV), wn.to(DEV), w.to(DEV), cfg, pre=True)
+    torch.cuda.synchronize()
+    _, h = oracle.add_rmsnorm(bits(x), np.zeros_like(bits(x)), bits(wn), EPS)
+    what = f"pre {kind} M={M} {cfg}"
+    if kind == "qkv":
+        assert_parity(got, from_bits(oracle.gemm(h, bits(w))), what)
+    elif kind == "gate_up":
+        I = w.shape[0] // 2
+        assert_gateup_parity(got, h, bits(w[:I]), bits(w[I:]), what)
+    else:
+        o_ids, o_max = oracle.lm_argmax(h, bits(w))
+        check_argmax_rows(got[0], got[1], oracle.gemm(h, bits(w)), o_ids, o_max, what)
