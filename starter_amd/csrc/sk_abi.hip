@@ -269,7 +269,7 @@ int plan_shape_impl(int op, int M, int N, int K, const sk_config& c, bool fused,
     pl->tku = KW;
     partial_rows = 16 * pl->tn;
     if (c.waves > sk::instance_waves(sk::KIND_MFMT, pl->tm, pl->tn, KW, pl->epi)) return SK_ERR_CONFIG;
-    pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + 16);
+    pl->pre_lds = (size_t)c.waves * 16 * (2 * 256 + sk::kRowPad);
   } else if (c.path == SK_PATH_WIDE) {
     // All rows in one workgroup: W = 4 or 8 waves split the (up to 8)
     // 16-row activation tiles, every wave multiplies the whole weight tile

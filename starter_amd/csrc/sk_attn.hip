@@ -293,13 +293,13 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a
   // of key 4j + l/16 for K and of key 4*(l/16) + j for V.
   //  * Scores: S^T[key][row] = K[16 keys, 128] . Q^T by four MFMAs with K as
   //    the A operand (lane l: key l%16, dims 32s + 8*(l/16)); the wave's K rows
-  //    pass through its own LDS tile (rows padded to 272 bytes, so neither the
+  //    pass through its own LDS tile (rows padded to 288 bytes, so neither the
   //    row writes nor the column reads conflict) into that layout.  Lane l then
   //    holds keys 4*(l/16) + i (i < 4) of query row l%16.
   //  * P.V: lane l's V loads hold keys 4*(l/16) + j, the keys of its scores.
   // The next blocks' rows are loaded while the current one is processed
   // (keys past `end` reload the last valid row and are masked).
-  constexpr int KPITCH = 2 * HEAD_D + 16;
+  constexpr int KPITCH = 2 * HEAD_D + kRowPad;
   __shared__ __attribute__((aligned(16))) char s_k[ATTN_WAVES][16 * KPITCH];
   char* const ktile = s_k[wave];
   const int64_t kv_row0 = (int64_t)bk * a.cap;

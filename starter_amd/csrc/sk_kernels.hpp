@@ -183,6 +183,14 @@ __device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
 // the loaded data.
 static __device__ __attribute__((aligned(128))) uint32_t kZeroLine[32] = {};
 
+// Padding of every LDS row that holds MFMA fragment data (a lane reads 16
+// bytes of row r16 at column byte 64u + 16 g4).  On gfx950 those reads run at
+// the full LDS rate when the row pitch in dwords is 8 or 24 mod 32 and at
+// ~60% of it when it is 4 mod 32 (measured with eight waves per CU: 288- and
+// 544-byte rows 367-382 B/ns per CU like linear reads, 272- and 528-byte rows
+// 230-241, 384-byte rows 139), so 256- and 512-byte rows get 32 bytes.
+constexpr int kRowPad = 32;
+
 // Data read once per call (weights, K/V cache rows): non-temporal loads, so it
 // does not evict the activations and partials from L2/MALL.
 __device__ __forceinline__ u32x4 ld16_stream(const uint16_t* p) {
@@ -790,7 +798,7 @@ __device__ __forceinline__ void mfmt_tile_body(Args p) {
   constexpr int RPI = 64 / LPR;                  // rows per load instruction
   constexpr int NLD = ROWS / RPI;                // load instructions per tile (all NT row tiles)
   constexpr int PASSES = KW / 256;               // a 512-column chunk is staged in two halves
-  constexpr int PITCH = 2 * 256 + 16;            // LDS bytes per staged row (256 columns)
+  constexpr int PITCH = 2 * 256 + kRowPad;       // LDS bytes per staged row (256 columns)
   static_assert(KW == 512 || KW == 256, "one or two rows per load instruction");
   static_assert(!GATEUP || NT == 2, "gate/up tiles pair 16 gate rows with 16 up rows");
 
@@ -999,7 +1007,7 @@ __device__ __forceinline__ void mfmt_ring_body(Args p, unsigned bid) {
   constexpr int UNITS = CW / 32;                 // MFMA K steps per slab
   constexpr int RING = 8;                        // load instructions per 16-row slab
   constexpr int RSLOTS = ring_slots(MT, CPW);    // of which in flight (ring registers)
-  constexpr int PITCH = 2 * CW + 16;             // LDS bytes per staged row
+  constexpr int PITCH = 2 * CW + kRowPad;        // LDS bytes per staged row
 
   extern __shared__ __attribute__((aligned(16))) float lds[];
   const int tid = threadIdx.x;

@@ -13,7 +13,7 @@
 //    tr up rows) and one K slice, and walks the slice in 256-column steps.
 //  * Each step's weight rows are loaded row-contiguous by all W waves (one
 //    load instruction = 512 B of each of two rows, the access pattern of the
-//    ring path), written once into one of two LDS buffers (row pitch 528 B:
+//    ring path), written once into one of two LDS buffers (row pitch 544 B:
 //    fragment reads are conflict-free) and read back as MFMA A fragments by
 //    every wave.
 //  * The waves split the activation rows: wave w owns the 16-row activation
@@ -43,7 +43,7 @@
 namespace sk {
 
 constexpr int kWideChunk = 256;                  // K columns per step
-constexpr int kWidePitch = 2 * kWideChunk + 16;  // LDS bytes per staged weight row
+constexpr int kWidePitch = 2 * kWideChunk + kRowPad;  // LDS bytes per staged weight row
 
 // LDS bytes of a wide instance: two weight buffers, then the argmax row bests
 // or the split-K ticket flags.

@@ -9,7 +9,7 @@
 // streams, not HBM, set its time.  Here:
 //
 //  * Each 128-column step stages the tile's weight rows AND the 128
-//    activation rows in LDS (one 272-byte row per staged row: fragment reads
+//    activation rows in LDS (one 288-byte row per staged row: fragment reads
 //    of 16 consecutive rows are conflict-free), loaded row-contiguous by all
 //    four waves (one instruction = 256 B of each of four rows).
 //  * Wave w holds the fp32 accumulators of activation tiles 2(w % 4) and
@@ -40,7 +40,7 @@
 namespace sk {
 
 constexpr int kW2Step = 128;                  // K columns per step
-constexpr int kW2Pitch = 2 * kW2Step + 16;    // LDS bytes per staged row
+constexpr int kW2Pitch = 2 * kW2Step + kRowPad;   // LDS bytes per staged row
 constexpr int kW2Rows = 128;                  // activation rows staged per step (M <= 128)
 
 // LDS bytes of a two-operand wide instance: two buffers of the weight tile's
