@@ -465,7 +465,9 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
-    {SK_OP_GEMM, 2560, 9728, 64, {3, 8, 8, 32, 5, 0}},  // down      23.37 us  2199 GB/s
+    // 49-64 rows: the two-operand wide path (20.2-20.6 us; the ring path
+    // with five K splits 22.8-23.7)
+    {SK_OP_GEMM, 2560, 9728, 64, {4, 8, 8, 32, 3, 0, 4}},  // down      20.58 us
     // 65-128 rows: the two-operand wide path, three K splits of 32-row tiles:
     // 34.4 us at 128 rows, 30.7 at 96 (four row groups with four splits 38.5
     // and 35.7; six splits of 64-row tiles within 0.4 us at twice the
@@ -485,7 +487,9 @@ const Tuned kTuned[] = {
     {SK_OP_LM_ARGMAX, 151936, 2560, 32, {3, 5, 16, 16, 1, 0}},  // lm_head  119.79 us  6495 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 40, {3, 10, 8, 16, 1, 0}},  // lm_head  129.22 us  6022 GB/s (half ring)
     {SK_OP_LM_ARGMAX, 151936, 2560, 48, {3, 10, 8, 16, 1, 0}},  // lm_head  139.09 us  5594 GB/s (half ring)
-    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // lm_head  181.3 us  4292 GB/s (two row groups; 219 without)
+    // 49-64 rows: the two-operand wide path over 128-row tiles (152-154 us;
+    // two ring row groups 155-162, one 219)
+    {SK_OP_LM_ARGMAX, 151936, 2560, 64, {4, 8, 8, 128, 1, 0, 4}},  // lm_head  153.8 us
     // lm_head + argmax at 65-128 rows: the two-operand wide path, every row
     // in one workgroup of eight waves over 128-row weight tiles (218 us at
     // 128 rows, 212 at 96; 96-row tiles 242 and 234, the weights-only-in-LDS
@@ -496,7 +500,12 @@ const Tuned kTuned[] = {
     // (eight ring groups 412; the add + RMSNorm launch then the plain
     // projection 214.7)
     {SK_OP_PRE_LM_ARGMAX, 151936, 2560, 128, {4, 8, 8, 128, 1, 0, 4}},
-    {SK_OP_GEMM, 151936, 2560, 64, {3, 10, 8, 16, 1, 256, 2}},  // lm_head logits: 37 staged tiles per workgroup fit the LDS
+    // lm_head logits at 33-64 rows: the two-operand wide path over 128-row
+    // tiles (138-159 us; the ring plans of the fused argmax's entries store
+    // logits at 139-185, two ring row groups 174-178)
+    {SK_OP_GEMM, 151936, 2560, 40, {4, 8, 8, 128, 1, 0, 4}},
+    {SK_OP_GEMM, 151936, 2560, 48, {4, 8, 8, 128, 1, 0, 4}},
+    {SK_OP_GEMM, 151936, 2560, 64, {4, 8, 8, 128, 1, 0, 4}},
     // lm_head logits at 65-128 rows: as for the fused argmax, 209 us at 128
     // rows and 193 at 96 (96-row tiles 243 and 229, four row groups 304-342)
     {SK_OP_GEMM, 151936, 2560, 128, {4, 8, 8, 128, 1, 0, 4}},

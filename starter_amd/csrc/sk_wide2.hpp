@@ -23,8 +23,9 @@
 //    gate_up at 128 rows 47.5 us against 36.1 with eight).
 //  * Global loads run ahead in a two-slot register ring (the steps of
 //    successive tiles form one sequence), LDS is double-buffered with one
-//    barrier per step: right after step g's barrier a wave stages step g + 1
-//    into the other buffer, which every wave finished reading at step g - 1.
+//    barrier per step: after step g's barrier a wave issues step g's MFMAs,
+//    then stages step g + 1 into the other buffer, which every wave finished
+//    reading at step g - 1.
 //
 // Epilogues and the cross-workgroup finishes are those of sk_wide.hpp: bf16
 // store, SwiGLU, fused argmax (per-row LDS bests, then argmax_fixup), split-K
@@ -68,11 +69,15 @@ __device__ __forceinline__ void wide2_body(Args p) {
   constexpr int ALD = kW2Rows / (4 * W);     // activation load instructions per wave and step
   static_assert(ROWS % (4 * W) == 0, "weight loads split evenly over the waves");
   constexpr int UW = UNITS / KH;             // MFMA K steps of one wave per step
-  // Step g + 1 is staged right after step g's barrier, beside step g's
-  // MFMAs (staging before the barrier, as sk_wide.hpp does, left the LDS
-  // writes and the MFMAs of a step in separate phases: gate_up at 128 rows
-  // 36.0 against 34.0 us); two register slots, each step's loads requested
-  // while the step three ahead of it is multiplied.
+  // A wave issues step g's MFMAs right after step g's barrier and only then
+  // stages step g + 1 (which waits for that step's loads) and requests step
+  // g + 3 into the freed register slot: the MFMAs already issued run while
+  // the wave waits.  Staging first held every MFMA of the step behind the
+  // wait (at 64 rows lm_head + argmax 192 -> 155 us, gate_up 30.1 -> 26.5; at
+  // 96 rows 205 -> 180 and 32.9 -> 29.4; at 128 rows within 1-2%).  Two
+  // register slots: a third, with each step's loads requested at its start,
+  // was slower at every row count (more requests in flight: gate_up at 128
+  // rows 38.8 against 34.0 us).
   constexpr int D = 2, PF = 3;
 
   extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -372,11 +377,9 @@ __device__ __forceinline__ void wide2_body(Args p) {
     char* const sb = buf + (g & 1) * (SROWS * kW2Pitch);
     // Step g's rows are staged (by the previous step or the prologue).  After
     // the barrier every wave has finished step g - 1's reads of the other
-    // buffer, so step g + 1 is staged there beside this step's MFMAs, and
-    // its register slot takes the loads of step g + 3.
+    // buffer, so step g + 1 is staged there after this step's MFMAs are
+    // issued, and its register slot then takes the loads of step g + 3.
     lds_barrier();
-    stage(std::integral_constant<int, (SL + 1) % D>{}, g + 1);
-    issue(std::integral_constant<int, (SL + 1) % D>{}, g + PF);
     // (a wave whose 32 activation rows all lie past M has nothing to
     // multiply; step G, run when G is odd, only stages and requests)
     if (g < G && 16 * MTW * mw < M) {
@@ -397,6 +400,8 @@ __device__ __forceinline__ void wide2_body(Args p) {
         }
       }
     }
+    stage(std::integral_constant<int, (SL + 1) % D>{}, g + 1);
+    issue(std::integral_constant<int, (SL + 1) % D>{}, g + PF);
     if (g < G && (g + 1) % nsteps == 0) {   // the tile's last step
       if constexpr (KH == 2) {
         // Waves 4-7 hand their K half to waves 4 below through this step's
