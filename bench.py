@@ -39,6 +39,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep [--wide]] [-
        python bench.py --probe --probe-op OP --M M      (launches for rocprofv3 --pmc)
        python bench.py --counters-from FOLDER           (markdown table of the counter passes)
        python bench.py --traffic-from FETCH_DIR WRITE_DIR --M M
+       python bench.py --trace-from FOLDER [--trace-passes]  (markdown tables of a kernel trace)
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
 
@@ -500,6 +501,46 @@ def trace_summary(folder: str, regex: str = "sk::", per: int = 0) -> int:
     return 0
 
 
+def trace_passes(folder: str, marker: str = "decode_attn_kernel<16") -> int:
+    """The verify passes of a ``--decode-only`` kernel trace, one markdown row
+    per (pass, kernel instance, launch shape, occurrence within the layer).
+    Launches are taken in start order from the first ``marker`` launch (the
+    tree attention, one per layer) on; each marker launch starts a layer, its
+    grid names the pass (workgroups of the attention), and a kernel's k-th
+    launch since the last marker is occurrence k (o_proj and down share one
+    wide instance: occurrences 1 and 2).  The kernel before the first marker
+    of a replay (the layer-0 qkv) and the lm_head launch after the last layer
+    count as occurrences of the preceding layer."""
+    import csv
+    import re
+
+    rows = []
+    for f in sorted(Path(folder).rglob("*kernel_trace.csv")):
+        with open(f, newline="") as fh:
+            rows += [r for r in csv.DictReader(fh) if "sk::" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    start = next((i for i, r in enumerate(rows) if marker in r["Kernel_Name"]), None)
+    if start is None:
+        print(f"no launch of {marker} in {folder}")
+        return 1
+    groups: dict = {}
+    pass_grid, seen = None, {}
+    for r in rows[start:]:
+        name = re.sub(r"^void ", "", r["Kernel_Name"]).split("(")[0]
+        wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]) // max(wg, 1)
+        if marker in name:
+            pass_grid, seen = grid, {}
+        k = seen[(name, grid)] = seen.get((name, grid), 0) + 1
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0
+        groups.setdefault((pass_grid, name, grid, k), []).append(us)
+    print("| pass (attention workgroups) | kernel | workgroups | occurrence | launches | avg us | median us |")
+    print("|---:|---|---:|---:|---:|---:|---:|")
+    for (pg, name, grid, k), us in groups.items():
+        print(f"| {pg} | `{name}` | {grid} | {k} | {len(us)} | {statistics.mean(us):.2f} | {statistics.median(us):.2f} |")
+    return 0
+
+
 def counters_summary(folder: str) -> int:
     """One markdown row per probe from the counter passes of ``--probe`` runs
     laid out as <folder>/<op>_m<M>_{kt,A,B,C,D} (kernel trace, then the four
@@ -841,6 +882,8 @@ def main() -> int:
                          "FOLDER and exit (--trace-regex, --trace-per)")
     ap.add_argument("--trace-regex", default="sk::", help="kernel-name pattern for --trace-from")
     ap.add_argument("--trace-per", type=int, default=0, help="with --trace-from: units to divide totals by")
+    ap.add_argument("--trace-passes", action="store_true",
+                    help="with --trace-from on a --decode-only trace: the verify passes by pass and layer position")
     ap.add_argument("--counters-from", metavar="FOLDER",
                     help="print a markdown row per probe from the rocprofv3 passes under FOLDER "
                          "(<op>_m<M>_kt, _A, _B, _C, _D) and exit")
@@ -848,6 +891,8 @@ def main() -> int:
     if args.counters_from:
         return counters_summary(args.counters_from)
     if args.trace_from:
+        if args.trace_passes:
+            return trace_passes(args.trace_from)
         return trace_summary(args.trace_from, args.trace_regex, args.trace_per)
     if args.traffic_from:
         return traffic_summary(args.traffic_from[0], args.traffic_from[1], args.M, args.probe_op)
