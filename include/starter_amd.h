@@ -99,10 +99,12 @@ typedef enum sk_path {
  *            1..48 gate rows and as many up rows, loaded as 16-row slabs
  *            whose rows past the tile are not read, so a height of N / 256
  *            gives every CU one tile; the whole-tile body (ku 16) and the
- *            residual hand-off ops take 16 or 32, gate/up 16; SK_PATH_WIDE:
+ *            residual hand-off ops on this path take 16 or 32, gate/up 16;
+ *            SK_PATH_WIDE:
  *            1..96 rows, gate/up 1..48, with WN = 2 gate/up 1..32, with
- *            WN = 4 1..128 rows (eight waves 1..96), gate/up 17..64 (eight
- *            waves 17..48))
+ *            WN = 4 1..128 rows (eight waves 1..128), gate/up 17..64 (eight
+ *            waves 17..48); with WN = 4 the residual hand-off producer takes
+ *            a multiple of 16 rows and split >= 2, the consumers split 1)
  *   split  : global K splits; >1 writes fp32 partials to the workspace and
  *            the last workgroup to finish a tile sums them in fixed split
  *            order (no floating-point atomics, no second kernel)
