@@ -171,7 +171,9 @@ __device__ __forceinline__ float rows4_sum(float x) {
 template <int QR, int ATTN_WAVES, bool TREE, bool ROPE = false>
 __global__ void __launch_bounds__(64 * ATTN_WAVES) decode_attn_kernel(AttnArgs a) {
   __shared__ float s_m[ATTN_WAVES][QR], s_l[ATTN_WAVES][QR];
-  __shared__ __attribute__((aligned(16))) float s_acc[ATTN_WAVES][QR][HEAD_D];
+  // (rows padded by 8 floats: the lanes of one f32x4 store hold 16 different
+  // rows, and 128-float rows put all of them on the same banks)
+  __shared__ __attribute__((aligned(16))) float s_acc[ATTN_WAVES][QR][HEAD_D + 8];
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
