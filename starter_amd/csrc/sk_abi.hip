@@ -443,7 +443,9 @@ const Tuned kTuned[] = {
     {SK_OP_GATEUP, 9728, 2560, 32, {3, 10, 8, 16, 1, 0}},  // gate_up   21.56 us  4656 GB/s (one partial buffer)
     {SK_OP_GATEUP, 9728, 2560, 40, {3, 10, 8, 16, 1, 0}},  // gate_up   24.79 us  4058 GB/s (half ring)
     {SK_OP_GATEUP, 9728, 2560, 48, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   24.7 us  4080 GB/s (two row groups; 25.8 half ring)
-    {SK_OP_GATEUP, 9728, 2560, 64, {3, 10, 8, 16, 1, 128, 2}},  // gate_up   30.0 us  3373 GB/s (two row groups; 45.0 without)
+    // 49-64 rows: the two-operand wide path (25.7 us against 26.5 for two ring
+    // row groups in one run; 45.0 for one group)
+    {SK_OP_GATEUP, 9728, 2560, 64, {4, 8, 8, 40, 1, 0, 4}},
     // 65-128 rows: the two-operand wide path, 40 + 40-row tiles (244
     // workgroups of eight waves): 36.1 us at 128 rows, 34.7 at 96, against
     // 42.9 and 38.1 for four row groups (55.9 as two 64-row launches).

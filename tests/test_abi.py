@@ -230,13 +230,13 @@ def test_row_groups_planning():
         _tickets(4 * 608) + 4 * 2 * 2 * 16 * 9728 * 4
     assert _lib.workspace_bytes(SK_OP_LM_ARGMAX, 64, 151936, 2560, ring(groups=2, grid=640)) == _tickets(2) + 64 * 8
     assert _lib.workspace_bytes(SK_OP_GEMM, 64, 6144, 2560, ring(groups=2)) == 0
-    # the tuned verify-width entries use them (qkv, gate_up; down and lm_head
+    # the tuned verify-width entries use them (qkv; gate_up, down and lm_head
     # + argmax run on the two-operand wide path at 49-64 rows), and so do the
     # hand-off ops
-    for name in ("qkv", "gu"):
+    for name in ("qkv",):
         op, N, K = QWEN[name]
         assert _lib.default_config(op, 64, N, K).groups == 2, name
-    for name in ("d", "lm_argmax", "lm"):
+    for name in ("gu", "d", "lm_argmax", "lm"):
         op, N, K = QWEN[name]
         cfg = _lib.default_config(op, 64, N, K)
         assert cfg.path == _lib.SK_PATH_WIDE and cfg.groups == 4, name
