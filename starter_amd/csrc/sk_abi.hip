@@ -463,7 +463,9 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 2, {2, 2, 10, 2, 1, 0}},  // down      11.33 us  4398 GB/s
     {SK_OP_GEMM, 2560, 9728, 4, {3, 8, 40, 12, 1, 0}},  // down      12.16 us  4098 GB/s
     {SK_OP_GEMM, 2560, 9728, 8, {3, 8, 40, 12, 1, 0}},  // down      12.59 us  3962 GB/s
-    {SK_OP_GEMM, 2560, 9728, 16, {3, 13, 8, 32, 3, 240}},  // down      13.5 us  3717 GB/s (with partial rows padded; 14.0 with four-chunk waves)
+    // down at M = 9-16: 10-row tiles, one per CU, eight waves of five chunks
+    // each (13.4 us against 14.0 for 32-row tiles in three K splits)
+    {SK_OP_GEMM, 2560, 9728, 16, {3, 8, 40, 10, 1, 0}},  // down      13.4 us  3717 GB/s
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
     {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
@@ -480,6 +482,10 @@ const Tuned kTuned[] = {
     {SK_OP_RESID_GEMM, 2560, 4096, 8, {3, 16, 8, 16, 1, 0}},   // o_proj producer  7.46 us
     {SK_OP_RESID_GEMM, 2560, 4096, 16, {3, 4, 32, 16, 1, 0}},  // o_proj producer  7.91 us
     {SK_OP_RESID_GEMM, 2560, 9728, 8, {3, 8, 40, 16, 1, 0}},   // down producer   13.18 us (16.24 with three splits)
+    // down producer at M = 9-16 (the decode step): 32-row tiles in three K
+    // splits, 14.8 us (a producer tile holds whole 16-column groups, so the
+    // plain plan's 10-row tiles do not apply)
+    {SK_OP_RESID_GEMM, 2560, 9728, 16, {3, 13, 8, 32, 3, 240}},
     {SK_OP_RESID_GEMM, 2560, 9728, 64, {3, 10, 8, 16, 4, 128, 2}},  // down producer: its plain plan has no residual instance (64-row tiles)
     {SK_OP_LM_ARGMAX, 151936, 2560, 1, {3, 10, 8, 16, 1, 0}},  // lm_head  118.18 us  6583 GB/s
     {SK_OP_LM_ARGMAX, 151936, 2560, 2, {3, 10, 8, 32, 1, 0}},  // lm_head  117.50 us  6621 GB/s
