@@ -468,7 +468,7 @@ const Tuned kTuned[] = {
     {SK_OP_GEMM, 2560, 9728, 16, {3, 8, 40, 10, 1, 0}},  // down      13.4 us  3717 GB/s
     {SK_OP_GEMM, 2560, 9728, 32, {3, 4, 32, 32, 3, 0}},  // down      19.71 us  2568 GB/s
     {SK_OP_GEMM, 2560, 9728, 40, {3, 10, 8, 16, 4, 0}},  // down      19.62 us  2588 GB/s (half ring)
-    {SK_OP_GEMM, 2560, 9728, 48, {3, 10, 8, 16, 4, 0}},  // down      20.32 us  2509 GB/s (half ring)
+    {SK_OP_GEMM, 2560, 9728, 48, {4, 8, 8, 32, 3, 0, 4}},  // down      20.1 us (two-operand wide path; 20.6 half ring)
     // 49-64 rows: the two-operand wide path (20.2-20.6 us; the ring path
     // with five K splits 22.8-23.7)
     {SK_OP_GEMM, 2560, 9728, 64, {4, 8, 8, 32, 3, 0, 4}},  // down      20.58 us
