@@ -54,7 +54,7 @@ def _noalloc(a: torch.Tensor, w: torch.Tensor, cfg: SkConfig | None) -> torch.Te
     return out
 
 
-SPLIT3 = SkConfig.make(SK_PATH_MFMA_LDS, waves=13, ku=8, rows=32, split=3)   # the tuned down plan at M = 16
+SPLIT3 = SkConfig.make(SK_PATH_MFMA_LDS, waves=13, ku=8, rows=32, split=3)   # the down producer's plan at M = 16
 SPLIT4 = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, split=4)
 # two row groups, each with its own counters and partials in the scratch
 GROUPS_A = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, split=4, grid=128, groups=2)
@@ -62,13 +62,13 @@ GROUPS_B = SkConfig.make(SK_PATH_MFMA_LDS, waves=10, ku=8, rows=16, split=4, gri
 
 
 @pytest.mark.parametrize("first,second", [
-    ((16, None), (3, SPLIT3)),        # down projection, default (split-K) plan, then a smaller batch
-    ((64, None), (16, None)),         # the M = 64 default (split 5) then M = 16 (split 3, 32-row tiles)
+    ((16, SPLIT3), (3, SPLIT3)),      # down projection, three K splits, then a smaller batch
+    ((64, None), (48, None)),         # the M = 64 default (wide path, three K splits), then 48 rows on it
     ((8, SPLIT4), (5, SPLIT3)),       # explicit split counts: the second call uses fewer tiles
     ((64, GROUPS_A), (40, GROUPS_B)),  # row groups with split K, then fewer rows and workgroups
 ])
 def test_noalloc_equals_workspace_entry_point_on_two_calls(first, second):
-    N, K = 2560, 9728                 # down: every default plan above splits K, so the scratch is used
+    N, K = 2560, 9728                 # down: every plan above splits K, so the scratch is used
     outs = []
     for i, (M, cfg) in enumerate((first, second)):
         assert _lib.workspace_bytes(_lib.SK_OP_GEMM, M, N, K, cfg) > 0, "the case must use the scratch"
