@@ -357,7 +357,13 @@ __device__ __forceinline__ void wide2_body(Args p) {
       const int m = idx >> 2, q = idx & 3;
       uint32_t bo = 0u;
       int bn = 0;
-#pragma unroll
+      // Not unrolled: with all QC columns unrolled the compiler computed every
+      // column's bound check up front and held the masks in scalar registers
+      // across the step loop (122 of them spilled to vector lanes, which cost
+      // the MFMA loop its fragment registers: each fragment read then waited
+      // for the one before, lm_head + argmax at 128 rows 212 against 204 us
+      // for the logits GEMM of the same loop).
+#pragma unroll 1
       for (int v = 0; v < QC / 8; ++v) {
         const u32x4 x = *reinterpret_cast<const u32x4*>(T + m * TP + q * QC + 8 * v);
 #pragma unroll
