@@ -62,7 +62,9 @@ def _units() -> list[tuple[Path, list[str], Path]]:
 def _run(cmd: list[str]) -> list[tuple[str, int, int]]:
     """Run one hipcc command; returns (kernel, VGPR spill count, VGPRs + AGPRs
     allocated) of every kernel whose resource-usage remark reports spilled
-    registers."""
+    registers.  A kernel that keeps private (scratch) memory without spilling,
+    i.e. a local array the compiler did not promote to registers, fails the
+    command: every kernel of this library keeps its arrays in registers."""
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -70,12 +72,15 @@ def _run(cmd: list[str]) -> list[tuple[str, int, int]]:
     # resource-usage remarks are parsed, not printed; anything else is surfaced.
     noise = ("packed-fp32-ops", "warning: feature flag", "1 warning generated", "warnings generated",
              "In file included from")
-    spills, name, regs = [], None, 0
+    spills, scratch, name, regs = [], [], None, 0
     for line in (r.stderr or "").splitlines():
         if "kernel-resource-usage" in line:
             field = lambda key: int(line.split(key)[1].split("[")[0])  # noqa: E731
             if "Function Name:" in line:
                 name, regs = line.split("Function Name:")[1].split("[")[0].strip(), 0
+            elif "ScratchSize [bytes/lane]:" in line:
+                if field("ScratchSize [bytes/lane]:"):
+                    scratch.append((name, field("ScratchSize [bytes/lane]:")))
             elif "VGPRs Spill:" in line:
                 if field("VGPRs Spill:"):
                     spills.append((name, field("VGPRs Spill:"), regs))
@@ -86,6 +91,11 @@ def _run(cmd: list[str]) -> list[tuple[str, int, int]]:
             continue
         if line.strip() and not any(n in line for n in noise):
             print(line, file=sys.stderr)
+    spilled = {n for n, _, _ in spills}
+    stack = [(n, b) for n, b in scratch if n not in spilled]
+    if stack:
+        raise RuntimeError("kernels keep private memory (a local array not promoted to registers):\n  " +
+                           "\n  ".join(f"{n} ({b} bytes per lane)" for n, b in stack))
     return spills
 
 

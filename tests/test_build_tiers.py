@@ -110,3 +110,30 @@ def test_mfma_64_rows_10_units_limited_to_its_tier(waves):
     split = 2 if waves == 4 else 1
     st = _lib.check_config(SK_OP_GEMM, 64, 6144, 2560, SkConfig.make(SK_PATH_MFMA, waves, 10, 16, split))
     assert (st == SK_OK) == (waves == 4)
+
+
+def _remarks(*kernels):
+    """hipcc-style resource-usage remarks: (name, scratch bytes, VGPR spills)."""
+    out = []
+    for name, scratch, spill in kernels:
+        tag = " [-Rpass-analysis=kernel-resource-usage]"
+        out += [f"x.hip:1:1: remark: Function Name: {name}{tag}", f"x.hip:1:1: remark:     VGPRs: 128{tag}",
+                f"x.hip:1:1: remark:     AGPRs: 0{tag}", f"x.hip:1:1: remark:     ScratchSize [bytes/lane]: {scratch}{tag}",
+                f"x.hip:1:1: remark:     VGPRs Spill: {spill}{tag}"]
+    return "\n".join(out)
+
+
+def _fake_hipcc(text):
+    import sys
+    return [sys.executable, "-c", f"import sys; sys.stderr.write({text!r})"]
+
+
+def test_remarks_report_spills_and_reject_private_arrays():
+    """Spilling kernels are returned for the tier loop; a kernel that keeps a
+    local array in scratch without spilling fails the compile step."""
+    ok = _remarks(("_ZN2sk10mfmt_entryILi1ELi2ELi256ELi1EEEvNS_4ArgsE", 0, 0),
+                  ("_ZN2sk11wide2_entryILi8ELi8ELi2EEEvNS_4ArgsE", 16, 3))
+    assert B._run(_fake_hipcc(ok)) == [("_ZN2sk11wide2_entryILi8ELi8ELi2EEEvNS_4ArgsE", 3, 128)]
+    stack = _remarks(("_ZN2sk11wide2_entryILi8ELi6ELi1EEEvNS_4ArgsE", 208, 0))
+    with pytest.raises(RuntimeError, match="private memory"):
+        B._run(_fake_hipcc(stack))
